@@ -1,0 +1,199 @@
+"""Decode throughput of the 2B-shaped Qwen3.5 hybrid model at 8k context on one MI355X, with
+the HBM roofline of the token-mixer kernels and the reference CPU path timed beside it.
+
+A step is one greedy decode token through all 24 layers (18 Gated-DeltaNet + 6 gated
+attention over an 8192-position fp32 KV cache), the tied lm_head and the device argmax.
+Weights are a random-init bf16 checkpoint (N(0, 0.02), seed 0) written by the library's
+synthetic writer; the KV cache is N(0,1) and the GDN states N(0, 0.1) (synthetic prefilled
+cache). Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen3.5-cpu-cpp_amd"))
+
+METRIC = "decode tok/s + mixer HBM GB/s (%peak), 2B-shaped @8k ctx, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+GDN_LAYER_BYTES = 2_384_640  # per token per GDN layer (state r/w, conv window r/w, conv w, inputs, output)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def ensure_model(path: str, dims, pyq35) -> None:
+    st = os.path.join(path, "model.safetensors")
+    if os.path.exists(st) and os.path.exists(os.path.join(path, "config.json")):
+        return
+    t = time.time()
+    pyq35.synth_write_model(path, dims, seed=0, std=0.02, threads=0)
+    log(f"wrote synthetic checkpoint {path} in {time.time() - t:.1f} s")
+
+
+def weight_bytes_per_step(d) -> int:
+    H, I, V = d.hidden_size, d.ffn_intermediate, d.vocab_size
+    KD, VD, VH = d.gdn_k_heads * 128, d.gdn_v_heads * 128, d.gdn_v_heads
+    NQ, NKV, HD = d.attn_q_heads, d.attn_kv_heads, d.attn_head_dim
+    gdn = ((2 * KD + VD) + VD + 2 * VH) * H + H * VD
+    attn = (2 * NQ * HD + 2 * NKV * HD) * H + H * NQ * HD
+    ffn = 3 * H * I
+    return 2 * (d.n_layers_gdn * gdn + d.n_layers_attn * attn + d.n_layers_total * ffn + V * H)
+
+
+def cpu_baseline(model_dir: str, dims, ctx: int, n_steps: int) -> dict:
+    """The reference engine (oracle/_ref) when it was built, else the oracle port, on the
+    same checkpoint with a synthetic cache of ctx positions; times n_steps decode steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_py as op
+    import pyq35
+
+    d = dims
+    conv = 2 * d.gdn_k_heads * 128 + d.gdn_v_heads * 128
+    kind = "reference" if op.ref_available() else "port"
+    max_ctx = ctx + n_steps + 2
+    t_load = time.time()
+    if kind == "reference":
+        eng = op.Ref(model_dir, max_ctx)
+        lib = op.Ref.lib()
+        kc = lambda i: op.view(lib.ref_kcache(eng.h, i), (max_ctx, d.attn_kv_heads, 256))  # noqa: E731
+        vc = lambda i: op.view(lib.ref_vcache(eng.h, i), (max_ctx, d.attn_kv_heads, 256))  # noqa: E731
+        st = lambda i: op.view(lib.ref_gdn_state(eng.h, i), (d.gdn_v_heads, 128, 128))  # noqa: E731
+        setpos = lambda p: lib.ref_set_position(eng.h, p)  # noqa: E731
+        step = eng.step
+    else:
+        eng = op.Oracle(model_dir, max_ctx)
+        kc, vc, st, setpos, step = eng.kcache, eng.vcache, eng.gdn_state, eng.set_position, eng.step
+    n = ctx * d.attn_kv_heads * 256
+    for i in range(d.n_layers_attn):
+        kc(i)[:ctx] = pyq35.synth_normal(n, 0, 1000 + i).reshape(ctx, d.attn_kv_heads, 256)
+        vc(i)[:ctx] = pyq35.synth_normal(n, 0, 2000 + i).reshape(ctx, d.attn_kv_heads, 256)
+    for i in range(d.n_layers_gdn):
+        st(i)[:] = pyq35.synth_normal(d.gdn_v_heads * 128 * 128, 0, 3000 + i, 0.1).reshape(d.gdn_v_heads, 128, 128)
+    setpos(ctx)
+    log(f"cpu baseline ({kind}) loaded in {time.time() - t_load:.1f} s; timing {n_steps} steps")
+    tok = 1
+    step(tok)  # untimed warm-up step
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        lg = step(tok)
+        tok = int(np.argmax(lg))
+    dt = time.perf_counter() - t0
+    threads = op.threads()
+    return {"value": n_steps / dt, "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{n_steps} greedy decode steps of the same 2B-shaped checkpoint at positions "
+                      f"{ctx + 1}..{ctx + n_steps} (synthetic cache), {dt:.1f} s, OpenMP threads={threads}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--model-dir", default="/tmp/q35_synth_2b_seed0")
+    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+              "(the multi-GPU sharding of the path is a design note, not built)", file=sys.stderr)
+        sys.exit(2)
+
+    import pyq35
+
+    d = pyq35.dims_for("2b")
+    ensure_model(a.model_dir, d, pyq35)
+    max_ctx = a.ctx + a.warmup + 2 * a.steps + 4
+    t = time.time()
+    m = pyq35.Model(a.model_dir, max_ctx)
+    log(f"model uploaded in {time.time() - t:.1f} s; budget {m.budget()}")
+    m.fill_synthetic(a.ctx, seed=0, state_std=0.1)
+    hip = pyq35.Hip()
+
+    # warm-up (builds and replays the step graph)
+    tok = 1
+    ids = m.decode_greedy(tok, a.warmup)
+    tok = int(ids[-1])
+    # timed: K greedy steps back to back on the device (graph replays), bracketed by syncs
+    stream = pyq35.lib.q35_model_stream(m.h)
+    e0, e1 = hip.event(), hip.event()
+    pyq35.check(pyq35.lib.q35_model_synchronize(m.h))
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    ids = m.decode_greedy(tok, a.steps)
+    hip.record(e1, stream)
+    pyq35.check(pyq35.lib.q35_model_synchronize(m.h))
+    wall = time.perf_counter() - t0
+    dev_ms = hip.elapsed_ms(e0, e1)
+    ms_per_step = 1e3 * wall / a.steps
+    tok = int(ids[-1])
+    log(f"{a.steps} steps: wall {wall * 1e3:.2f} ms, device {dev_ms:.2f} ms")
+
+    # kernel-timed pass: the same steps launched eagerly with events around every launch
+    p_first = m.position
+    m.set_kernel_timing(True)
+    m.decode_greedy(tok, a.steps)
+    kt = m.kernel_times()
+    m.set_kernel_timing(False)
+    mean_n = p_first + (a.steps + 1) / 2.0  # mean attended positions (pos + 1) over the pass
+    NKV, HD, NQ = d.attn_kv_heads, d.attn_head_dim, d.attn_q_heads
+    attn_ms, attn_n = kt["attn_decode"]
+    attn_avg_s = attn_ms / 1e3 / attn_n
+    attn_bytes = 2 * NKV * HD * 4 * mean_n + NQ * HD * 4  # K and V rows + the queries
+    attn_gbs = attn_bytes / attn_avg_s / 1e9
+    mixer_ms = sum(kt[k][0] for k in ("attn_prep", "attn_decode", "attn_combine"))
+    mixer_bytes = 4096 * mean_n + 59_392  # per layer incl. projection outputs, append, output
+    mixer_gbs = mixer_bytes * attn_n / (mixer_ms / 1e3) / 1e9
+    gdn_ms, gdn_n = kt["gdn_decode"]
+    gdn_gbs = GDN_LAYER_BYTES * gdn_n / (gdn_ms / 1e3) / 1e9
+    gemv_ms, gemv_n = kt["gemv"]
+    wb = weight_bytes_per_step(d)
+    gemv_gbs = wb * a.steps / (gemv_ms / 1e3) / 1e9
+    kernels = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in kt.items()}
+
+    result = {
+        "metric": METRIC,
+        "value": a.steps / wall,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: random-init bf16 weights N(0,0.02) seed 0, KV cache N(0,1), GDN state N(0,0.1)",
+        "config": {"workload": f"2B-shaped Qwen3.5 greedy decode at {a.ctx} context",
+                   "hidden": d.hidden_size, "layers": "24 = 18 GDN + 6 gated attention",
+                   "gdn_heads": d.gdn_v_heads, "attn_heads": f"{NQ}q/{NKV}kv x {HD}",
+                   "ffn": d.ffn_intermediate, "vocab": d.vocab_size, "context": a.ctx,
+                   "batch": 1},
+        "roofline": {"bound": "hbm", "kernel": "attention decode split-K partial (per layer)",
+                     "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": attn_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": attn_bytes, "avg_launch_us": attn_avg_s * 1e6},
+        "mixers": {
+            "attention_mixer_GBs": mixer_gbs, "attention_mixer_frac": mixer_gbs / HBM_PEAK_GBS,
+            "gdn_decode_GBs": gdn_gbs, "gdn_decode_frac": gdn_gbs / HBM_PEAK_GBS,
+            "gemv_GBs": gemv_gbs, "gemv_frac": gemv_gbs / HBM_PEAK_GBS,
+        },
+        "kernels": kernels,
+        "device_ms_per_step": dev_ms / a.steps,
+    }
+    m.close()
+    if not a.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(a.model_dir, d, a.ctx, a.cpu_steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,164 @@
+// Kernel-level C ABI on caller-owned device pointers: the forward_pass.h primitives
+// (include/forward_pass.h:21-54) and the two decode mixers. Shapes are validated here so
+// that no kernel is launched with an extent it does not support.
+#include <hip/hip_runtime.h>
+
+#include "../host/q35_internal.h"
+#include "launch.hpp"
+
+namespace {
+
+q35_status launched(hipError_t e, const char* what) {
+    return e == hipSuccess ? Q35_OK : q35::fail(Q35_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t as_stream(q35_stream s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+q35_status q35_matmul_bf16(const uint16_t* W, const float* x, float* y, int32_t out_dim,
+                           int32_t in_dim, q35_stream s) {
+    if (!W || !x || !y || out_dim <= 0 || in_dim <= 0)
+        return q35::fail(Q35_ERR_ARG, "q35_matmul_bf16: bad argument");
+    if (in_dim % 8 != 0 || in_dim > q35k::kGemvMaxIn)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_matmul_bf16: in_dim %d (needs %%8 == 0, <= %d)", in_dim,
+                         q35k::kGemvMaxIn);
+    if ((reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
+        return q35::fail(Q35_ERR_ARG, "q35_matmul_bf16: W and x must be 16-byte aligned");
+    q35k::GemvArgs a{};
+    a.W = W;
+    a.x = x;
+    a.y = y;
+    a.rows = out_dim;
+    a.in_dim = in_dim;
+    return launched(q35k::launch_gemv(a, q35k::kProPlain, as_stream(s)), "q35_matmul_bf16");
+}
+
+q35_status q35_rmsnorm(const float* x, const float* w, float* y, int32_t rows, int32_t n, float eps,
+                       q35_stream s) {
+    if (!x || !w || !y || rows <= 0 || n <= 0) return q35::fail(Q35_ERR_ARG, "q35_rmsnorm: bad argument");
+    return launched(q35k::launch_rmsnorm_rows(x, w, y, rows, n, eps, 0, nullptr, as_stream(s)), "q35_rmsnorm");
+}
+
+q35_status q35_rmsnorm_gated(const float* x, const float* w, const float* gate, float* y, int32_t rows,
+                             int32_t n, float eps, q35_stream s) {
+    if (!x || !w || !gate || !y || rows <= 0 || n <= 0)
+        return q35::fail(Q35_ERR_ARG, "q35_rmsnorm_gated: bad argument");
+    return launched(q35k::launch_rmsnorm_rows(x, w, y, rows, n, eps, 1, gate, as_stream(s)), "q35_rmsnorm_gated");
+}
+
+q35_status q35_l2norm(float* x, int32_t rows, int32_t n, float eps, q35_stream s) {
+    if (!x || rows <= 0 || n <= 0) return q35::fail(Q35_ERR_ARG, "q35_l2norm: bad argument");
+    return launched(q35k::launch_l2norm_rows(x, rows, n, eps, as_stream(s)), "q35_l2norm");
+}
+
+q35_status q35_apply_rope(float* x, int32_t rows, int32_t head_dim, int32_t rotary_dim, const int32_t* pos,
+                          int32_t pos0, double theta, q35_stream s) {
+    if (!x || rows <= 0 || head_dim <= 0 || rotary_dim < 0 || rotary_dim > head_dim || (rotary_dim & 1))
+        return q35::fail(Q35_ERR_ARG, "q35_apply_rope: bad argument");
+    return launched(q35k::launch_rope_rows(x, rows, head_dim, rotary_dim, pos, pos0, theta, as_stream(s)),
+                    "q35_apply_rope");
+}
+
+q35_status q35_gdn_decode(const q35_gdn_decode_args* args, q35_stream s) {
+    if (!args) return q35::fail(Q35_ERR_ARG, "q35_gdn_decode: null args");
+    const q35_gdn_decode_args& g = *args;
+    if (g.head_dim_k != 128 || g.head_dim_v != 128 || g.conv_kernel != 4)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_gdn_decode: needs DK == DV == 128 and conv kernel 4");
+    if (g.n_layers <= 0 || g.k_heads <= 0 || g.v_heads <= 0 || g.v_heads % g.k_heads != 0 || g.pos < 0)
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_decode: bad head counts or position");
+    if (!g.qkv || !g.b || !g.a || !g.conv_w || !g.A_log || !g.dt_bias || !g.conv_ring || !g.state || !g.out)
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_decode: null pointer");
+    if (g.norm_w && !g.z) return q35::fail(Q35_ERR_ARG, "q35_gdn_decode: the gated norm needs z");
+    q35k::GdnDecodeArgs a{};
+    a.n_layers = g.n_layers;
+    a.KH = g.k_heads;
+    a.VH = g.v_heads;
+    a.KER = 4;
+    a.pos_val = g.pos;
+    a.eps = g.eps;
+    a.qkv = g.qkv;
+    a.z = g.z;
+    a.b = g.b;
+    a.a = g.a;
+    a.conv_w = g.conv_w;
+    a.A_log = g.A_log;
+    a.dt_bias = g.dt_bias;
+    a.norm_w = g.norm_w;
+    a.conv_ring = g.conv_ring;
+    a.state = g.state;
+    a.out = g.out;
+    return launched(q35k::launch_gdn_decode(a, g.norm_w != nullptr, as_stream(s)), "q35_gdn_decode");
+}
+
+uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args* args) {
+    if (!args || args->kv_heads <= 0 || args->q_heads <= 0) return 0;
+    int splits = args->n_splits;
+    if (splits <= 0) {
+        const int64_t want = (args->max_context + q35k::kAttnChunk - 1) / q35k::kAttnChunk;
+        splits = static_cast<int>(want < 1 ? 1 : want > 1024 ? 1024 : want);
+    }
+    const uint64_t qw = (static_cast<uint64_t>(args->q_heads) * args->head_dim * 4 + 255) & ~255ULL;
+    return qw + static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
+}
+
+q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
+    if (!args) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: null args");
+    const q35_attn_decode_args& g = *args;
+    if (g.head_dim != 256) return q35::fail(Q35_ERR_UNSUPPORTED, "q35_attn_decode: head_dim must be 256");
+    if (g.kv_heads <= 0 || g.q_heads % g.kv_heads != 0)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: bad head counts");
+    const int grp = g.q_heads / g.kv_heads;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_attn_decode: GQA group %d", grp);
+    if (g.rotary_dim < 0 || g.rotary_dim > 256 || (g.rotary_dim & 1))
+        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: rotary_dim %d", g.rotary_dim);
+    if (g.pos < 0 || g.pos >= g.max_context)
+        return q35::fail(Q35_ERR_RANGE, "q35_attn_decode: position %d outside [0, %lld)", g.pos,
+                         static_cast<long long>(g.max_context));
+    if (!g.qg || !g.k_new || !g.v_new || !g.q_norm || !g.k_norm || !g.k_cache || !g.v_cache || !g.out ||
+        !g.workspace)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: null pointer");
+    if (g.n_splits < 0 || g.n_splits > 4096) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: n_splits %d", g.n_splits);
+    if (g.workspace_bytes < q35_attn_decode_workspace_bytes(args))
+        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: workspace of %llu bytes, needs %llu",
+                         static_cast<unsigned long long>(g.workspace_bytes),
+                         static_cast<unsigned long long>(q35_attn_decode_workspace_bytes(args)));
+    int splits = g.n_splits;
+    if (splits <= 0) {
+        const int64_t want = (g.max_context + q35k::kAttnChunk - 1) / q35k::kAttnChunk;
+        splits = static_cast<int>(want < 1 ? 1 : want > 1024 ? 1024 : want);
+    }
+    q35k::AttnDecodeArgs a{};
+    a.NQ = g.q_heads;
+    a.NKV = g.kv_heads;
+    a.HD = 256;
+    a.ROT = g.rotary_dim;
+    a.pos_val = g.pos;
+    a.max_ctx = g.max_context;
+    a.n_splits = splits;
+    a.theta = g.rope_theta;
+    a.eps = g.eps;
+    a.qg = g.qg;
+    a.k_new = g.k_new;
+    a.v_new = g.v_new;
+    a.q_norm = g.q_norm;
+    a.k_norm = g.k_norm;
+    a.k_cache = g.k_cache;
+    a.v_cache = g.v_cache;
+    a.out = g.out;
+    const uint64_t qw = (static_cast<uint64_t>(g.q_heads) * 256 * 4 + 255) & ~255ULL;
+    a.q_work = static_cast<float*>(g.workspace);
+    a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(g.workspace) + qw);
+    a.part_ml = a.part_o + static_cast<int64_t>(g.kv_heads) * splits * grp * 256;
+    hipStream_t st = as_stream(s);
+    q35_status r = launched(q35k::launch_attn_prep(a, st), "attn prep");
+    if (r != Q35_OK) return r;
+    r = launched(q35k::launch_attn_partial(a, st), "attn partial");
+    if (r != Q35_OK) return r;
+    return launched(q35k::launch_attn_combine(a, st), "attn combine");
+}
+
+}  // extern "C"

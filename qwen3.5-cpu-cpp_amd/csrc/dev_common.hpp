@@ -1,0 +1,69 @@
+#pragma once
+// Device helpers shared by the gfx950 kernels: 64-lane wavefront reductions, bf16
+// widening, the scalar activations of the reference (include/forward_pass.h:21-24).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace q35k {
+
+constexpr int kWave = 64;
+
+// bf16 pair packed in one 32-bit word: element 0 in the low half.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// silu(x) = x / (1 + e^-x), sigmoid, softplus with the > 20 pass-through.
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+// Sum of a double over the whole block (blockDim.x a multiple of 64, <= 1024).
+// `red` needs blockDim.x / 64 doubles of LDS. Every thread gets the total.
+__device__ __forceinline__ double block_sum(double v, double* red) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+// Counter-based normal draw (splitmix64 finaliser + Box-Muller in double); the same
+// formula as the host generator of synthetic checkpoints.
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ULL;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+    return x ^ (x >> 31);
+}
+__device__ __forceinline__ double normal_at(uint64_t key, uint64_t i) {
+    const uint64_t a = mix64(key + 2 * i), b = mix64(key + 2 * i + 1);
+    const double u1 = (static_cast<double>(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    const double u2 = static_cast<double>(b >> 11) * (1.0 / 9007199254740992.0);
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+}  // namespace q35k

@@ -1,0 +1,190 @@
+// Gated-DeltaNet decode: one token through the conv window, q/k l2-normalisation, the
+// decay + delta-rule update of the 128 x 128 fp32 state and the readout, for one or more
+// layers in one launch (QwenModel::gdn_step after its projections,
+// src/qwen_model.cpp:173-207).
+//
+// Work split: one 256-thread workgroup per (layer, v-head, column slice of CS state
+// columns). The delta rule is column-separable -- for a state column vv,
+//     S[:,vv] <- a S[:,vv];  d = (v[vv] - S[:,vv].k) b;  S[:,vv] += k d;  o[vv] = S[:,vv].q
+// -- so a slice needs only k, q (shared by the head) and its own v entries. Each thread
+// holds RPT = 128*CS/256 state values of one column in registers; the state is read from
+// HBM once and written once, with CS consecutive floats per row (128 B for CS = 32).
+// The two column dot products are reduced over the 256/CS row groups through LDS.
+//
+// Conv window: a ring of KER = 4 slots per channel in the state arena, the input of
+// position t in slot t % 4. Step t reads slots (t-3..t-1) % 4 and writes slot t % 4, so
+// the workgroups that share the q/k channels of a k-head can all read the window while
+// one of them (v-head % rep == 0, slice 0) stores the new input, without a race.
+//
+// With CS = 128 (one workgroup per head) the gated rmsnorm of the readout
+// (src/forward_pass.cpp:86-93) is fused too; with CS = 32 the raw readout is written and
+// the norm runs in the prologue of the out_proj matvec.
+#include "dev_common.hpp"
+#include "launch.hpp"
+
+namespace q35k {
+namespace {
+
+constexpr int kD = 128;  // DK == DV
+
+template <int CS, bool FUSE_NORM>
+__global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
+    constexpr int NSPLIT = kD / CS;
+    constexpr int NRG = 256 / CS;
+    constexpr int RPT = kD / NRG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int vh = blockIdx.x / NSPLIT, split = blockIdx.x - vh * NSPLIT;
+    const int layer = blockIdx.y;
+    const int rep = a.VH / a.KH, kh = vh / rep;
+    const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
+
+    const float* qkv = a.qkv + layer * a.ls_qkv;
+    const float* zin = a.z ? a.z + layer * a.ls_z : nullptr;
+    const float* bin = a.b + layer * a.ls_ba;
+    const float* ain = a.a + layer * a.ls_ba;
+    const float* convw = a.conv_w + layer * a.ls_convw;
+    const float* A_log = a.A_log + layer * a.ls_vh;
+    const float* dt_bias = a.dt_bias + layer * a.ls_vh;
+    float* ring = a.conv_ring + layer * a.ls_ring;
+    float* S = a.state + layer * a.ls_state + static_cast<int64_t>(vh) * kD * kD;
+    float* out = a.out + layer * a.ls_out;
+
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_val;
+    const int s_new = pos & 3, s_m1 = (pos + 3) & 3, s_m2 = (pos + 2) & 3, s_m3 = (pos + 1) & 3;
+
+    __shared__ float q_s[kD], k_s[kD], v_s[CS], d_s[CS];
+    __shared__ float part[NRG][CS];
+    __shared__ double red[4];
+
+    // causal conv (taps oldest first) + SiLU for the 128 q and 128 k channels of head kh
+    {
+        const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
+        const float* w4 = convw + static_cast<int64_t>(ch) * 4;
+        const float xn = qkv[ch];
+        float acc = 0.0f;
+        acc += w4[0] * ring[static_cast<int64_t>(s_m3) * CONV + ch];
+        acc += w4[1] * ring[static_cast<int64_t>(s_m2) * CONV + ch];
+        acc += w4[2] * ring[static_cast<int64_t>(s_m1) * CONV + ch];
+        acc += w4[3] * xn;
+        const float y = silu_f(acc);
+        if (tid < kD) q_s[tid] = y;
+        else k_s[tid - kD] = y;
+        if (vh % rep == 0 && split == 0) ring[static_cast<int64_t>(s_new) * CONV + ch] = xn;
+    }
+    // ... and for this slice's v channels
+    if (tid < CS) {
+        const int ch = 2 * KD + vh * kD + split * CS + tid;
+        const float* w4 = convw + static_cast<int64_t>(ch) * 4;
+        const float xn = qkv[ch];
+        float acc = 0.0f;
+        acc += w4[0] * ring[static_cast<int64_t>(s_m3) * CONV + ch];
+        acc += w4[1] * ring[static_cast<int64_t>(s_m2) * CONV + ch];
+        acc += w4[2] * ring[static_cast<int64_t>(s_m1) * CONV + ch];
+        acc += w4[3] * xn;
+        v_s[tid] = silu_f(acc);
+        ring[static_cast<int64_t>(s_new) * CONV + ch] = xn;
+    }
+    __syncthreads();
+
+    // l2norm (eps 1e-6, sum of squares in double); q also scaled by DK^-1/2
+    {
+        const float v = tid < kD ? q_s[tid] : k_s[tid - kD];
+        double ss = static_cast<double>(v) * v;
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const double sq = red[0] + red[1], sk = red[2] + red[3];
+        if (tid < kD) {
+            const float inv = 1.0f / sqrtf(static_cast<float>(sq) + 1e-6f);
+            q_s[tid] = (v * inv) * (1.0f / sqrtf(static_cast<float>(kD)));
+        } else {
+            const float inv = 1.0f / sqrtf(static_cast<float>(sk) + 1e-6f);
+            k_s[tid - kD] = v * inv;
+        }
+    }
+    const float g = -expf(A_log[vh]) * softplus_f(ain[vh] + dt_bias[vh]);
+    const float alpha = expf(g), beta = sigmoid_f(bin[vh]);
+    __syncthreads();
+
+    // decay, S^T k, delta, rank-1 update, S^T q on the register-resident slice
+    const int c = tid % CS, rg = tid / CS, r0 = rg * RPT;
+    float* Sc = S + split * CS + c;
+    float s[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) s[i] = Sc[(r0 + i) * kD];
+    float km = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        s[i] *= alpha;
+        km += s[i] * k_s[r0 + i];
+    }
+    part[rg][c] = km;
+    __syncthreads();
+    if (tid < CS) {
+        float t = 0.0f;
+#pragma unroll
+        for (int r = 0; r < NRG; ++r) t += part[r][tid];
+        d_s[tid] = (v_s[tid] - t) * beta;
+    }
+    __syncthreads();
+    const float dv = d_s[c];
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        s[i] += k_s[r0 + i] * dv;
+        o += s[i] * q_s[r0 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) Sc[(r0 + i) * kD] = s[i];
+    part[rg][c] = o;
+    __syncthreads();
+
+    float ov = 0.0f;
+    if (tid < CS) {
+#pragma unroll
+        for (int r = 0; r < NRG; ++r) ov += part[r][tid];
+    }
+    if constexpr (FUSE_NORM) {
+        // CS == 128: threads 0..127 hold the head's readout
+        double ss = tid < kD ? static_cast<double>(ov) * ov : 0.0;
+        ss = wave_sum(ss);
+        __syncthreads();
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const double tot = red[0] + red[1];
+        if (tid < kD) {
+            const float inv = 1.0f / sqrtf(static_cast<float>(tot / kD) + a.eps);
+            const float zz = zin[vh * kD + tid];
+            out[vh * kD + tid] = a.norm_w[layer * a.ls_normw + tid] * (ov * inv) * silu_f(zz);
+        }
+    } else {
+        if (tid < CS) out[vh * kD + split * CS + tid] = ov;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gdn_decode(const GdnDecodeArgs& in, bool fuse_norm, hipStream_t s) {
+    GdnDecodeArgs a = in;
+    const int64_t KD = static_cast<int64_t>(a.KH) * kD, VD = static_cast<int64_t>(a.VH) * kD;
+    const int64_t CONV = 2 * KD + VD;
+    if (!a.ls_qkv) a.ls_qkv = CONV;
+    if (!a.ls_z) a.ls_z = VD;
+    if (!a.ls_ba) a.ls_ba = a.VH;
+    if (!a.ls_convw) a.ls_convw = CONV * 4;
+    if (!a.ls_vh) a.ls_vh = a.VH;
+    if (!a.ls_normw) a.ls_normw = kD;
+    if (!a.ls_ring) a.ls_ring = CONV * 4;
+    if (!a.ls_state) a.ls_state = static_cast<int64_t>(a.VH) * kD * kD;
+    if (!a.ls_out) a.ls_out = VD;
+    if (fuse_norm) {
+        dim3 grid(a.VH, a.n_layers);
+        gdn_decode_kernel<128, true><<<grid, 256, 0, s>>>(a);
+    } else {
+        dim3 grid(a.VH * (kD / 32), a.n_layers);
+        gdn_decode_kernel<32, false><<<grid, 256, 0, s>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace q35k

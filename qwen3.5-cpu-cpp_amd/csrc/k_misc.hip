@@ -1,0 +1,224 @@
+// Small kernels of the decode step and of the primitive entry points: row-wise norms and
+// RoPE (src/forward_pass.cpp:77-112), embedding gather
+// (SafeTensors::get_row_f32, src/safetensors_loader.cpp:280-298), greedy argmax
+// (src/qwen_model.cpp:249-250: first index of the maximum), counters and fills.
+#include <math.h>
+
+#include <climits>
+
+#include "dev_common.hpp"
+#include "launch.hpp"
+
+namespace q35k {
+namespace {
+
+// One block per row: y = x * rsqrt(mean(x^2) + eps) * (1 + w), or for the gated form
+// y = w * (x * rsqrt(mean(x^2) + eps)) * silu(gate).
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const float* w,
+                                                           float* y, int n, float eps,
+                                                           int gated, const float* gate) {
+    __shared__ double red[4];
+    const int64_t off = static_cast<int64_t>(blockIdx.x) * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const double v = x[off + i];
+        ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = x[off + i];
+        y[off + i] = gated ? w[i] * (v * inv) * silu_f(gate[off + i]) : v * inv * (1.0f + w[i]);
+    }
+}
+
+// x *= 1 / sqrt(sum(x^2) + eps), in place, one block per row.
+__global__ __launch_bounds__(256) void l2norm_rows_kernel(float* x, int n, float eps) {
+    __shared__ double red[4];
+    const int64_t off = static_cast<int64_t>(blockIdx.x) * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const double v = x[off + i];
+        ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss) + eps);
+    for (int i = threadIdx.x; i < n; i += 256) x[off + i] *= inv;
+}
+
+// Rotate-half on dims [0, rot) of each row; angle pos * theta^(-2i/rot) in double.
+__global__ __launch_bounds__(64) void rope_rows_kernel(float* x, int hd, int rot, const int* pos,
+                                                       int pos0, double theta) {
+    const int half = rot / 2;
+    const int p = pos ? pos[blockIdx.x] : pos0;
+    float* v = x + static_cast<int64_t>(blockIdx.x) * hd;
+    for (int i = threadIdx.x; i < half; i += 64) {
+        const double inv_freq = pow(theta, -static_cast<double>(2 * i) / rot);
+        const double ang = static_cast<double>(p) * inv_freq;
+        const float c = static_cast<float>(cos(ang)), s = static_cast<float>(sin(ang));
+        const float x1 = v[i], x2 = v[i + half];
+        v[i] = x1 * c - x2 * s;
+        v[i + half] = x2 * c + x1 * s;
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* embed, const int* token,
+                                                    float* hidden, int H) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < H) hidden[i] = bf16_to_f32(embed[static_cast<int64_t>(*token) * H + i]);
+}
+
+// (value, index) order for the argmax: larger value first, then smaller index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void block_best(float& bv, int& bi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int w = 1; w < 4; ++w)
+        if (better(sv[w], si[w], bv, bi)) {
+            bv = sv[w];
+            bi = si[w];
+        }
+}
+
+__global__ __launch_bounds__(256) void argmax_pass1(const float* logits, int n, float* pv, int* pi) {
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += 256 * kArgmaxBlocks) {
+        const float v = logits[i];
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    block_best(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_pass2(const float* pv, const int* pi, int* token_out,
+                                                    int* ids, int* pos) {
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int b = threadIdx.x; b < kArgmaxBlocks; b += 256)
+        if (better(pv[b], pi[b], bv, bi)) {
+            bv = pv[b];
+            bi = pi[b];
+        }
+    block_best(bv, bi);
+    if (threadIdx.x == 0) {
+        const int am = bi == INT_MAX ? 0 : bi;
+        *token_out = am;
+        if (pos) {
+            if (ids) ids[*pos] = am;
+            *pos += 1;
+        }
+    }
+}
+
+__global__ void add_int_kernel(int* p, int v) { *p += v; }
+__global__ void set_int_kernel(int* p, int v) { *p = v; }
+
+__global__ __launch_bounds__(256) void copy_kernel(float* dst, const float* src, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(float* dst, int64_t n, float v) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        dst[i] = v;
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(float* dst, int64_t n, uint64_t key, float std) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        dst[i] = static_cast<float>(std * normal_at(key, static_cast<uint64_t>(i)));
+}
+
+int grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return static_cast<int>(b < 4096 ? (b > 0 ? b : 1) : 4096);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
+                               float eps, int gated, const float* gate, hipStream_t s) {
+    rmsnorm_rows_kernel<<<rows, 256, 0, s>>>(x, w, y, n, eps, gated, gate);
+    return hipGetLastError();
+}
+
+hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s) {
+    l2norm_rows_kernel<<<rows, 256, 0, s>>>(x, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
+                            double theta, hipStream_t s) {
+    rope_rows_kernel<<<rows, 64, 0, s>>>(x, hd, rot, pos, pos0, theta);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* hidden, int H,
+                        hipStream_t s) {
+    embed_kernel<<<(H + 255) / 256, 256, 0, s>>>(embed, token_dev, hidden, H);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int n, void* part, int* token_out, int* ids,
+                         int* pos, hipStream_t s) {
+    float* pv = static_cast<float*>(part);
+    int* pi = reinterpret_cast<int*>(pv + kArgmaxBlocks);
+    argmax_pass1<<<kArgmaxBlocks, 256, 0, s>>>(logits, n, pv, pi);
+    argmax_pass2<<<1, 256, 0, s>>>(pv, pi, token_out, ids, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_int(int* p, int v, hipStream_t s) {
+    add_int_kernel<<<1, 1, 0, s>>>(p, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_int(int* p, int v, hipStream_t s) {
+    set_int_kernel<<<1, 1, 0, s>>>(p, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t s) {
+    copy_kernel<<<grid_for(n), 256, 0, s>>>(dst, src, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s) {
+    fill_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s) {
+    fill_normal_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, key, std);
+    return hipGetLastError();
+}
+
+}  // namespace q35k

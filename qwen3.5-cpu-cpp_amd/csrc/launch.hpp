@@ -1,0 +1,95 @@
+#pragma once
+// Host-side launchers of the gfx950 kernels. Each returns the hipError_t of its launch.
+// Shapes are checked by the callers (c_api_kernels.hip, runtime.hip) before launching.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace q35k {
+
+// ---------------------------------------------------------------- bf16 x fp32 matvec
+// y[r] = (resid ? resid[r] : 0) + sum_i W[r][i] * x'[i] for r < rows, where x' is the input
+// after the prologue:
+enum GemvPrologue : int {
+    kProPlain = 0,      // x' = x
+    kProRmsNorm = 1,    // x' = x * rsqrt(mean(x^2) + eps) * (1 + norm_w)     (input norms)
+    kProSwiGlu = 2,     // x' = silu(x[i]) * x[in_dim + i]                     (FFN down)
+    kProGatedNorm = 3,  // x' = norm_w[i % hd] * (x * rsqrt(mean_head(x^2)+eps)) * silu(gate)
+};
+struct GemvArgs {
+    const uint16_t* W;  // [rows][in_dim] bf16, 16-byte aligned rows (in_dim % 8 == 0)
+    const float* x;
+    const float* norm_w;
+    const float* gate;
+    const float* resid;  // may alias y
+    float* y;
+    int rows, in_dim, head_dim;
+    float eps;
+};
+hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s);
+// Largest in_dim the matvec stages in LDS.
+constexpr int kGemvMaxIn = 16384;
+
+// ---------------------------------------------------------------- GDN decode
+struct GdnDecodeArgs {
+    int n_layers, KH, VH, KER;  // DK = DV = 128
+    int pos_val;
+    const int* pos_dev;         // position read on the device when non-null
+    float eps;
+    const float *qkv, *z, *b, *a;                 // per-layer contiguous inputs
+    const float *conv_w, *A_log, *dt_bias, *norm_w;
+    float *conv_ring, *state, *out;
+    // per-layer strides in elements (0 = derive the contiguous stride)
+    int64_t ls_qkv, ls_z, ls_ba, ls_convw, ls_vh, ls_normw, ls_ring, ls_state, ls_out;
+};
+hipError_t launch_gdn_decode(const GdnDecodeArgs& a, bool fuse_norm, hipStream_t s);
+
+// ---------------------------------------------------------------- attention decode
+struct AttnDecodeArgs {
+    int NQ, NKV, HD, ROT;       // HD = 256
+    int pos_val;
+    const int* pos_dev;
+    int64_t max_ctx;
+    int n_splits;               // splits per kv head (grid.x of the partial kernel)
+    double theta;
+    float eps;
+    const float *qg, *k_new, *v_new, *q_norm, *k_norm;
+    float *k_cache, *v_cache;   // [NKV][max_ctx][HD]
+    float* q_work;              // [NQ][HD] normed + rotated queries
+    float* part_o;              // [NKV][n_splits][GRP][HD]
+    float* part_ml;             // [NKV][n_splits][GRP][2]
+    float* out;                 // [NQ][HD]
+};
+constexpr int kAttnChunk = 32;  // positions per sub-chunk of a split
+hipError_t launch_attn_prep(const AttnDecodeArgs& a, hipStream_t s);
+hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s);
+hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s);
+// workspace floats for part_o + part_ml (q_work excluded)
+inline int64_t attn_partial_floats(int NQ, int NKV, int HD, int n_splits) {
+    const int grp = NQ / NKV;
+    return static_cast<int64_t>(NKV) * n_splits * grp * (HD + 2);
+}
+
+// ---------------------------------------------------------------- small kernels
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
+                               float eps, int gated, const float* gate, hipStream_t s);
+hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s);
+hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
+                            double theta, hipStream_t s);
+// hidden[i] = bf16 embed[token][i]; token read from token_dev
+hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* hidden, int H,
+                        hipStream_t s);
+// argmax over n logits (first index of the maximum) in two passes through `part`
+// (2 * kArgmaxBlocks words). The final pass writes the index to token_out; when pos is
+// non-null it also stores the index at ids[*pos] (ids may be null) and increments *pos.
+constexpr int kArgmaxBlocks = 256;
+hipError_t launch_argmax(const float* logits, int n, void* part, int* token_out, int* ids,
+                         int* pos, hipStream_t s);
+hipError_t launch_add_int(int* p, int v, hipStream_t s);
+hipError_t launch_set_int(int* p, int v, hipStream_t s);
+hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t s);
+hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s);
+// dst[i] = std * N(0,1)(key, i)
+hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s);
+
+}  // namespace q35k

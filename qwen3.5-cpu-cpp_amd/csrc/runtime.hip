@@ -1,0 +1,1021 @@
+// Device-resident decoder behind the model-level C ABI (QwenModel, src/qwen_model.cpp).
+//
+// Memory plan: four device arenas, one hipMalloc each, made when the model is created:
+//   weights  every projection as bf16 (layer matrices fused row-wise where one matvec
+//            serves several reference matmuls), small vectors widened to fp32
+//   state    GDN states [L_gdn][VH][DK][DV] fp32, conv rings [L_gdn][4][CONV] fp32
+//   kv       [L_attn][K|V][NKV][max_context][HD] fp32
+//   scratch  per-step activations, split-K partials, logits, argmax partials, device
+//            token / position, the greedy id history
+// A decode step launches kernels only: no allocation, no host synchronisation. The
+// position lives on the device, so a captured step graph replays unchanged every token.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <iostream>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../host/memory_budget.h"
+#include "../host/model_config.h"
+#include "../host/q35_internal.h"
+#include "../host/safetensors_loader.h"
+#include "../host/synth.h"
+#include "launch.hpp"
+
+namespace {
+
+std::atomic<int64_t> g_dev_allocs{0};
+
+#define HIPCHK(expr)                                                                        \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return q35::fail(Q35_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));  \
+    } while (0)
+
+hipError_t dev_alloc(void** p, size_t bytes) {
+    g_dev_allocs.fetch_add(1);
+    return hipMalloc(p, bytes);
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct LayerDev {
+    bool attn = false;
+    int idx = 0;
+    const uint16_t* w_in = nullptr;   // GDN [qkv|z|b|a] or attention [q|k|v], rows x H
+    const uint16_t* w_out = nullptr;  // out_proj / o_proj
+    const uint16_t* w_gu = nullptr;   // [gate|up] 2I x H
+    const uint16_t* w_down = nullptr; // H x I
+    const float* input_ln = nullptr;
+    const float* post_ln = nullptr;
+    const float* conv_w = nullptr;
+    const float* A_log = nullptr;
+    const float* dt_bias = nullptr;
+    const float* gdn_norm = nullptr;
+    const float* q_norm = nullptr;
+    const float* k_norm = nullptr;
+    int in_rows = 0;
+};
+
+}  // namespace
+
+struct q35_model {
+    q35_dims d{};
+    int64_t max_ctx = 0;
+    hipStream_t stream = nullptr;
+    uint8_t* w_arena = nullptr;
+    size_t w_bytes = 0;
+    float* state_arena = nullptr;
+    size_t state_bytes = 0;
+    float* kv_arena = nullptr;
+    size_t kv_bytes = 0;
+    uint8_t* scratch = nullptr;
+    size_t scratch_bytes = 0;
+
+    std::vector<LayerDev> layers;
+    const uint16_t* embed = nullptr;
+    const uint16_t* head = nullptr;
+    int64_t embed_rows = 0;
+    const float* final_norm = nullptr;
+
+    float* gdn_state = nullptr;  // inside state_arena
+    float* conv_ring = nullptr;
+
+    float *hidden = nullptr, *proj = nullptr, *mix = nullptr, *gu = nullptr, *qwork = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr, *trace = nullptr;
+    void* argmax_part = nullptr;
+    int *token_dev = nullptr, *pos_dev = nullptr, *ids_dev = nullptr;
+    int n_splits = 0;
+
+    int64_t pos = 0;  // host mirror of *pos_dev
+    int32_t* pinned_token = nullptr;
+
+    bool use_graph = true;
+    bool graph_valid = false;
+    bool trace_on = false;
+    bool timing_on = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    std::vector<hipEvent_t> ev;  // timing event pairs
+    std::vector<int> ev_class;
+    size_t ev_used = 0;
+    double kt_ms[Q35_KT_COUNT] = {};
+    int64_t kt_n[Q35_KT_COUNT] = {};
+
+    q35_budget budget{};
+};
+
+namespace {
+
+// ------------------------------------------------------------------ shape checks
+q35_status check_dims(const q35_dims& d) {
+    if (d.hidden_size <= 0 || d.n_layers_total <= 0 || d.attn_interval <= 0 || d.vocab_size <= 0)
+        return q35::fail(Q35_ERR_ARG, "invalid dims");
+    if (d.gdn_k_head_dim != 128 || d.gdn_v_head_dim != 128)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "GDN head dims must be 128 (got %d/%d)",
+                         d.gdn_k_head_dim, d.gdn_v_head_dim);
+    if (d.gdn_conv_kernel != 4)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "conv kernel must be 4 (got %d)", d.gdn_conv_kernel);
+    if (d.gdn_k_heads <= 0 || d.gdn_v_heads % d.gdn_k_heads != 0 || d.gdn_v_heads > 64)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "GDN heads %d/%d unsupported", d.gdn_k_heads, d.gdn_v_heads);
+    if (d.attn_head_dim != 256)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "attention head_dim must be 256 (got %d)", d.attn_head_dim);
+    if (d.attn_kv_heads <= 0 || d.attn_q_heads % d.attn_kv_heads != 0)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "attention heads %d/%d", d.attn_q_heads, d.attn_kv_heads);
+    const int grp = d.attn_q_heads / d.attn_kv_heads;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "GQA group %d not in {1,2,4,8,16}", grp);
+    const int rot = static_cast<int>(d.attn_head_dim * d.partial_rotary_factor);
+    if (rot < 0 || rot > d.attn_head_dim || (rot & 1))
+        return q35::fail(Q35_ERR_UNSUPPORTED, "rotary dims %d", rot);
+    const int H = d.hidden_size, I = d.ffn_intermediate;
+    const int VD = d.gdn_v_heads * 128, QD = d.attn_q_heads * 256;
+    for (int n : {H, I, VD, QD})
+        if (n % 8 != 0 || n > q35k::kGemvMaxIn)
+            return q35::fail(Q35_ERR_UNSUPPORTED, "matvec input width %d (needs %%8 == 0, <= %d)", n,
+                             q35k::kGemvMaxIn);
+    return Q35_OK;
+}
+
+int rot_dims(const q35_dims& d) { return static_cast<int>(d.attn_head_dim * d.partial_rotary_factor); }
+
+// ------------------------------------------------------------------ weight arena layout
+struct Piece {
+    const q35_tensor* src;
+    size_t off;   // byte offset in the arena
+    bool to_f32;  // widen to fp32 (small vectors) instead of keeping bf16
+};
+
+int64_t numel_of(const q35_tensor* t) {
+    int64_t n = 1;
+    for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+    return t->ndim > 0 ? n : 0;
+}
+
+class ArenaPlanner {
+public:
+    explicit ArenaPlanner(const q35_tensor* ts, int n) : ts_(ts), n_(n) {}
+    const q35_tensor* find(const std::string& name) const {
+        for (int i = 0; i < n_; ++i)
+            if (ts_[i].name && name == ts_[i].name) return &ts_[i];
+        return nullptr;
+    }
+    // bf16 matrix rows x cols; returns arena offset or SIZE_MAX with the error set
+    size_t mat(const std::vector<std::string>& names, int64_t cols, int64_t* rows_out, q35_status* st) {
+        int64_t rows = 0;
+        const size_t off = cursor_;
+        for (const std::string& nm : names) {
+            const q35_tensor* t = find(nm);
+            if (!t) {
+                *st = q35::fail(Q35_ERR_MISSING, "missing weight: %s", nm.c_str());
+                return SIZE_MAX;
+            }
+            if (t->dtype != 0) {
+                *st = q35::fail(Q35_ERR_UNSUPPORTED, "weight %s must be BF16", nm.c_str());
+                return SIZE_MAX;
+            }
+            const int64_t n = numel_of(t);
+            if (n % cols != 0 || t->shape[t->ndim - 1] != cols) {
+                *st = q35::fail(Q35_ERR_FORMAT, "weight %s has %lld elements, not a multiple of %lld columns",
+                                nm.c_str(), static_cast<long long>(n), static_cast<long long>(cols));
+                return SIZE_MAX;
+            }
+            pieces_.push_back({t, cursor_ + static_cast<size_t>(rows * cols) * 2, false});
+            rows += n / cols;
+        }
+        cursor_ = align256(cursor_ + static_cast<size_t>(rows * cols) * 2);
+        if (rows_out) *rows_out = rows;
+        return off;
+    }
+    size_t vec(const std::string& name, int64_t expect, q35_status* st) {
+        const q35_tensor* t = find(name);
+        if (!t) {
+            *st = q35::fail(Q35_ERR_MISSING, "missing weight: %s", name.c_str());
+            return SIZE_MAX;
+        }
+        if (t->dtype != 0 && t->dtype != 1) {
+            *st = q35::fail(Q35_ERR_UNSUPPORTED, "weight %s: unsupported dtype", name.c_str());
+            return SIZE_MAX;
+        }
+        if (numel_of(t) != expect) {
+            *st = q35::fail(Q35_ERR_FORMAT, "weight %s has %lld elements, expected %lld", name.c_str(),
+                            static_cast<long long>(numel_of(t)), static_cast<long long>(expect));
+            return SIZE_MAX;
+        }
+        const size_t off = cursor_;
+        pieces_.push_back({t, off, true});
+        cursor_ = align256(cursor_ + static_cast<size_t>(expect) * 4);
+        return off;
+    }
+    size_t bytes() const { return cursor_; }
+    const std::vector<Piece>& pieces() const { return pieces_; }
+
+private:
+    const q35_tensor* ts_;
+    int n_;
+    size_t cursor_ = 0;
+    std::vector<Piece> pieces_;
+};
+
+// ------------------------------------------------------------------ step enqueue
+struct Launcher {
+    q35_model* m;
+    hipStream_t s;
+    bool timed;
+    q35_status st = Q35_OK;
+
+    template <class F>
+    void run(int cls, F&& f) {
+        if (st != Q35_OK) return;
+        if (timed) {
+            if (m->ev_used + 2 > m->ev.size()) {
+                hipEvent_t a = nullptr, b = nullptr;
+                if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+                    st = q35::fail(Q35_ERR_HIP, "hipEventCreate failed");
+                    return;
+                }
+                m->ev.push_back(a);
+                m->ev.push_back(b);
+                m->ev_class.push_back(cls);
+            }
+            m->ev_class[m->ev_used / 2] = cls;
+            if (hipEventRecord(m->ev[m->ev_used], s) != hipSuccess) {
+                st = q35::fail(Q35_ERR_HIP, "hipEventRecord failed");
+                return;
+            }
+        }
+        const hipError_t e = f();
+        if (e != hipSuccess) st = q35::fail(Q35_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+        if (timed) {
+            if (hipEventRecord(m->ev[m->ev_used + 1], s) != hipSuccess && st == Q35_OK)
+                st = q35::fail(Q35_ERR_HIP, "hipEventRecord failed");
+            m->ev_used += 2;
+        }
+    }
+};
+
+q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
+    const q35_dims& d = m->d;
+    const int H = d.hidden_size, I = d.ffn_intermediate;
+    const int KH = d.gdn_k_heads, VH = d.gdn_v_heads, KD = KH * 128, VD = VH * 128;
+    const int CONV = 2 * KD + VD;
+    const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    Launcher L{m, s, timed};
+    L.run(Q35_KT_OTHER, [&] { return q35k::launch_embed(m->embed, m->token_dev, m->hidden, H, s); });
+    for (size_t li = 0; li < m->layers.size(); ++li) {
+        const LayerDev& ly = m->layers[li];
+        q35k::GemvArgs g{};
+        g.W = ly.w_in;
+        g.x = m->hidden;
+        g.norm_w = ly.input_ln;
+        g.y = m->proj;
+        g.rows = ly.in_rows;
+        g.in_dim = H;
+        g.eps = d.rms_norm_eps;
+        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(g, q35k::kProRmsNorm, s); });
+        if (!ly.attn) {
+            q35k::GdnDecodeArgs ga{};
+            ga.n_layers = 1;
+            ga.KH = KH;
+            ga.VH = VH;
+            ga.KER = 4;
+            ga.pos_dev = m->pos_dev;
+            ga.eps = d.rms_norm_eps;
+            ga.qkv = m->proj;
+            ga.z = m->proj + CONV;
+            ga.b = m->proj + CONV + VD;
+            ga.a = m->proj + CONV + VD + VH;
+            ga.conv_w = ly.conv_w;
+            ga.A_log = ly.A_log;
+            ga.dt_bias = ly.dt_bias;
+            ga.norm_w = ly.gdn_norm;
+            ga.conv_ring = m->conv_ring + static_cast<int64_t>(ly.idx) * 4 * CONV;
+            ga.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
+            ga.out = m->mix;
+            L.run(Q35_KT_GDN_DECODE, [&] { return q35k::launch_gdn_decode(ga, false, s); });
+            q35k::GemvArgs o{};
+            o.W = ly.w_out;
+            o.x = m->mix;
+            o.norm_w = ly.gdn_norm;
+            o.gate = m->proj + CONV;
+            o.head_dim = 128;
+            o.resid = m->hidden;
+            o.y = m->hidden;
+            o.rows = H;
+            o.in_dim = VD;
+            o.eps = d.rms_norm_eps;
+            L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(o, q35k::kProGatedNorm, s); });
+        } else {
+            q35k::AttnDecodeArgs aa{};
+            aa.NQ = NQ;
+            aa.NKV = NKV;
+            aa.HD = HD;
+            aa.ROT = rot_dims(d);
+            aa.pos_dev = m->pos_dev;
+            aa.max_ctx = m->max_ctx;
+            aa.n_splits = m->n_splits;
+            aa.theta = d.rope_theta;
+            aa.eps = d.rms_norm_eps;
+            aa.qg = m->proj;
+            aa.k_new = m->proj + 2 * NQ * HD;
+            aa.v_new = m->proj + 2 * NQ * HD + NKV * HD;
+            aa.q_norm = ly.q_norm;
+            aa.k_norm = ly.k_norm;
+            aa.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
+            aa.v_cache = aa.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
+            aa.q_work = m->qwork;
+            aa.part_o = m->part_o;
+            aa.part_ml = m->part_ml;
+            aa.out = m->mix;
+            L.run(Q35_KT_ATTN_PREP, [&] { return q35k::launch_attn_prep(aa, s); });
+            L.run(Q35_KT_ATTN_DECODE, [&] { return q35k::launch_attn_partial(aa, s); });
+            L.run(Q35_KT_ATTN_COMBINE, [&] { return q35k::launch_attn_combine(aa, s); });
+            q35k::GemvArgs o{};
+            o.W = ly.w_out;
+            o.x = m->mix;
+            o.resid = m->hidden;
+            o.y = m->hidden;
+            o.rows = H;
+            o.in_dim = NQ * HD;
+            L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(o, q35k::kProPlain, s); });
+        }
+        q35k::GemvArgs f1{};
+        f1.W = ly.w_gu;
+        f1.x = m->hidden;
+        f1.norm_w = ly.post_ln;
+        f1.y = m->gu;
+        f1.rows = 2 * I;
+        f1.in_dim = H;
+        f1.eps = d.rms_norm_eps;
+        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f1, q35k::kProRmsNorm, s); });
+        q35k::GemvArgs f2{};
+        f2.W = ly.w_down;
+        f2.x = m->gu;
+        f2.resid = m->hidden;
+        f2.y = m->hidden;
+        f2.rows = H;
+        f2.in_dim = I;
+        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f2, q35k::kProSwiGlu, s); });
+        if (m->trace_on)
+            L.run(Q35_KT_OTHER, [&] {
+                return q35k::launch_copy_f32(m->trace + li * H, m->hidden, H, s);
+            });
+    }
+    q35k::GemvArgs hd{};
+    hd.W = m->head;
+    hd.x = m->hidden;
+    hd.norm_w = m->final_norm;
+    hd.y = m->logits;
+    hd.rows = d.vocab_size;
+    hd.in_dim = H;
+    hd.eps = d.rms_norm_eps;
+    L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(hd, q35k::kProRmsNorm, s); });
+    L.run(Q35_KT_OTHER, [&] {
+        return q35k::launch_argmax(m->logits, d.vocab_size, m->argmax_part, m->token_dev, m->ids_dev,
+                                   m->pos_dev, s);
+    });
+    return L.st;
+}
+
+void drop_graph(q35_model* m) {
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    m->graph_valid = false;
+}
+
+q35_status build_graph(q35_model* m) {
+    drop_graph(m);
+    HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    const q35_status st = enqueue_step(m, m->stream, false);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (st != Q35_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return q35::fail(Q35_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+    m->graph = g;
+    HIPCHK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    m->graph_valid = true;
+    return Q35_OK;
+}
+
+// Enqueue one step for the token already in token_dev.
+q35_status launch_one_step(q35_model* m) {
+    if (m->timing_on || m->trace_on || !m->use_graph) {
+        const q35_status st = enqueue_step(m, m->stream, m->timing_on);
+        if (st != Q35_OK) return st;
+    } else {
+        if (!m->graph_valid) {
+            const q35_status st = build_graph(m);
+            if (st != Q35_OK) return st;
+        }
+        HIPCHK(hipGraphLaunch(m->exec, m->stream));
+    }
+    m->pos += 1;
+    return Q35_OK;
+}
+
+q35_status collect_timing(q35_model* m) {
+    if (!m->timing_on || m->ev_used == 0) return Q35_OK;
+    HIPCHK(hipStreamSynchronize(m->stream));
+    for (size_t i = 0; i + 1 < m->ev_used; i += 2) {
+        float ms = 0.0f;
+        HIPCHK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
+        const int c = m->ev_class[i / 2];
+        m->kt_ms[c] += ms;
+        m->kt_n[c] += 1;
+    }
+    m->ev_used = 0;
+    return Q35_OK;
+}
+
+void destroy(q35_model* m) {
+    if (!m) return;
+    // teardown: errors are not actionable here, each release is attempted
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    drop_graph(m);
+    for (hipEvent_t e : m->ev) (void)hipEventDestroy(e);
+    if (m->pinned_token) (void)hipHostFree(m->pinned_token);
+    if (m->w_arena) (void)hipFree(m->w_arena);
+    if (m->state_arena) (void)hipFree(m->state_arena);
+    if (m->kv_arena) (void)hipFree(m->kv_arena);
+    if (m->scratch) (void)hipFree(m->scratch);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int64_t max_ctx,
+                        q35_model** out) {
+    if (!dims || !ts || !out || nt <= 0) return q35::fail(Q35_ERR_ARG, "q35_model_create: null argument");
+    *out = nullptr;
+    if (max_ctx <= 0 || max_ctx > (int64_t{1} << 30))
+        return q35::fail(Q35_ERR_RANGE, "max_context %lld out of range", static_cast<long long>(max_ctx));
+    q35_dims d = *dims;
+    d.n_layers_attn = d.n_layers_total / d.attn_interval;
+    d.n_layers_gdn = d.n_layers_total - d.n_layers_attn;
+    q35_status st = check_dims(d);
+    if (st != Q35_OK) return st;
+
+    const int H = d.hidden_size, I = d.ffn_intermediate;
+    const int KH = d.gdn_k_heads, VH = d.gdn_v_heads, KD = KH * 128, VD = VH * 128;
+    const int CONV = 2 * KD + VD;
+    const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    const std::string lm = "model.language_model.";
+
+    // weight arena plan
+    ArenaPlanner plan(ts, nt);
+    struct LayerOff {
+        size_t w_in, w_out, w_gu, w_down, input_ln, post_ln, conv_w, A_log, dt_bias, gdn_norm, q_norm, k_norm;
+        int64_t in_rows;
+    };
+    std::vector<LayerOff> lo(static_cast<size_t>(d.n_layers_total));
+    auto bad = [](size_t o) { return o == SIZE_MAX; };
+    for (int l = 0; l < d.n_layers_total; ++l) {
+        const std::string p = lm + "layers." + std::to_string(l) + ".";
+        LayerOff& o = lo[static_cast<size_t>(l)];
+        o = LayerOff{};
+        o.input_ln = plan.vec(p + "input_layernorm.weight", H, &st);
+        if (bad(o.input_ln)) return st;
+        o.post_ln = plan.vec(p + "post_attention_layernorm.weight", H, &st);
+        if (bad(o.post_ln)) return st;
+        int64_t r = 0;
+        o.w_gu = plan.mat({p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"}, H, &r, &st);
+        if (bad(o.w_gu)) return st;
+        if (r != 2 * I) return q35::fail(Q35_ERR_FORMAT, "layer %d: gate/up rows %lld != 2*%d", l, (long long)r, I);
+        o.w_down = plan.mat({p + "mlp.down_proj.weight"}, I, &r, &st);
+        if (bad(o.w_down)) return st;
+        if (r != H) return q35::fail(Q35_ERR_FORMAT, "layer %d: down_proj rows %lld != %d", l, (long long)r, H);
+        if ((l + 1) % d.attn_interval == 0) {
+            const std::string a = p + "self_attn.";
+            o.w_in = plan.mat({a + "q_proj.weight", a + "k_proj.weight", a + "v_proj.weight"}, H, &o.in_rows, &st);
+            if (bad(o.w_in)) return st;
+            if (o.in_rows != 2LL * NQ * HD + 2LL * NKV * HD)
+                return q35::fail(Q35_ERR_FORMAT, "layer %d: q/k/v rows %lld", l, (long long)o.in_rows);
+            o.w_out = plan.mat({a + "o_proj.weight"}, static_cast<int64_t>(NQ) * HD, &r, &st);
+            if (bad(o.w_out)) return st;
+            if (r != H) return q35::fail(Q35_ERR_FORMAT, "layer %d: o_proj rows %lld", l, (long long)r);
+            o.q_norm = plan.vec(a + "q_norm.weight", HD, &st);
+            if (bad(o.q_norm)) return st;
+            o.k_norm = plan.vec(a + "k_norm.weight", HD, &st);
+            if (bad(o.k_norm)) return st;
+        } else {
+            const std::string g = p + "linear_attn.";
+            o.w_in = plan.mat({g + "in_proj_qkv.weight", g + "in_proj_z.weight", g + "in_proj_b.weight",
+                               g + "in_proj_a.weight"},
+                              H, &o.in_rows, &st);
+            if (bad(o.w_in)) return st;
+            if (o.in_rows != static_cast<int64_t>(CONV) + VD + 2 * VH)
+                return q35::fail(Q35_ERR_FORMAT, "layer %d: GDN in-projection rows %lld", l, (long long)o.in_rows);
+            o.w_out = plan.mat({g + "out_proj.weight"}, VD, &r, &st);
+            if (bad(o.w_out)) return st;
+            if (r != H) return q35::fail(Q35_ERR_FORMAT, "layer %d: out_proj rows %lld", l, (long long)r);
+            o.conv_w = plan.vec(g + "conv1d.weight", static_cast<int64_t>(CONV) * 4, &st);
+            if (bad(o.conv_w)) return st;
+            o.dt_bias = plan.vec(g + "dt_bias", VH, &st);
+            if (bad(o.dt_bias)) return st;
+            o.A_log = plan.vec(g + "A_log", VH, &st);
+            if (bad(o.A_log)) return st;
+            o.gdn_norm = plan.vec(g + "norm.weight", 128, &st);
+            if (bad(o.gdn_norm)) return st;
+        }
+    }
+    const q35_tensor* emb_t = plan.find(lm + "embed_tokens.weight");
+    if (!emb_t) return q35::fail(Q35_ERR_MISSING, "missing weight: %sembed_tokens.weight", lm.c_str());
+    int64_t emb_rows = 0;
+    const size_t emb_off = plan.mat({lm + "embed_tokens.weight"}, H, &emb_rows, &st);
+    if (bad(emb_off)) return st;
+    size_t head_off = emb_off;
+    int64_t head_rows = emb_rows;
+    for (const std::string& hn : {std::string("lm_head.weight"), lm + "lm_head.weight"}) {
+        if (plan.find(hn)) {
+            head_off = plan.mat({hn}, H, &head_rows, &st);
+            if (bad(head_off)) return st;
+            break;
+        }
+    }
+    if (head_rows < d.vocab_size || emb_rows < d.vocab_size)
+        return q35::fail(Q35_ERR_FORMAT, "embedding / output head rows %lld / %lld < vocab %d", (long long)emb_rows,
+                         (long long)head_rows, d.vocab_size);
+    const size_t fnorm_off = plan.vec(lm + "norm.weight", H, &st);
+    if (bad(fnorm_off)) return st;
+
+    std::unique_ptr<q35_model, void (*)(q35_model*)> m(new (std::nothrow) q35_model(), destroy);
+    if (!m) return q35::fail(Q35_ERR_ARG, "out of host memory");
+    m->d = d;
+    m->max_ctx = max_ctx;
+    HIPCHK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+
+    // state, kv and scratch plans
+    const size_t gdn_bytes = static_cast<size_t>(d.n_layers_gdn) * VH * 128 * 128 * 4;
+    const size_t ring_bytes = static_cast<size_t>(d.n_layers_gdn) * 4 * CONV * 4;
+    m->state_bytes = align256(gdn_bytes) + align256(ring_bytes);
+    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * static_cast<size_t>(max_ctx) * HD * 4;
+    m->n_splits = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(1, (max_ctx + q35k::kAttnChunk - 1) / q35k::kAttnChunk)));
+    const int64_t proj_n = std::max<int64_t>(static_cast<int64_t>(CONV) + VD + 2 * VH, 2LL * NQ * HD + 2LL * NKV * HD);
+    size_t sc = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = sc;
+        sc = align256(sc + bytes);
+        return o;
+    };
+    const size_t o_hidden = take(static_cast<size_t>(H) * 4);
+    const size_t o_proj = take(static_cast<size_t>(proj_n) * 4);
+    const size_t o_mix = take(static_cast<size_t>(std::max(VD, NQ * HD)) * 4);
+    const size_t o_gu = take(static_cast<size_t>(2) * I * 4);
+    const size_t o_qwork = take(static_cast<size_t>(NQ) * HD * 4);
+    const int64_t pf = q35k::attn_partial_floats(NQ, NKV, HD, m->n_splits);
+    const size_t o_part = take(static_cast<size_t>(pf) * 4);
+    const size_t o_logits = take(static_cast<size_t>(d.vocab_size) * 4);
+    const size_t o_trace = take(static_cast<size_t>(d.n_layers_total) * H * 4);
+    const size_t o_am = take(static_cast<size_t>(2) * q35k::kArgmaxBlocks * 4);
+    const size_t o_ints = take(16 * 4);
+    const size_t o_ids = take(static_cast<size_t>(max_ctx) * 4);
+    m->scratch_bytes = sc;
+    m->w_bytes = plan.bytes();
+
+    std::cout << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
+              << " MiB, state " << (m->state_bytes >> 10) << " KiB, kv " << (m->kv_bytes >> 20)
+              << " MiB, scratch " << (m->scratch_bytes >> 10) << " KiB\n";
+
+    void* p = nullptr;
+    HIPCHK(dev_alloc(&p, m->w_bytes));
+    m->w_arena = static_cast<uint8_t*>(p);
+    HIPCHK(dev_alloc(&p, m->state_bytes));
+    m->state_arena = static_cast<float*>(p);
+    HIPCHK(dev_alloc(&p, std::max<size_t>(m->kv_bytes, 256)));
+    m->kv_arena = static_cast<float*>(p);
+    HIPCHK(dev_alloc(&p, m->scratch_bytes));
+    m->scratch = static_cast<uint8_t*>(p);
+    HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&m->pinned_token), 64, hipHostMallocDefault));
+
+    // upload
+    std::vector<float> tmp;
+    for (const Piece& pc : plan.pieces()) {
+        const int64_t n = numel_of(pc.src);
+        if (!pc.to_f32) {
+            HIPCHK(hipMemcpy(m->w_arena + pc.off, pc.src->data, static_cast<size_t>(n) * 2, hipMemcpyHostToDevice));
+        } else {
+            tmp.resize(static_cast<size_t>(n));
+            if (pc.src->dtype == 1) {
+                std::memcpy(tmp.data(), pc.src->data, static_cast<size_t>(n) * 4);
+            } else {
+                const auto* b = static_cast<const uint16_t*>(pc.src->data);
+                for (int64_t i = 0; i < n; ++i) tmp[static_cast<size_t>(i)] = bf16_to_f32(b[i]);
+            }
+            HIPCHK(hipMemcpy(m->w_arena + pc.off, tmp.data(), static_cast<size_t>(n) * 4, hipMemcpyHostToDevice));
+        }
+    }
+
+    auto W16 = [&](size_t off) { return reinterpret_cast<const uint16_t*>(m->w_arena + off); };
+    auto W32 = [&](size_t off) { return reinterpret_cast<const float*>(m->w_arena + off); };
+    int ai = 0, gi = 0;
+    m->layers.resize(static_cast<size_t>(d.n_layers_total));
+    for (int l = 0; l < d.n_layers_total; ++l) {
+        const LayerOff& o = lo[static_cast<size_t>(l)];
+        LayerDev& ly = m->layers[static_cast<size_t>(l)];
+        ly.attn = (l + 1) % d.attn_interval == 0;
+        ly.idx = ly.attn ? ai++ : gi++;
+        ly.w_in = W16(o.w_in);
+        ly.w_out = W16(o.w_out);
+        ly.w_gu = W16(o.w_gu);
+        ly.w_down = W16(o.w_down);
+        ly.input_ln = W32(o.input_ln);
+        ly.post_ln = W32(o.post_ln);
+        ly.in_rows = static_cast<int>(o.in_rows);
+        if (ly.attn) {
+            ly.q_norm = W32(o.q_norm);
+            ly.k_norm = W32(o.k_norm);
+        } else {
+            ly.conv_w = W32(o.conv_w);
+            ly.A_log = W32(o.A_log);
+            ly.dt_bias = W32(o.dt_bias);
+            ly.gdn_norm = W32(o.gdn_norm);
+        }
+    }
+    m->embed = W16(emb_off);
+    m->embed_rows = emb_rows;
+    m->head = W16(head_off);
+    m->final_norm = W32(fnorm_off);
+    m->gdn_state = m->state_arena;
+    m->conv_ring = m->state_arena + align256(gdn_bytes) / 4;
+    auto S32 = [&](size_t off) { return reinterpret_cast<float*>(m->scratch + off); };
+    m->hidden = S32(o_hidden);
+    m->proj = S32(o_proj);
+    m->mix = S32(o_mix);
+    m->gu = S32(o_gu);
+    m->qwork = S32(o_qwork);
+    m->part_o = S32(o_part);
+    m->part_ml = m->part_o + static_cast<int64_t>(NKV) * m->n_splits * (NQ / NKV) * HD;
+    m->logits = S32(o_logits);
+    m->trace = S32(o_trace);
+    m->argmax_part = m->scratch + o_am;
+    int* ints = reinterpret_cast<int*>(m->scratch + o_ints);
+    m->token_dev = ints;
+    m->pos_dev = ints + 1;
+    m->ids_dev = reinterpret_cast<int*>(m->scratch + o_ids);
+
+    // reset: zero state, kv and scratch with fill kernels
+    HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_fill_f32(reinterpret_cast<float*>(m->scratch), static_cast<int64_t>(m->scratch_bytes / 4), 0.0f, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+
+    m->budget.weight_bytes = m->w_bytes;
+    m->budget.gdn_state_bytes = gdn_bytes;
+    m->budget.gdn_conv_bytes = ring_bytes;
+    m->budget.kv_cache_bytes = m->kv_bytes;
+    m->budget.activation_bytes = m->scratch_bytes;
+    m->budget.vision_scratch_bytes = 0;
+    *out = m.release();
+    return Q35_OK;
+}
+
+// reference window [CONV][KER-1] (oldest first) <-> ring slot (t % 4) for t = pos-3..pos-1
+int64_t ring_slot(int64_t pos, int k) { return (((pos - 3 + k) % 4) + 4) % 4; }
+
+q35_status check_model(const q35_model* m) {
+    return m ? Q35_OK : q35::fail(Q35_ERR_ARG, "null model");
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t q35_device_alloc_count(void) { return g_dev_allocs.load(); }
+
+q35_status q35_model_create(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
+                            int64_t max_context, q35_model** out) {
+    return create_model(d, tensors, n_tensors, max_context, out);
+}
+
+q35_status q35_model_open(const char* model_dir, int64_t max_context, q35_model** out) {
+    if (!model_dir || !out) return q35::fail(Q35_ERR_ARG, "q35_model_open: null argument");
+    ModelConfig cfg;
+    load_model_config(std::string(model_dir) + "/config.json", cfg);
+    SafeTensors st;
+    if (!st.load_model(model_dir)) return q35::fail(Q35_ERR_IO, "cannot load safetensors from %s", model_dir);
+    std::vector<q35_tensor> table;
+    std::vector<std::string> names;
+    names.reserve(st.entries().size());
+    for (const auto& kv : st.entries()) names.push_back(kv.first);
+    table.reserve(names.size());
+    for (const std::string& nm : names) {
+        const SafeTensors::Entry* e = st.find(nm);
+        q35_tensor t{};
+        t.name = nm.c_str();
+        t.dtype = e->dtype == "BF16" ? 0 : e->dtype == "F32" ? 1 : 2;
+        t.ndim = static_cast<int32_t>(std::min<size_t>(4, e->shape.size()));
+        for (int i = 0; i < t.ndim; ++i) t.shape[i] = e->shape[static_cast<size_t>(i)];
+        t.data = st.data(nm);
+        table.push_back(t);
+    }
+    q35_dims d;
+    q35::dims_from_config(cfg, &d);
+    return create_model(&d, table.data(), static_cast<int32_t>(table.size()), max_context, out);
+}
+
+void q35_model_destroy(q35_model* m) { destroy(m); }
+
+q35_status q35_model_dims(const q35_model* m, q35_dims* out) {
+    if (!m || !out) return q35::fail(Q35_ERR_ARG, "null argument");
+    *out = m->d;
+    return Q35_OK;
+}
+
+q35_status q35_model_budget(const q35_model* m, q35_budget* out) {
+    if (!m || !out) return q35::fail(Q35_ERR_ARG, "null argument");
+    *out = m->budget;
+    return Q35_OK;
+}
+
+int64_t q35_model_position(const q35_model* m) { return m ? m->pos : -1; }
+int64_t q35_model_max_context(const q35_model* m) { return m ? m->max_ctx : -1; }
+q35_stream q35_model_stream(const q35_model* m) { return m ? m->stream : nullptr; }
+
+q35_status q35_model_synchronize(q35_model* m) {
+    if (check_model(m) != Q35_OK) return Q35_ERR_ARG;
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_reset(q35_model* m) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_set_int(m->pos_dev, 0, m->stream));
+    m->pos = 0;
+    return Q35_OK;
+}
+
+q35_status q35_model_step(q35_model* m, int32_t token, float* logits_host, int32_t* argmax) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (token < 0 || token >= m->embed_rows || token >= m->d.vocab_size)
+        return q35::fail(Q35_ERR_RANGE, "token %d outside [0, %d)", token, m->d.vocab_size);
+    if (m->pos >= m->max_ctx)
+        return q35::fail(Q35_ERR_RANGE, "position %lld reached max_context %lld", (long long)m->pos,
+                         (long long)m->max_ctx);
+    *m->pinned_token = token;
+    HIPCHK(hipMemcpyAsync(m->token_dev, m->pinned_token, 4, hipMemcpyHostToDevice, m->stream));
+    q35_status st = launch_one_step(m);
+    if (st != Q35_OK) return st;
+    if (logits_host)
+        HIPCHK(hipMemcpyAsync(logits_host, m->logits, static_cast<size_t>(m->d.vocab_size) * 4,
+                              hipMemcpyDeviceToHost, m->stream));
+    if (argmax) HIPCHK(hipMemcpyAsync(argmax, m->token_dev, 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return collect_timing(m);
+}
+
+}  // extern "C"
+
+namespace {
+
+// n_steps back-to-back steps on the device: the first fed with `token`, each next one with
+// the argmax the previous step left in token_dev. ids_dev[p] receives the argmax after
+// the step at position p.
+q35_status run_greedy(q35_model* m, int32_t token, int32_t n_steps) {
+    if (token < 0 || token >= m->d.vocab_size)
+        return q35::fail(Q35_ERR_RANGE, "token %d outside [0, %d)", token, m->d.vocab_size);
+    if (m->pos + n_steps > m->max_ctx)
+        return q35::fail(Q35_ERR_RANGE, "position %lld + %d steps exceeds max_context %lld", (long long)m->pos,
+                         n_steps, (long long)m->max_ctx);
+    *m->pinned_token = token;
+    HIPCHK(hipMemcpyAsync(m->token_dev, m->pinned_token, 4, hipMemcpyHostToDevice, m->stream));
+    for (int i = 0; i < n_steps; ++i) {
+        const q35_status st = launch_one_step(m);
+        if (st != Q35_OK) return st;
+        if (m->timing_on) {
+            const q35_status t = collect_timing(m);
+            if (t != Q35_OK) return t;
+        }
+    }
+    return Q35_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+q35_status q35_model_decode_greedy(q35_model* m, int32_t token, int32_t n_new, int32_t* out) {
+    if (!m || (n_new > 0 && !out) || n_new < 0) return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (n_new == 0) return Q35_OK;
+    const int64_t p0 = m->pos;
+    const q35_status st = run_greedy(m, token, n_new);
+    if (st != Q35_OK) return st;
+    HIPCHK(hipMemcpyAsync(out, m->ids_dev + p0, static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+// Same step sequence as the reference loop (src/qwen_model.cpp:241-255): every prompt token,
+// then n_new greedy steps, the last of which is fed with the last emitted id.
+q35_status q35_model_generate_greedy(q35_model* m, const int32_t* prompt, int32_t n_prompt,
+                                     int32_t n_new, int32_t* out) {
+    if (!m || (n_prompt > 0 && !prompt) || n_prompt < 0 || n_new < 0 || (n_new > 0 && !out))
+        return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (n_prompt + static_cast<int64_t>(n_new) > m->max_ctx)
+        return q35::fail(Q35_ERR_RANGE, "prompt + new tokens (%d + %d) exceed max_context %lld", n_prompt, n_new,
+                         (long long)m->max_ctx);
+    q35_status st = q35_model_reset(m);
+    if (st != Q35_OK) return st;
+    if (n_prompt == 0) return Q35_OK;  // the reference emits nothing without logits
+    for (int i = 0; i + 1 < n_prompt; ++i) {
+        st = q35_model_step(m, prompt[i], nullptr, nullptr);
+        if (st != Q35_OK) return st;
+    }
+    int32_t am = 0;
+    st = q35_model_step(m, prompt[n_prompt - 1], nullptr, &am);
+    if (st != Q35_OK || n_new == 0) return st;
+    st = run_greedy(m, am, n_new);
+    if (st != Q35_OK) return st;
+    HIPCHK(hipMemcpyAsync(out, m->ids_dev + (n_prompt - 1), static_cast<size_t>(n_new) * 4, hipMemcpyDeviceToHost,
+                          m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_set_graph(q35_model* m, int32_t enable) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    m->use_graph = enable != 0;
+    return Q35_OK;
+}
+
+q35_status q35_model_set_layer_trace(q35_model* m, int32_t enable) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    m->trace_on = enable != 0;
+    return Q35_OK;
+}
+
+q35_status q35_model_read_layer_trace(q35_model* m, float* host) {
+    if (!m || !host) return q35::fail(Q35_ERR_ARG, "null argument");
+    HIPCHK(hipMemcpyAsync(host, m->trace, static_cast<size_t>(m->d.n_layers_total) * m->d.hidden_size * 4,
+                          hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_read_hidden(q35_model* m, float* host) {
+    if (!m || !host) return q35::fail(Q35_ERR_ARG, "null argument");
+    HIPCHK(hipMemcpyAsync(host, m->hidden, static_cast<size_t>(m->d.hidden_size) * 4, hipMemcpyDeviceToHost,
+                          m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_set_kernel_timing(q35_model* m, int32_t enable) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    m->timing_on = enable != 0;
+    m->ev_used = 0;
+    return Q35_OK;
+}
+
+q35_status q35_model_kernel_times(q35_model* m, double* ms, int64_t* launches) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    const q35_status st = collect_timing(m);
+    if (st != Q35_OK) return st;
+    for (int i = 0; i < Q35_KT_COUNT; ++i) {
+        if (ms) ms[i] = m->kt_ms[i];
+        if (launches) launches[i] = m->kt_n[i];
+        m->kt_ms[i] = 0.0;
+        m->kt_n[i] = 0;
+    }
+    return Q35_OK;
+}
+
+q35_status q35_model_read_gdn_state(q35_model* m, int32_t layer, float* host) {
+    if (!m || !host || layer < 0 || layer >= m->d.n_layers_gdn) return q35::fail(Q35_ERR_ARG, "bad argument");
+    const size_t n = static_cast<size_t>(m->d.gdn_v_heads) * 128 * 128;
+    HIPCHK(hipMemcpyAsync(host, m->gdn_state + layer * n, n * 4, hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_write_gdn_state(q35_model* m, int32_t layer, const float* host) {
+    if (!m || !host || layer < 0 || layer >= m->d.n_layers_gdn) return q35::fail(Q35_ERR_ARG, "bad argument");
+    const size_t n = static_cast<size_t>(m->d.gdn_v_heads) * 128 * 128;
+    HIPCHK(hipMemcpyAsync(m->gdn_state + layer * n, host, n * 4, hipMemcpyHostToDevice, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_read_conv_state(q35_model* m, int32_t layer, float* host) {
+    if (!m || !host || layer < 0 || layer >= m->d.n_layers_gdn) return q35::fail(Q35_ERR_ARG, "bad argument");
+    const int64_t conv = 2LL * m->d.gdn_k_heads * 128 + m->d.gdn_v_heads * 128;
+    std::vector<float> ring(static_cast<size_t>(4 * conv));
+    HIPCHK(hipMemcpyAsync(ring.data(), m->conv_ring + layer * 4 * conv, ring.size() * 4, hipMemcpyDeviceToHost,
+                          m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    for (int64_t c = 0; c < conv; ++c)
+        for (int k = 0; k < 3; ++k) host[c * 3 + k] = ring[static_cast<size_t>(ring_slot(m->pos, k) * conv + c)];
+    return Q35_OK;
+}
+
+q35_status q35_model_write_conv_state(q35_model* m, int32_t layer, const float* host) {
+    if (!m || !host || layer < 0 || layer >= m->d.n_layers_gdn) return q35::fail(Q35_ERR_ARG, "bad argument");
+    const int64_t conv = 2LL * m->d.gdn_k_heads * 128 + m->d.gdn_v_heads * 128;
+    std::vector<float> ring(static_cast<size_t>(4 * conv), 0.0f);
+    for (int64_t c = 0; c < conv; ++c)
+        for (int k = 0; k < 3; ++k) ring[static_cast<size_t>(ring_slot(m->pos, k) * conv + c)] = host[c * 3 + k];
+    HIPCHK(hipMemcpyAsync(m->conv_ring + layer * 4 * conv, ring.data(), ring.size() * 4, hipMemcpyHostToDevice,
+                          m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_read_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t n, float* k_host,
+                             float* v_host) {
+    if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
+        return q35::fail(Q35_ERR_ARG, "bad argument");
+    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
+    const float* base = m->kv_arena + static_cast<int64_t>(layer) * 2 * NKV * m->max_ctx * HD;
+    for (int which = 0; which < 2; ++which) {
+        float* dst = which == 0 ? k_host : v_host;
+        if (!dst) continue;
+        for (int kh = 0; kh < NKV; ++kh) {
+            const float* src = base + (static_cast<int64_t>(which) * NKV + kh) * m->max_ctx * HD + pos0 * HD;
+            HIPCHK(hipMemcpy2DAsync(dst + kh * HD, static_cast<size_t>(NKV) * HD * 4, src,
+                                    static_cast<size_t>(HD) * 4, static_cast<size_t>(HD) * 4,
+                                    static_cast<size_t>(n), hipMemcpyDeviceToHost, m->stream));
+        }
+    }
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_write_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t n, const float* k_host,
+                              const float* v_host) {
+    if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
+        return q35::fail(Q35_ERR_ARG, "bad argument");
+    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
+    float* base = m->kv_arena + static_cast<int64_t>(layer) * 2 * NKV * m->max_ctx * HD;
+    for (int which = 0; which < 2; ++which) {
+        const float* src = which == 0 ? k_host : v_host;
+        if (!src) continue;
+        for (int kh = 0; kh < NKV; ++kh) {
+            float* dst = base + (static_cast<int64_t>(which) * NKV + kh) * m->max_ctx * HD + pos0 * HD;
+            HIPCHK(hipMemcpy2DAsync(dst, static_cast<size_t>(HD) * 4, src + kh * HD, static_cast<size_t>(NKV) * HD * 4,
+                                    static_cast<size_t>(HD) * 4, static_cast<size_t>(n), hipMemcpyHostToDevice,
+                                    m->stream));
+        }
+    }
+    HIPCHK(hipStreamSynchronize(m->stream));
+    return Q35_OK;
+}
+
+q35_status q35_model_set_position(q35_model* m, int64_t pos) {
+    if (!m || pos < 0 || pos > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "bad position");
+    HIPCHK(q35k::launch_set_int(m->pos_dev, static_cast<int>(pos), m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    m->pos = pos;
+    return Q35_OK;
+}
+
+q35_status q35_model_fill_synthetic(q35_model* m, int64_t pos, uint64_t seed, float state_std) {
+    if (!m || pos < 0 || pos > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "bad position");
+    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
+    for (int l = 0; l < m->d.n_layers_attn; ++l)
+        for (int which = 0; which < 2; ++which)
+            for (int kh = 0; kh < NKV; ++kh) {
+                float* dst = m->kv_arena + ((static_cast<int64_t>(l) * 2 + which) * NKV + kh) * m->max_ctx * HD;
+                const uint64_t stream = 0x4b560000ULL + (static_cast<uint64_t>(l) << 8) + (which << 4) + kh;
+                HIPCHK(q35k::launch_fill_normal(dst, pos * HD, q35synth::stream_key(seed, stream), 1.0f, m->stream));
+            }
+    const int64_t ns = static_cast<int64_t>(m->d.n_layers_gdn) * m->d.gdn_v_heads * 128 * 128;
+    HIPCHK(q35k::launch_fill_normal(m->gdn_state, ns, q35synth::stream_key(seed, 0x47444eULL), state_std, m->stream));
+    const int64_t conv = 2LL * m->d.gdn_k_heads * 128 + m->d.gdn_v_heads * 128;
+    HIPCHK(q35k::launch_fill_f32(m->conv_ring, static_cast<int64_t>(m->d.n_layers_gdn) * 4 * conv, 0.0f, m->stream));
+    HIPCHK(q35k::launch_set_int(m->pos_dev, static_cast<int>(pos), m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    m->pos = pos;
+    return Q35_OK;
+}
+
+q35_status q35_model_prefill(q35_model* m, const int32_t* ids, int32_t n, float* logits_host) {
+    if (!m || !ids || n <= 0) return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (n > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "prompt of %d exceeds max_context", n);
+    // Token-serial prefill through the decode kernels: the state it leaves is exactly
+    // what n decode steps leave. The chunked GDN / flash-attention prefill kernels
+    // replace this loop when built.
+    q35_status st = q35_model_reset(m);
+    if (st != Q35_OK) return st;
+    for (int t = 0; t < n; ++t) {
+        st = q35_model_step(m, ids[t], logits_host ? logits_host + static_cast<int64_t>(t) * m->d.vocab_size : nullptr,
+                            nullptr);
+        if (st != Q35_OK) return st;
+    }
+    return Q35_OK;
+}
+
+}  // extern "C"

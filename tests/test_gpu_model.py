@@ -1,0 +1,217 @@
+"""The device decoder (q35_model_*) against the golden vectors of the compiled reference and
+against the oracle: logits and residual stream after every layer, greedy ids, recurrent state
+and KV rows after 512 steps, the 0.8B-shaped full greedy decode, graph replay, the
+zero-allocation step and the error paths."""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle_py as op
+import pyq35
+from helpers import REL_L2, golden, rel_l2, sha256
+
+pytestmark = pytest.mark.gpu
+NAMES = ["tiny", "tiny_gqa", "tiny_untied"]
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_prompt_logits_and_layers(model_dirs, name):
+    g = golden(name)
+    m = pyq35.Model(model_dirs[name], 600)
+    m.set_layer_trace(True)
+    worst = 0.0
+    for t, tok in enumerate(g["prompt"]):
+        lg, _ = m.step(int(tok))
+        assert rel_l2(lg, g["logits"][t]) < REL_L2, f"logits step {t}"
+        tr = m.layer_trace()
+        for l in range(tr.shape[0]):
+            e = rel_l2(tr[l], g["trace"][t, l])
+            worst = max(worst, e)
+            assert e < REL_L2, f"step {t} layer {l}: {e}"
+    print(f"{name}: worst per-layer rel_l2 {worst:.3g}")
+    m.close()
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_greedy_ids(model_dirs, name):
+    g = golden(name)
+    m = pyq35.Model(model_dirs[name], 600)
+    ids = m.generate_greedy(g["prompt"], len(g["greedy"]))
+    np.testing.assert_array_equal(ids, g["greedy"])
+    m.close()
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_state_after_512_steps(model_dirs, name):
+    g = golden(name)
+    m = pyq35.Model(model_dirs[name], 600)
+    for t in g["long_ids"]:
+        lg, _ = m.step(int(t))
+    assert rel_l2(m.gdn_state(0), g["S512"]) < REL_L2
+    np.testing.assert_array_equal(m.conv_state(0), g["W512"])
+    K, V = m.kv(0, 0, 512)
+    assert rel_l2(K[-8:], g["K512_last"]) < REL_L2
+    assert rel_l2(V[-8:], g["V512_last"]) < REL_L2
+    assert rel_l2(K.sum(axis=(1, 2)), g["K512_sum"]) < REL_L2
+    assert rel_l2(V.sum(axis=(1, 2)), g["V512_sum"]) < REL_L2
+    assert rel_l2(lg, g["logits512"]) < REL_L2
+    assert rel_l2(m.hidden(), g["hidden512"]) < REL_L2
+    m.close()
+
+
+def test_graph_replay_matches_eager(model_dirs):
+    g = golden("tiny_untied")
+    m = pyq35.Model(model_dirs["tiny_untied"], 600)
+    res = []
+    for graph in (False, True, True):
+        m.set_graph(graph)
+        m.reset()
+        res.append(np.stack([m.step(int(t))[0] for t in g["prompt"]]))
+    np.testing.assert_array_equal(res[0], res[1])
+    np.testing.assert_array_equal(res[1], res[2])
+    # the device-side greedy loop (graph replays, no host round trip) = step-by-step argmax
+    m.reset()
+    for t in g["prompt"][:-1]:
+        m.step(int(t))
+    ids = m.decode_greedy(int(g["prompt"][-1]), 16)
+    np.testing.assert_array_equal(ids, g["greedy"])
+    m.close()
+
+
+def test_step_allocates_nothing(model_dirs):
+    m = pyq35.Model(model_dirs["tiny"], 600)
+    before = pyq35.lib.q35_device_alloc_count()
+    for graph in (False, True):
+        m.set_graph(graph)
+        for t in range(20):
+            m.step(t)
+        m.decode_greedy(3, 10)
+    m.reset()
+    assert pyq35.lib.q35_device_alloc_count() == before
+    b = m.budget()
+    assert b["kv_cache_bytes"] == 1 * 2 * 1 * 600 * 256 * 4
+    assert b["gdn_state_bytes"] == 3 * 2 * 128 * 128 * 4
+    m.close()
+
+
+def test_error_paths(model_dirs):
+    m = pyq35.Model(model_dirs["tiny"], 4)
+    with pytest.raises(pyq35.Q35Error) as e:
+        m.step(1024)
+    assert e.value.status == -6
+    with pytest.raises(pyq35.Q35Error):
+        m.step(-1)
+    for t in range(4):
+        m.step(t)
+    with pytest.raises(pyq35.Q35Error) as e:
+        m.step(0)
+    assert e.value.status == -6 and m.position == 4
+    with pytest.raises(pyq35.Q35Error):
+        m.decode_greedy(0, 1)
+    m.reset()
+    assert m.position == 0
+    m.step(0)
+    m.close()
+
+
+def test_state_import_then_step_matches_oracle(model_dirs):
+    """Write a random state in the reference layouts, step once on both sides."""
+    rng = np.random.default_rng(3)
+    d = pyq35.dims_for("tiny")
+    m = pyq35.Model(model_dirs["tiny"], 64)
+    o = op.Oracle(model_dirs["tiny"], 64)
+    pos = 9
+    m.set_position(pos)
+    o.set_position(pos)
+    conv = 2 * d.gdn_k_heads * 128 + d.gdn_v_heads * 128
+    for l in range(d.n_layers_gdn):
+        S = (0.1 * rng.standard_normal((d.gdn_v_heads, 128, 128))).astype(np.float32)
+        W = rng.standard_normal((conv, 3)).astype(np.float32)
+        m.set_gdn_state(l, S)
+        m.set_conv_state(l, W)
+        np.testing.assert_array_equal(m.gdn_state(l), S)
+        np.testing.assert_array_equal(m.conv_state(l), W)
+        o.gdn_state(l)[:] = S
+        o.conv_state(l)[:] = W
+    K = rng.standard_normal((pos, d.attn_kv_heads, 256)).astype(np.float32)
+    V = rng.standard_normal((pos, d.attn_kv_heads, 256)).astype(np.float32)
+    m.set_kv(0, 0, K, V)
+    Kb, Vb = m.kv(0, 0, pos)
+    np.testing.assert_array_equal(Kb, K)
+    np.testing.assert_array_equal(Vb, V)
+    o.kcache(0)[:pos] = K
+    o.vcache(0)[:pos] = V
+    lg, _ = m.step(5)
+    ref = o.step(5)
+    assert rel_l2(lg, ref) < REL_L2
+    assert rel_l2(m.gdn_state(0), o.gdn_state(0)) < REL_L2
+    np.testing.assert_array_equal(m.conv_state(0), o.conv_state(0))
+    m.close()
+
+
+def test_fill_synthetic(model_dirs):
+    m = pyq35.Model(model_dirs["tiny"], 4096)
+    m.fill_synthetic(4000, seed=11, state_std=0.1)
+    assert m.position == 4000
+    K, V = m.kv(0, 0, 4000)
+    assert abs(K.mean()) < 0.01 and abs(K.std() - 1) < 0.01 and abs(V.std() - 1) < 0.01
+    assert not np.array_equal(K, V)
+    S = m.gdn_state(1)
+    assert abs(S.std() - 0.1) < 0.002
+    assert (m.conv_state(2) == 0).all()
+    m.step(1)
+    assert m.position == 4001
+    m.close()
+
+
+def test_prefill_logits_match_reference(model_dirs):
+    g = golden("tiny")
+    m = pyq35.Model(model_dirs["tiny"], 600)
+    lg = m.prefill(g["prompt"])
+    assert rel_l2(lg, g["prefill_logits"]) < REL_L2
+    assert m.position == len(g["prompt"])
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def c1_dir():
+    d = pyq35.dims_for("0.8b")
+    root = tempfile.mkdtemp(prefix="q35_c1_")
+    path = os.path.join(root, "m")
+    pyq35.synth_write_model(path, d, seed=0, std=0.02, threads=16)
+    yield path
+    for f in os.listdir(path):
+        os.remove(os.path.join(path, f))
+    os.rmdir(path)
+    os.rmdir(root)
+
+
+def test_c1_08b_greedy_decode(c1_dir):
+    """0.8B-shaped model, 32-token prompt (seed 1), 128 greedy steps: token-exact against
+    the reference; residual stream after every layer and the top logits at three positions."""
+    g = golden("c1_08b")
+    assert sha256(os.path.join(c1_dir, "model.safetensors")) == str(g["sha256"])
+    prompt, greedy = g["prompt"], g["greedy"]
+    m = pyq35.Model(c1_dir, len(prompt) + len(greedy) + 2)
+    ids = m.generate_greedy(prompt, len(greedy))
+    np.testing.assert_array_equal(ids, greedy)
+    seq = np.concatenate([prompt, greedy[:-1]])
+    record = list(g["record"])
+    m.reset()
+    m.set_layer_trace(True)
+    worst = 0.0
+    for t, tok in enumerate(seq):
+        lg, _ = m.step(int(tok), want_logits=t in record)
+        if t in record:
+            i = record.index(t)
+            tr = m.layer_trace()
+            for l in range(tr.shape[0]):
+                e = rel_l2(tr[l], g["trace"][i, l])
+                worst = max(worst, e)
+                assert e < REL_L2, f"position {t} layer {l}: {e}"
+            np.testing.assert_array_equal(np.argsort(-lg, kind="stable")[:4], g["top_idx"][i][:4])
+            np.testing.assert_allclose(lg[g["top_idx"][i]], g["top_val"][i], rtol=1e-4, atol=1e-4)
+    print(f"0.8b worst per-layer rel_l2 {worst:.3g}")
+    m.close()
