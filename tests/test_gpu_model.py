@@ -50,7 +50,8 @@ def test_state_after_512_steps(model_dirs, name):
     for t in g["long_ids"]:
         lg, _ = m.step(int(t))
     assert rel_l2(m.gdn_state(0), g["S512"]) < REL_L2
-    np.testing.assert_array_equal(m.conv_state(0), g["W512"])
+    # the window holds in_proj_qkv outputs of the last three tokens (fp32 matvec results)
+    assert rel_l2(m.conv_state(0), g["W512"]) < REL_L2
     K, V = m.kv(0, 0, 512)
     assert rel_l2(K[-8:], g["K512_last"]) < REL_L2
     assert rel_l2(V[-8:], g["V512_last"]) < REL_L2
@@ -147,7 +148,11 @@ def test_state_import_then_step_matches_oracle(model_dirs):
     ref = o.step(5)
     assert rel_l2(lg, ref) < REL_L2
     assert rel_l2(m.gdn_state(0), o.gdn_state(0)) < REL_L2
-    np.testing.assert_array_equal(m.conv_state(0), o.conv_state(0))
+    # the window shifted by one: the two older inputs were imported, the newest is the
+    # in_proj_qkv output of this step
+    win = m.conv_state(0)
+    np.testing.assert_array_equal(win[:, :2], o.conv_state(0)[:, :2])
+    assert rel_l2(win[:, 2], o.conv_state(0)[:, 2]) < REL_L2
     m.close()
 
 
