@@ -149,7 +149,7 @@ def main() -> None:
     attn_avg_s = attn_ms / 1e3 / attn_n
     attn_bytes = 2 * NKV * HD * 4 * mean_n + NQ * HD * 4  # K and V rows + the queries
     attn_gbs = attn_bytes / attn_avg_s / 1e9
-    mixer_ms = sum(kt[k][0] for k in ("attn_prep", "attn_decode", "attn_combine"))
+    mixer_ms = sum(kt[k][0] for k in ("attn_decode", "attn_combine"))
     mixer_bytes = 4096 * mean_n + 59_392  # per layer incl. projection outputs, append, output
     mixer_gbs = mixer_bytes * attn_n / (mixer_ms / 1e3) / 1e9
     gdn_ms, gdn_n = kt["gdn_decode"]

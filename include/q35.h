@@ -176,14 +176,16 @@ q35_status q35_model_read_hidden(q35_model *m, float *host);
  * the model stream around each launch; graph replay is bypassed while it is on). */
 #define Q35_KT_GEMV 0
 #define Q35_KT_GDN_DECODE 1
-#define Q35_KT_ATTN_DECODE 2   /* split-K partial kernel */
+#define Q35_KT_ATTN_DECODE 2   /* split-K kernel (q/k norm + RoPE + KV append folded in) */
 #define Q35_KT_ATTN_COMBINE 3
-#define Q35_KT_ATTN_PREP 4     /* q/k norm + RoPE + KV append */
-#define Q35_KT_OTHER 5
-#define Q35_KT_COUNT 6
+#define Q35_KT_OTHER 4
+#define Q35_KT_COUNT 5
 q35_status q35_model_set_kernel_timing(q35_model *m, int32_t enable);
 /* ms[Q35_KT_COUNT] total milliseconds, launches[Q35_KT_COUNT]; resets the counters. */
 q35_status q35_model_kernel_times(q35_model *m, double *ms, int64_t *launches);
+/* KV splits per kv head of the attention decode kernel (0 = the default for max_context);
+ * at most 1024. A tuning knob: results are the same for every value. */
+q35_status q35_model_set_attn_splits(q35_model *m, int32_t n_splits);
 
 /* State access, in the reference layouts (src/qwen_model.cpp:50-61):
  * GDN state [VH][DK][DV], conv window [CONV][KER-1] oldest first, K/V rows [n][NKV][HD]. */

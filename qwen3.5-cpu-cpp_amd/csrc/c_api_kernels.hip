@@ -95,13 +95,9 @@ q35_status q35_gdn_decode(const q35_gdn_decode_args* args, q35_stream s) {
 
 uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args* args) {
     if (!args || args->kv_heads <= 0 || args->q_heads <= 0) return 0;
-    int splits = args->n_splits;
-    if (splits <= 0) {
-        const int64_t want = (args->max_context + q35k::kAttnChunk - 1) / q35k::kAttnChunk;
-        splits = static_cast<int>(want < 1 ? 1 : want > 1024 ? 1024 : want);
-    }
-    const uint64_t qw = (static_cast<uint64_t>(args->q_heads) * args->head_dim * 4 + 255) & ~255ULL;
-    return qw + static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
+    const int splits = args->n_splits > 0 ? args->n_splits
+                                          : q35k::attn_default_splits(args->max_context, args->kv_heads, q35k::device_cu_count());
+    return static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
 }
 
 q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
@@ -126,11 +122,7 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
         return q35::fail(Q35_ERR_ARG, "q35_attn_decode: workspace of %llu bytes, needs %llu",
                          static_cast<unsigned long long>(g.workspace_bytes),
                          static_cast<unsigned long long>(q35_attn_decode_workspace_bytes(args)));
-    int splits = g.n_splits;
-    if (splits <= 0) {
-        const int64_t want = (g.max_context + q35k::kAttnChunk - 1) / q35k::kAttnChunk;
-        splits = static_cast<int>(want < 1 ? 1 : want > 1024 ? 1024 : want);
-    }
+    const int splits = g.n_splits > 0 ? g.n_splits : q35k::attn_default_splits(g.max_context, g.kv_heads, q35k::device_cu_count());
     q35k::AttnDecodeArgs a{};
     a.NQ = g.q_heads;
     a.NKV = g.kv_heads;
@@ -149,14 +141,10 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
     a.k_cache = g.k_cache;
     a.v_cache = g.v_cache;
     a.out = g.out;
-    const uint64_t qw = (static_cast<uint64_t>(g.q_heads) * 256 * 4 + 255) & ~255ULL;
-    a.q_work = static_cast<float*>(g.workspace);
-    a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(g.workspace) + qw);
+    a.part_o = static_cast<float*>(g.workspace);
     a.part_ml = a.part_o + static_cast<int64_t>(g.kv_heads) * splits * grp * 256;
     hipStream_t st = as_stream(s);
-    q35_status r = launched(q35k::launch_attn_prep(a, st), "attn prep");
-    if (r != Q35_OK) return r;
-    r = launched(q35k::launch_attn_partial(a, st), "attn partial");
+    const q35_status r = launched(q35k::launch_attn_partial(a, st), "attn partial");
     if (r != Q35_OK) return r;
     return launched(q35k::launch_attn_combine(a, st), "attn combine");
 }

@@ -1,25 +1,24 @@
 // Gated GQA attention decode over the fp32 KV cache (QwenModel::attn_step after its
-// projections, src/qwen_model.cpp:119-150), in three launches:
+// projections, src/qwen_model.cpp:119-150), in two launches:
 //
-//   prep     q_norm + RoPE of every query head, k_norm + RoPE of the new key, K/V append
-//            at `pos` (rmsnorm (1+w) with the sum of squares in double; RoPE angles in
-//            double, src/forward_pass.cpp:77-84,102-112).
-//   partial  split-K over the cache: grid (n_splits, NKV). A workgroup owns a contiguous
-//            range of positions of one kv head and serves all GRP = NQ/NKV query heads of
-//            that group, so each K/V row is read from HBM once per token (the reference
-//            re-reads it for every query head). The range is walked in sub-chunks of 32
-//            positions; for each sub-chunk every K and V row load is issued up front
-//            (16 float4 per lane), then the scores, a running-max softmax update and the
-//            P.V accumulation run from registers. Writes the unnormalised partial output
-//            and (max, sum) per query head.
-//   combine  per query head: merge the splits with the usual max-rescaled sum, divide,
-//            multiply by sigmoid(gate).
-//
-// Scores use LPP lanes per position (16 for GRP <= 4, 32 above), each lane holding
-// 256/LPP dims of the query vectors; the GRP partial dots are reduced over the LPP lanes
-// with a butterfly that halves the set of values carried at each exchange, ending with
-// each lane owning the full dot of one query head. P.V uses 4 dims per lane over all 64
-// lanes with the softmax weights broadcast from LDS.
+//   partial  split-K over the cache, grid (n_splits, NKV), 8 waves per workgroup. A
+//            workgroup owns a contiguous range of positions of one kv head and serves all
+//            GRP = NQ/NKV query heads of the group, so each K/V row is read from HBM once per
+//            token (the reference re-reads it for every query head). Prologue: rmsnorm (1+w)
+//            + RoPE of its GRP query rows (sum of squares and rotation angles in double,
+//            src/forward_pass.cpp:77-84,102-112); the workgroup holding position `pos` also
+//            norms + rotates the new key and appends the K/V rows. Each wave then walks its
+//            own sub-range in batches with no block barrier: the next batch's K and V rows
+//            are requested before the current one is consumed (register double buffer), the
+//            scores use LPP lanes per position (16 for GRP <= 4, 32 above) with the GRP partial
+//            dots reduced by a butterfly that halves the carried set at each exchange, the
+//            running max and sum of each head live in the lanes that own that head, and P.V
+//            (4 dims per lane) takes each softmax weight as a scalar operand read from its
+//            lane. The waves are merged once at the end (max-rescaled, fixed order).
+//            Output: unnormalised partial output and (max, sum) per query head and split.
+//   combine  grid (NQ, HD/64): merges the splits with max-rescaled sums (the splits are
+//            shared over the 4 waves, one dim per lane), divides, multiplies by
+//            sigmoid(gate).
 #include <math.h>
 
 #include "dev_common.hpp"
@@ -29,57 +28,12 @@ namespace q35k {
 namespace {
 
 constexpr int kHD = 256;
-constexpr int kChunk = kAttnChunk;
 
 __device__ __forceinline__ int read_pos(const AttnDecodeArgs& a) {
     return a.pos_dev ? *a.pos_dev : a.pos_val;
 }
 
-// Positions per split: ceil(n / n_splits) rounded up to whole sub-chunks.
-__device__ __forceinline__ int split_len(int n, int n_splits) {
-    const int per = (n + n_splits - 1) / n_splits;
-    return ((per + kChunk - 1) / kChunk) * kChunk;
-}
-
-__global__ __launch_bounds__(256) void attn_prep_kernel(AttnDecodeArgs a) {
-    const int b = blockIdx.x, t = threadIdx.x;
-    const int pos = read_pos(a);
-    __shared__ float buf[kHD];
-    __shared__ double red[4];
-    const float* src;
-    const float* w;
-    float* dst;
-    int kh = -1;
-    if (b < a.NQ) {
-        src = a.qg + static_cast<int64_t>(b) * 2 * kHD;
-        w = a.q_norm;
-        dst = a.q_work + static_cast<int64_t>(b) * kHD;
-    } else {
-        kh = b - a.NQ;
-        src = a.k_new + static_cast<int64_t>(kh) * kHD;
-        w = a.k_norm;
-        dst = a.k_cache + (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD;
-    }
-    const float x = src[t];
-    const double ss = block_sum(static_cast<double>(x) * x, red);
-    const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + a.eps);
-    float y = x * inv * (1.0f + w[t]);
-    buf[t] = y;
-    __syncthreads();
-    const int half = a.ROT / 2;
-    if (t < a.ROT) {
-        const int i = t < half ? t : t - half;
-        const double inv_freq = pow(a.theta, -static_cast<double>(2 * i) / a.ROT);
-        const double ang = static_cast<double>(pos) * inv_freq;
-        const float c = static_cast<float>(cos(ang)), s = static_cast<float>(sin(ang));
-        const float x1 = buf[i], x2 = buf[i + half];
-        y = t < half ? x1 * c - x2 * s : x2 * c + x1 * s;
-    }
-    dst[t] = y;
-    if (kh >= 0)
-        a.v_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + t] =
-            a.v_new[static_cast<int64_t>(kh) * kHD + t];
-}
+__device__ __forceinline__ int split_len(int n, int n_splits) { return (n + n_splits - 1) / n_splits; }
 
 // Reduce GRP per-lane partial sums over groups of LPP lanes. On return lane l holds in v[0]
 // the full sum of query head `head`.
@@ -108,66 +62,130 @@ __device__ __forceinline__ void butterfly(float (&v)[GRP], int lane, int& head) 
     }
 }
 
+constexpr int kWaves = 8;   // waves per workgroup
+
+// lane holding the full score of query head h (for lane group `sub`) after the butterfly
 template <int GRP, int LPP>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnDecodeArgs a) {
-    constexpr int NF4 = 64 / LPP;            // float4 of one row per lane in the score phase
-    constexpr int PPW = 64 / LPP;            // positions per wave per score pass
-    constexpr int QIT = kChunk / (4 * PPW);  // score passes per sub-chunk
-    constexpr int VIT = kChunk / 4;          // P.V rows per wave per sub-chunk
-    constexpr int OWN = LPP / GRP;           // lanes sharing one head after the butterfly
+__device__ __forceinline__ constexpr int head_lane(int sub, int h) { return sub * LPP + h * (LPP / GRP); }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+template <int GRP, int LPP, int kBatch, bool DBUF>
+__global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
+    constexpr int NF4 = 64 / LPP;   // float4 of one K row per lane in the score layout
+    constexpr int PPW = 64 / LPP;   // positions per score pass (one per lane group)
+    constexpr int QIT = kBatch / PPW;
+    constexpr int OWN = LPP / GRP;  // lanes sharing one head after the butterfly
+    constexpr int NROW = GRP + 1;   // normed rows: GRP queries (+ the new key)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x, kh = blockIdx.y;
-    const int n = read_pos(a) + 1;
+    const int pos = read_pos(a);
+    const int n = pos + 1;
     const int per = split_len(n, a.n_splits);
     const int j0 = split * per;
     if (j0 >= n) return;
     const int j1 = min(n, j0 + per);
+    const bool owns_new = j1 == n;  // this split holds position pos
+    // each wave walks its own contiguous sub-range [w0, w1)
+    const int wpe = (j1 - j0 + kWaves - 1) / kWaves;
+    const int w0 = j0 + wave * wpe, w1 = min(j1, w0 + wpe);
 
     const float* K = a.k_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
     const float* V = a.v_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
-    const float* Q = a.q_work + static_cast<int64_t>(kh) * GRP * kHD;
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
-    __shared__ float s_l[kChunk][GRP];
-    __shared__ float m_s[GRP], l_s[GRP], f_s[GRP];
+    __shared__ float rows_s[NROW][kHD];  // normed + rotated q rows, then the new key
+    __shared__ float vnew_s[kHD];
+    __shared__ float cs_s[2][kHD / 2];   // RoPE cos / sin of this position
+    __shared__ float ml_s[kWaves][GRP][2];
     __shared__ float red[GRP][kHD];
 
     const int pl = lane % LPP, sub = lane / LPP;
+    float4 kA[QIT][NF4], vA[kBatch];
+    float4 kB[DBUF ? QIT : 1][NF4], vB[DBUF ? kBatch : 1];
+    auto load = [&](float4 (&kr)[QIT][NF4], float4 (&vr)[kBatch], int b0) {
+#pragma unroll
+        for (int it = 0; it < QIT; ++it) {
+            const int row = min(b0 + it * PPW + sub, w1 - 1);
+            const float* src = K + static_cast<int64_t>(row) * kHD + pl * 4;
+#pragma unroll
+            for (int m = 0; m < NF4; ++m) kr[it][m] = *reinterpret_cast<const float4*>(src + m * LPP * 4);
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int row = min(b0 + j, w1 - 1);
+            vr[j] = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(row) * kHD + lane * 4);
+        }
+    };
+    if (w0 < w1) load(kA, vA, w0);  // first batch in flight during the prologue
+
+    // ---- prologue: q_norm + RoPE of the GRP query rows (and k_norm + RoPE of the new key)
+    const int half = a.ROT / 2;
+    if (tid < half) {
+        const double inv_freq = pow(a.theta, -static_cast<double>(2 * tid) / a.ROT);
+        const double ang = static_cast<double>(pos) * inv_freq;
+        cs_s[0][tid] = static_cast<float>(cos(ang));
+        cs_s[1][tid] = static_cast<float>(sin(ang));
+    }
+    const int nrow = owns_new ? NROW : GRP;
+    for (int r = wave; r < nrow; r += kWaves) {
+        const bool is_q = r < GRP;
+        const float* src = is_q ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
+                                : a.k_new + static_cast<int64_t>(kh) * kHD;
+        const float* w = is_q ? a.q_norm : a.k_norm;
+        const float4 x = *reinterpret_cast<const float4*>(src + lane * 4);
+        double ss = static_cast<double>(x.x) * x.x + static_cast<double>(x.y) * x.y +
+                    static_cast<double>(x.z) * x.z + static_cast<double>(x.w) * x.w;
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + a.eps);
+        const float4 wv = *reinterpret_cast<const float4*>(w + lane * 4);
+        float4 y;
+        y.x = x.x * inv * (1.0f + wv.x);
+        y.y = x.y * inv * (1.0f + wv.y);
+        y.z = x.z * inv * (1.0f + wv.z);
+        y.w = x.w * inv * (1.0f + wv.w);
+        *reinterpret_cast<float4*>(&rows_s[r][lane * 4]) = y;
+    }
+    if (owns_new && tid < kHD / 4)
+        *reinterpret_cast<float4*>(&vnew_s[tid * 4]) =
+            *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + tid * 4);
+    __syncthreads();
+    for (int t = tid; t < nrow * half; t += kWaves * 64) {
+        const int r = t / half, i = t - r * half;
+        const float c = cs_s[0][i], s = cs_s[1][i];
+        const float x1 = rows_s[r][i], x2 = rows_s[r][i + half];
+        rows_s[r][i] = x1 * c - x2 * s;
+        rows_s[r][i + half] = x2 * c + x1 * s;
+    }
+    __syncthreads();
+    if (owns_new && tid < kHD) {  // append the new K / V rows
+        a.k_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + tid] = rows_s[GRP][tid];
+        a.v_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + tid] = vnew_s[tid];
+    }
+
     float4 qr[GRP][NF4];
 #pragma unroll
     for (int h = 0; h < GRP; ++h)
 #pragma unroll
-        for (int m = 0; m < NF4; ++m)
-            qr[h][m] = *reinterpret_cast<const float4*>(Q + h * kHD + pl * 4 + m * LPP * 4);
-    if (tid < GRP) {
-        m_s[tid] = -INFINITY;
-        l_s[tid] = 0.0f;
-    }
+        for (int m = 0; m < NF4; ++m) qr[h][m] = *reinterpret_cast<const float4*>(&rows_s[h][pl * 4 + m * LPP * 4]);
     float4 acc[GRP];
 #pragma unroll
     for (int h = 0; h < GRP; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    float m_run = -INFINITY, l_run = 0.0f;  // running max / sum of this lane's head
 
-    for (int c0 = j0; c0 < j1; c0 += kChunk) {
-        const int cn = min(kChunk, j1 - c0);
-        float4 kr[QIT][NF4];
-        float4 vr[VIT];
+    // one batch of kBatch positions starting at b0, from registers kr / vr
+    auto consume = [&](float4 (&kr)[QIT][NF4], float4 (&vr)[kBatch], int b0) {
+        float s[QIT];
 #pragma unroll
         for (int it = 0; it < QIT; ++it) {
-            const int jl = it * 4 * PPW + wave * PPW + sub;
-            const float* row = K + static_cast<int64_t>(c0 + min(jl, cn - 1)) * kHD + pl * 4;
+            const int p = b0 + it * PPW + sub;
+            if (owns_new && min(p, w1 - 1) == pos)  // loaded before this workgroup appended it
 #pragma unroll
-            for (int m = 0; m < NF4; ++m) kr[it][m] = *reinterpret_cast<const float4*>(row + m * LPP * 4);
-        }
-#pragma unroll
-        for (int it = 0; it < VIT; ++it) {
-            const int jl = it * 4 + wave;
-            vr[it] = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(c0 + min(jl, cn - 1)) * kHD + lane * 4);
-        }
-        // scores
-#pragma unroll
-        for (int it = 0; it < QIT; ++it) {
-            const int jl = it * 4 * PPW + wave * PPW + sub;
-            float p[GRP];
+                for (int m = 0; m < NF4; ++m)
+                    kr[it][m] = *reinterpret_cast<const float4*>(&rows_s[GRP][pl * 4 + m * LPP * 4]);
+            float d[GRP];
 #pragma unroll
             for (int h = 0; h < GRP; ++h) {
                 float t = 0.0f;
@@ -178,54 +196,85 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnDecodeArgs a) {
                     t = fmaf(qr[h][m].z, kr[it][m].z, t);
                     t = fmaf(qr[h][m].w, kr[it][m].w, t);
                 }
-                p[h] = t;
+                d[h] = t;
             }
             int head;
-            butterfly<GRP, LPP>(p, lane, head);
-            if ((pl % OWN) == 0) s_l[jl][head] = jl < cn ? p[0] * sc : -INFINITY;
+            butterfly<GRP, LPP>(d, lane, head);
+            s[it] = p < w1 ? d[0] * sc : -INFINITY;
         }
-        __syncthreads();
-        // running-max softmax update, one wave per query head
-        for (int h = wave; h < GRP; h += 4) {
-            const float v = lane < kChunk ? s_l[lane][h] : -INFINITY;
-            const float cmax = wave_max(v);
-            const float m_old = m_s[h];
-            const float m_new = fmaxf(m_old, cmax);
-            const float e = (lane < kChunk && lane < cn) ? expf(v - m_new) : 0.0f;
-            if (lane < kChunk) s_l[lane][h] = e;
-            const float es = wave_sum(e);
-            if (lane == 0) {
-                const float f = expf(m_old - m_new);
-                f_s[h] = f;
-                m_s[h] = m_new;
-                l_s[h] = l_s[h] * f + es;
-            }
+        float cmax = s[0];
+#pragma unroll
+        for (int it = 1; it < QIT; ++it) cmax = fmaxf(cmax, s[it]);
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o));
+        const float m_new = fmaxf(m_run, cmax);
+        const float f = expf(m_run - m_new);
+        float e[QIT], es = 0.0f;
+#pragma unroll
+        for (int it = 0; it < QIT; ++it) {
+            e[it] = b0 + it * PPW + sub < w1 ? expf(s[it] - m_new) : 0.0f;
+            es += e[it];
         }
-        __syncthreads();
+#pragma unroll
+        for (int o = LPP; o < 64; o <<= 1) es += __shfl_xor(es, o);
+        l_run = l_run * f + es;
+        m_run = m_new;
 #pragma unroll
         for (int h = 0; h < GRP; ++h) {
-            const float f = f_s[h];
-            acc[h].x *= f;
-            acc[h].y *= f;
-            acc[h].z *= f;
-            acc[h].w *= f;
+            const float fh = readlane_f(f, head_lane<GRP, LPP>(0, h));
+            acc[h].x *= fh;
+            acc[h].y *= fh;
+            acc[h].z *= fh;
+            acc[h].w *= fh;
         }
 #pragma unroll
-        for (int it = 0; it < VIT; ++it) {
-            const int jl = it * 4 + wave;
+        for (int j = 0; j < kBatch; ++j) {
+            if (owns_new && min(b0 + j, w1 - 1) == pos) vr[j] = *reinterpret_cast<const float4*>(&vnew_s[lane * 4]);
 #pragma unroll
             for (int h = 0; h < GRP; ++h) {
-                const float e = s_l[jl][h];
-                acc[h].x = fmaf(e, vr[it].x, acc[h].x);
-                acc[h].y = fmaf(e, vr[it].y, acc[h].y);
-                acc[h].z = fmaf(e, vr[it].z, acc[h].z);
-                acc[h].w = fmaf(e, vr[it].w, acc[h].w);
+                const float ev = readlane_f(e[j / PPW], head_lane<GRP, LPP>(j % PPW, h));
+                acc[h].x = fmaf(ev, vr[j].x, acc[h].x);
+                acc[h].y = fmaf(ev, vr[j].y, acc[h].y);
+                acc[h].z = fmaf(ev, vr[j].z, acc[h].z);
+                acc[h].w = fmaf(ev, vr[j].w, acc[h].w);
             }
         }
-        __syncthreads();
+    };
+
+    if constexpr (DBUF) {
+        for (int b0 = w0; b0 < w1; b0 += 2 * kBatch) {
+            const int b1 = b0 + kBatch;
+            if (b1 < w1) load(kB, vB, b1);
+            consume(kA, vA, b0);
+            if (b1 >= w1) break;
+            if (b1 + kBatch < w1) load(kA, vA, b1 + kBatch);
+            consume(kB, vB, b1);
+        }
+    } else {
+        for (int b0 = w0; b0 < w1; b0 += kBatch) {
+            if (b0 != w0) load(kA, vA, b0);
+            consume(kA, vA, b0);
+        }
     }
-    // fixed-order cross-wave sum of the P.V accumulators
-    for (int w = 0; w < 4; ++w) {
+
+    // ---- merge the waves: rescale each wave's P.V to the workgroup max, fixed-order sum
+    if (sub == 0 && (pl % OWN) == 0) {
+        ml_s[wave][pl / OWN][0] = m_run;
+        ml_s[wave][pl / OWN][1] = l_run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < GRP; ++h) {
+        float M = ml_s[0][h][0];
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][h][0]);
+        const float mw = ml_s[wave][h][0];
+        const float g = mw == -INFINITY ? 0.0f : expf(mw - M);
+        acc[h].x *= g;
+        acc[h].y *= g;
+        acc[h].z *= g;
+        acc[h].w *= g;
+    }
+    for (int w = 0; w < kWaves; ++w) {
         if (wave == w) {
 #pragma unroll
             for (int h = 0; h < GRP; ++h) {
@@ -245,60 +294,78 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnDecodeArgs a) {
         __syncthreads();
     }
     const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
-#pragma unroll
-    for (int h = 0; h < GRP; ++h) a.part_o[(base + h) * kHD + tid] = red[h][tid];
+    for (int i = tid; i < GRP * kHD; i += kWaves * 64) a.part_o[base * kHD + i] = red[i / kHD][i % kHD];
     if (tid < GRP) {
-        a.part_ml[(base + tid) * 2] = m_s[tid];
-        a.part_ml[(base + tid) * 2 + 1] = l_s[tid];
+        float M = ml_s[0][tid][0];
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][tid][0]);
+        float L = 0.0f;
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = ml_s[w][tid][0];
+            if (mw != -INFINITY) L += ml_s[w][tid][1] * expf(mw - M);
+        }
+        a.part_ml[(base + tid) * 2] = M;
+        a.part_ml[(base + tid) * 2 + 1] = L;
     }
 }
 
+// grid (NQ, HD / 64), 256 threads: wave w merges splits w, w+4, ... for 64 dims (one per lane)
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
-    const int h = blockIdx.x, t = threadIdx.x;
+    const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = blockIdx.y * 64 + lane;
     const int grp = a.NQ / a.NKV, kh = h / grp, g = h - kh * grp;
     const int n = read_pos(a) + 1;
     const int per = split_len(n, a.n_splits);
     const int nact = (n + per - 1) / per;
-    extern __shared__ float w_s[];
-    __shared__ float redf[4];
     const int64_t base = static_cast<int64_t>(kh) * a.n_splits * grp + g;
+    __shared__ float o_s[4][64], l_s[4];
     float mx = -INFINITY;
-    for (int s = t; s < nact; s += 256) mx = fmaxf(mx, a.part_ml[(base + static_cast<int64_t>(s) * grp) * 2]);
-    mx = wave_max(mx);
-    if ((t & 63) == 0) redf[t >> 6] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-    __syncthreads();
-    for (int s = t; s < nact; s += 256) {
-        const float* ml = a.part_ml + (base + static_cast<int64_t>(s) * grp) * 2;
-        const float w = expf(ml[0] - M);
-        w_s[s] = w;
-        w_s[a.n_splits + s] = ml[1] * w;
-    }
-    __syncthreads();
+    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, a.part_ml[(base + static_cast<int64_t>(s) * grp) * 2]);
+    const float M = wave_max(mx);
     float L = 0.0f, o = 0.0f;
-    for (int s = 0; s < nact; ++s) {
-        L += w_s[a.n_splits + s];
-        o = fmaf(a.part_o[(base + static_cast<int64_t>(s) * grp) * kHD + t], w_s[s], o);
+    int s = wave;
+    for (; s + 12 < nact; s += 16) {
+        float mv[4], lv[4], ov[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = base + static_cast<int64_t>(s + 4 * u) * grp;
+            mv[u] = a.part_ml[i * 2];
+            lv[u] = a.part_ml[i * 2 + 1];
+            ov[u] = a.part_o[i * kHD + d];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float w = expf(mv[u] - M);
+            L = fmaf(lv[u], w, L);
+            o = fmaf(ov[u], w, o);
+        }
     }
-    const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + t];
-    a.out[static_cast<int64_t>(h) * kHD + t] = (o / L) * sigmoid_f(gate);
+    for (; s < nact; s += 4) {
+        const int64_t i = base + static_cast<int64_t>(s) * grp;
+        const float w = expf(a.part_ml[i * 2] - M);
+        L = fmaf(a.part_ml[i * 2 + 1], w, L);
+        o = fmaf(a.part_o[i * kHD + d], w, o);
+    }
+    o_s[wave][lane] = o;
+    if (lane == 0) l_s[wave] = L;
+    __syncthreads();
+    if (wave == 0) {
+        const float Lt = (l_s[0] + l_s[1]) + (l_s[2] + l_s[3]);
+        const float ot = (o_s[0][lane] + o_s[1][lane]) + (o_s[2][lane] + o_s[3][lane]);
+        const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + d];
+        a.out[static_cast<int64_t>(h) * kHD + d] = (ot / Lt) * sigmoid_f(gate);
+    }
 }
 
 template <int GRP>
 hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
     constexpr int LPP = GRP <= 4 ? 16 : 32;
     dim3 grid(a.n_splits, a.NKV);
-    attn_partial_kernel<GRP, LPP><<<grid, 256, 0, s>>>(a);
+    constexpr int BATCH = GRP <= 4 ? 8 : GRP == 8 ? 4 : 2;
+    attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8)><<<grid, kWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
 }  // namespace
-
-hipError_t launch_attn_prep(const AttnDecodeArgs& a, hipStream_t s) {
-    attn_prep_kernel<<<a.NQ + a.NKV, kHD, 0, s>>>(a);
-    return hipGetLastError();
-}
 
 hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s) {
     switch (a.NQ / a.NKV) {
@@ -311,9 +378,17 @@ hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s) {
     }
 }
 
+int device_cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s) {
-    const size_t lds = static_cast<size_t>(a.n_splits) * 2 * sizeof(float);
-    attn_combine_kernel<<<a.NQ, kHD, lds, s>>>(a);
+    dim3 grid(a.NQ, kHD / 64);
+    attn_combine_kernel<<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -3,6 +3,7 @@
 // Shapes are checked by the callers (c_api_kernels.hip, runtime.hip) before launching.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 namespace q35k {
@@ -55,20 +56,27 @@ struct AttnDecodeArgs {
     float eps;
     const float *qg, *k_new, *v_new, *q_norm, *k_norm;
     float *k_cache, *v_cache;   // [NKV][max_ctx][HD]
-    float* q_work;              // [NQ][HD] normed + rotated queries
     float* part_o;              // [NKV][n_splits][GRP][HD]
     float* part_ml;             // [NKV][n_splits][GRP][2]
     float* out;                 // [NQ][HD]
 };
-constexpr int kAttnChunk = 32;  // positions per sub-chunk of a split
-hipError_t launch_attn_prep(const AttnDecodeArgs& a, hipStream_t s);
+// split-K partials, with the q/k norm + RoPE + K/V append of position pos folded in
 hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s);
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s);
-// workspace floats for part_o + part_ml (q_work excluded)
+// workspace floats for part_o + part_ml
 inline int64_t attn_partial_floats(int NQ, int NKV, int HD, int n_splits) {
     const int grp = NQ / NKV;
     return static_cast<int64_t>(NKV) * n_splits * grp * (HD + 2);
 }
+// Default splits per kv head: one 8-wave workgroup per CU over all kv heads, and no split
+// shorter than 64 positions at full context.
+inline int attn_default_splits(int64_t max_ctx, int NKV, int n_cu) {
+    const int64_t want = (max_ctx + 63) / 64;
+    const int64_t cap = std::max<int64_t>(1, n_cu / std::max(1, NKV));
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(want, cap)));
+}
+// Compute units of the current device (256 on MI355X when the query fails).
+int device_cu_count();
 
 // ---------------------------------------------------------------- small kernels
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,

@@ -47,6 +47,9 @@ hipError_t dev_alloc(void** p, size_t bytes) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// split-K workspace is sized for this many splits per kv head
+constexpr int kMaxSplits = 1024;
+
 struct LayerDev {
     bool attn = false;
     int idx = 0;
@@ -89,11 +92,12 @@ struct q35_model {
     float* gdn_state = nullptr;  // inside state_arena
     float* conv_ring = nullptr;
 
-    float *hidden = nullptr, *proj = nullptr, *mix = nullptr, *gu = nullptr, *qwork = nullptr;
+    float *hidden = nullptr, *proj = nullptr, *mix = nullptr, *gu = nullptr;
     float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr, *trace = nullptr;
     void* argmax_part = nullptr;
     int *token_dev = nullptr, *pos_dev = nullptr, *ids_dev = nullptr;
     int n_splits = 0;
+    int n_cu = 256;
 
     int64_t pos = 0;  // host mirror of *pos_dev
     int32_t* pinned_token = nullptr;
@@ -332,11 +336,9 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
             aa.k_norm = ly.k_norm;
             aa.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
             aa.v_cache = aa.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
-            aa.q_work = m->qwork;
             aa.part_o = m->part_o;
             aa.part_ml = m->part_ml;
             aa.out = m->mix;
-            L.run(Q35_KT_ATTN_PREP, [&] { return q35k::launch_attn_prep(aa, s); });
             L.run(Q35_KT_ATTN_DECODE, [&] { return q35k::launch_attn_partial(aa, s); });
             L.run(Q35_KT_ATTN_COMBINE, [&] { return q35k::launch_attn_combine(aa, s); });
             q35k::GemvArgs o{};
@@ -562,7 +564,8 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     const size_t ring_bytes = static_cast<size_t>(d.n_layers_gdn) * 4 * CONV * 4;
     m->state_bytes = align256(gdn_bytes) + align256(ring_bytes);
     m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * static_cast<size_t>(max_ctx) * HD * 4;
-    m->n_splits = static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(1, (max_ctx + q35k::kAttnChunk - 1) / q35k::kAttnChunk)));
+    m->n_cu = q35k::device_cu_count();
+    m->n_splits = q35k::attn_default_splits(max_ctx, NKV, m->n_cu);
     const int64_t proj_n = std::max<int64_t>(static_cast<int64_t>(CONV) + VD + 2 * VH, 2LL * NQ * HD + 2LL * NKV * HD);
     size_t sc = 0;
     auto take = [&](size_t bytes) {
@@ -574,8 +577,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     const size_t o_proj = take(static_cast<size_t>(proj_n) * 4);
     const size_t o_mix = take(static_cast<size_t>(std::max(VD, NQ * HD)) * 4);
     const size_t o_gu = take(static_cast<size_t>(2) * I * 4);
-    const size_t o_qwork = take(static_cast<size_t>(NQ) * HD * 4);
-    const int64_t pf = q35k::attn_partial_floats(NQ, NKV, HD, m->n_splits);
+    const int64_t pf = q35k::attn_partial_floats(NQ, NKV, HD, kMaxSplits);
     const size_t o_part = take(static_cast<size_t>(pf) * 4);
     const size_t o_logits = take(static_cast<size_t>(d.vocab_size) * 4);
     const size_t o_trace = take(static_cast<size_t>(d.n_layers_total) * H * 4);
@@ -585,7 +587,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->scratch_bytes = sc;
     m->w_bytes = plan.bytes();
 
-    std::cout << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
+    std::cerr << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
               << " MiB, state " << (m->state_bytes >> 10) << " KiB, kv " << (m->kv_bytes >> 20)
               << " MiB, scratch " << (m->scratch_bytes >> 10) << " KiB\n";
 
@@ -655,9 +657,8 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->proj = S32(o_proj);
     m->mix = S32(o_mix);
     m->gu = S32(o_gu);
-    m->qwork = S32(o_qwork);
     m->part_o = S32(o_part);
-    m->part_ml = m->part_o + static_cast<int64_t>(NKV) * m->n_splits * (NQ / NKV) * HD;
+    m->part_ml = m->part_o + static_cast<int64_t>(NKV) * kMaxSplits * (NQ / NKV) * HD;
     m->logits = S32(o_logits);
     m->trace = S32(o_trace);
     m->argmax_part = m->scratch + o_am;
@@ -849,6 +850,15 @@ q35_status q35_model_generate_greedy(q35_model* m, const int32_t* prompt, int32_
 q35_status q35_model_set_graph(q35_model* m, int32_t enable) {
     if (!m) return q35::fail(Q35_ERR_ARG, "null model");
     m->use_graph = enable != 0;
+    return Q35_OK;
+}
+
+q35_status q35_model_set_attn_splits(q35_model* m, int32_t n_splits) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (n_splits < 0 || n_splits > kMaxSplits)
+        return q35::fail(Q35_ERR_RANGE, "n_splits %d outside [0, %d]", n_splits, kMaxSplits);
+    m->n_splits = n_splits > 0 ? n_splits : q35k::attn_default_splits(m->max_ctx, m->d.attn_kv_heads, m->n_cu);
+    drop_graph(m);
     return Q35_OK;
 }
 

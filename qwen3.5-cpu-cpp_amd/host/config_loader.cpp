@@ -107,7 +107,7 @@ bool load_model_config(const std::string& path, ModelConfig& cfg) {
     cfg.n_params = static_cast<int64_t>(cfg.vocab_size) * cfg.hidden_size +
                    static_cast<int64_t>(cfg.n_layers_total) * 12 * cfg.hidden_size * cfg.hidden_size;
 
-    std::cout << "[config] " << path << ": hidden=" << cfg.hidden_size
+    std::cerr << "[config] " << path << ": hidden=" << cfg.hidden_size
               << " layers=" << cfg.n_layers_total << " (" << cfg.n_layers_gdn << " gdn / "
               << cfg.n_layers_attn << " attn) ffn=" << cfg.ffn_intermediate
               << " vocab=" << cfg.vocab_size << " tie=" << cfg.tie_word_embeddings << "\n";

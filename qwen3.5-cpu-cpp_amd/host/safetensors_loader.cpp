@@ -214,7 +214,7 @@ bool SafeTensors::parse_shard(const std::string& path) {
         std::cerr << "[safetensors] header parse error\n";
         return false;
     }
-    std::cout << "[safetensors] shard '" << path << "': " << (size / (1024 * 1024)) << " MB\n";
+    std::cerr << "[safetensors] shard '" << path << "': " << (size / (1024 * 1024)) << " MB\n";
     return true;
 }
 
@@ -236,7 +236,7 @@ bool SafeTensors::load_model(const std::string& model_dir) {
     std::sort(files.begin(), files.end());
     for (const std::string& f : files)
         if (!parse_shard(f)) return false;
-    std::cout << "[safetensors] " << files.size() << " shard(s), " << entries_.size()
+    std::cerr << "[safetensors] " << files.size() << " shard(s), " << entries_.size()
               << " tensors\n";
     return true;
 }

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libq35.so")
 
 Q35_OK = 0
-KT_NAMES = ["gemv", "gdn_decode", "attn_decode", "attn_combine", "attn_prep", "other"]
+KT_NAMES = ["gemv", "gdn_decode", "attn_decode", "attn_combine", "other"]
 
 
 class Q35Error(RuntimeError):
@@ -110,6 +110,7 @@ def _load():
         "q35_model_read_layer_trace": (S, [P, P]),
         "q35_model_read_hidden": (S, [P, P]),
         "q35_model_set_kernel_timing": (S, [P, I32]),
+        "q35_model_set_attn_splits": (S, [P, I32]),
         "q35_model_kernel_times": (S, [P, P, P]),
         "q35_model_read_gdn_state": (S, [P, I32, P]),
         "q35_model_write_gdn_state": (S, [P, I32, P]),
@@ -263,6 +264,9 @@ class Model:
 
     def set_kernel_timing(self, on: bool):
         check(lib.q35_model_set_kernel_timing(self.h, int(on)))
+
+    def set_attn_splits(self, n: int):
+        check(lib.q35_model_set_attn_splits(self.h, n))
 
     def kernel_times(self) -> dict:
         ms = np.zeros(len(KT_NAMES), np.float64)
