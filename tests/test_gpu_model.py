@@ -220,3 +220,19 @@ def test_c1_08b_greedy_decode(c1_dir):
             np.testing.assert_allclose(lg[g["top_idx"][i]], g["top_val"][i], rtol=1e-4, atol=1e-4)
     print(f"0.8b worst per-layer rel_l2 {worst:.3g}")
     m.close()
+
+
+def test_cpp_cli_generate(model_dirs):
+    """The C++ drop-in (SafeTensors + QwenModel, reference CLI flow) through lib/q35_generate."""
+    import subprocess
+
+    import pyq35 as _p
+
+    g = golden("tiny_untied")
+    exe = os.path.join(os.path.dirname(_p.LIB_PATH), "q35_generate")
+    ids = ",".join(str(int(t)) for t in g["prompt"])
+    out = subprocess.run([exe, model_dirs["tiny_untied"], str(len(g["greedy"])), ids], capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 0, out.stderr[-2000:]
+    got = [int(x) for x in out.stdout.strip().split(",")]
+    assert got == g["greedy"].tolist()
