@@ -92,6 +92,162 @@ def cpu_baseline(model_dir: str, dims, ctx: int, n_steps: int) -> dict:
                       f"{ctx + 1}..{ctx + n_steps} (synthetic cache), {dt:.1f} s, OpenMP threads={threads}"}
 
 
+def bench_gdn(a) -> dict:
+    """Isolated GDN decode: 18 layers of 16 x 128 x 128 fp32 state in one launch per token,
+    `steps` sequential tokens (q/k/v/z/a/b drawn N(0,1), A_log and dt_bias N(0,1), state
+    N(0, 0.1)). With --rotate R, R independent state sets are visited round-robin so the
+    working set exceeds the 256 MB Infinity Cache."""
+    import pyq35
+
+    hip = pyq35.Hip()
+    L, KH, VH, D = 18, 16, 16, 128
+    CONV, VD = 2 * KH * D + VH * D, VH * D
+    R = max(1, a.rotate)
+    P = 32  # distinct per-token input sets on the device, cycled
+    rng_seed = 7
+
+    def normal(n, stream, std=1.0):
+        return pyq35.synth_normal(n, rng_seed, stream, std)
+
+    qkv = hip.upload(normal(P * L * CONV, 1))
+    z = hip.upload(normal(P * L * VD, 2))
+    b = hip.upload(normal(P * L * VH, 3))
+    av = hip.upload(normal(P * L * VH, 4))
+    convw = hip.upload(normal(L * CONV * 4, 5, 0.5))
+    alog = hip.upload(normal(L * VH, 6))
+    dtb = hip.upload(normal(L * VH, 7))
+    normw = hip.upload(np.ones(L * D, np.float32))
+    states = [hip.upload(normal(L * VH * D * D, 100 + r, 0.1)) for r in range(R)]
+    rings = [hip.upload(np.zeros(L * 4 * CONV, np.float32)) for r in range(R)]
+    out = hip.malloc(L * VD * 4)
+    res = {}
+    for fused in (False, True):
+        def launch(t):
+            r = t % R
+            p = t % P
+            args = pyq35.GdnDecodeArgs(
+                n_layers=L, k_heads=KH, v_heads=VH, head_dim_k=D, head_dim_v=D, conv_kernel=4,
+                pos=t // R, eps=1e-6, qkv=qkv + p * L * CONV * 4, z=z + p * L * VD * 4,
+                b=b + p * L * VH * 4, a=av + p * L * VH * 4, conv_w=convw, A_log=alog,
+                dt_bias=dtb, norm_w=normw if fused else None, conv_ring=rings[r],
+                state=states[r], out=out)
+            pyq35.check(pyq35.lib.q35_gdn_decode(args, None))
+        for t in range(a.warmup):
+            launch(t)
+        hip.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for t in range(a.steps):
+            launch(a.warmup + t)
+        hip.record(e1)
+        ms = hip.elapsed_ms(e0, e1)
+        per = ms / a.steps
+        nbytes = L * (GDN_LAYER_BYTES - (0 if fused else VD * 4))
+        res["fused_norm" if fused else "split"] = {
+            "us_per_token": per * 1e3, "tok_per_s": 1e3 / per, "GBs": nbytes / (per / 1e3) / 1e9,
+            "frac": nbytes / (per / 1e3) / 1e9 / HBM_PEAK_GBS, "bytes_per_launch": nbytes}
+    best = max(res.values(), key=lambda v: v["GBs"])
+    return {"metric": "isolated GDN decode (18 layers x 16 heads of 128x128 fp32 state) tok/s",
+            "value": best["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": best["us_per_token"] / 1e3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic N(0,1) inputs",
+            "config": {"workload": "isolated GDN decode", "layers": L, "heads": VH, "state": "128x128",
+                       "rotated_state_sets": R, "working_set_MiB": R * L * VH * D * D * 4 / 2**20},
+            "roofline": {"bound": "hbm", "kernel": "gdn_decode (18 layers per launch)",
+                         "achieved": best["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": best["frac"], "traffic": None, "bytes_per_launch": best["bytes_per_launch"],
+                         "avg_launch_us": best["us_per_token"]},
+            "variants": res}
+
+
+def bench_attn(a) -> dict:
+    """Isolated gated-attention decode at the 2B shape: 6 layers with their own fp32 KV
+    caches (N(0,1)) at each context of --ctx-list, one new token per step across the 6 layers
+    (q/k norm + RoPE + append + split-K softmax + gate)."""
+    import pyq35
+
+    hip = pyq35.Hip()
+    NQ, NKV, HD, L = 16, 2, 256, 6
+    res = {}
+    for ctx in a.ctx_list:
+        maxc = ctx + 2 * (a.warmup + a.steps) + 1
+        n = NKV * maxc * HD  # one layer's K (or V) cache
+        K = hip.upload(pyq35.synth_normal(L * n, 11, 0))
+        V = hip.upload(pyq35.synth_normal(L * n, 11, 1))
+        qg = hip.upload(pyq35.synth_normal(L * 2 * NQ * HD, 12, 0))
+        kn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 1))
+        vn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 2))
+        w = hip.upload(np.zeros(L * HD, np.float32))
+        out = hip.malloc(L * NQ * HD * 4)
+        row = {"kv_working_set_MiB": 2 * L * n * 4 / 2**20}
+        p = ctx
+        for mode in ("batched", "per_layer"):
+            args = pyq35.AttnDecodeArgs(q_heads=NQ, kv_heads=NKV, head_dim=HD, rotary_dim=64, pos=ctx,
+                                        n_splits=a.attn_splits, n_layers=L if mode == "batched" else 1,
+                                        max_context=maxc, rope_theta=1e7, eps=1e-6)
+            ws = pyq35.lib.q35_attn_decode_workspace_bytes(args)
+            wsp = hip.malloc(ws)
+            args.out, args.workspace, args.workspace_bytes = out, wsp, ws
+
+            def step(pos):
+                args.pos = pos
+                if mode == "batched":
+                    args.qg, args.k_new, args.v_new, args.q_norm, args.k_norm = qg, kn, vn, w, w
+                    args.k_cache, args.v_cache = K, V
+                    pyq35.check(pyq35.lib.q35_attn_decode(args, None))
+                else:
+                    for l in range(L):
+                        args.qg, args.k_new = qg + l * 2 * NQ * HD * 4, kn + l * NKV * HD * 4
+                        args.v_new, args.q_norm, args.k_norm = vn + l * NKV * HD * 4, w, w
+                        args.k_cache, args.v_cache = K + l * n * 4, V + l * n * 4
+                        pyq35.check(pyq35.lib.q35_attn_decode(args, None))
+            for _ in range(a.warmup):
+                step(p)
+                p += 1
+            hip.sync()
+            e0, e1 = hip.event(), hip.event()
+            p_first = p
+            hip.record(e0)
+            for _ in range(a.steps):
+                step(p)
+                p += 1
+            hip.record(e1)
+            per = hip.elapsed_ms(e0, e1) / a.steps
+            T = p_first + (a.steps + 1) / 2.0
+            nbytes = L * (4096 * T + 59_392)
+            row[mode] = {"ms_per_token": per, "GBs": nbytes / (per / 1e3) / 1e9,
+                         "frac": nbytes / (per / 1e3) / 1e9 / HBM_PEAK_GBS}
+            hip.free(wsp)
+        res[str(ctx)] = row
+        for q in (K, V, qg, kn, vn, w, out):
+            hip.free(q)
+    key = str(8192) if "8192" in res else list(res)[0]
+    r = res[key]["batched"]
+    return {"metric": "isolated gated-attention decode (6 layers, 2B shape) mixer GB/s", "value": r["GBs"],
+            "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": r["ms_per_token"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+            "data": "synthetic N(0,1) KV cache and inputs",
+            "config": {"workload": "isolated attention decode", "context": int(key), "layers": L,
+                       "heads": f"{NQ}q/{NKV}kv x {HD}"},
+            "roofline": {"bound": "hbm", "kernel": "attention decode (split-K + combine), 6 layers",
+                         "achieved": r["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
+                         "traffic": None},
+            "contexts": res}
+
+
+def calibration_copy(nbytes: int = 256 << 20) -> None:
+    """One device-to-device copy of a known size (the runtime's copy kernel), the reference
+    for scaling FETCH_SIZE / WRITE_SIZE counters to bytes in counter runs."""
+    import pyq35
+
+    hip = pyq35.Hip()
+    src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+    hip.rt.hipMemcpy(pyq35.C.c_void_p(dst), pyq35.C.c_void_p(src), nbytes, 3)
+    hip.sync()
+    hip.free(src)
+    hip.free(dst)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,11 +257,24 @@ def main() -> None:
     ap.add_argument("--model-dir", default="/tmp/q35_synth_2b_seed0")
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["decode", "gdn", "attn"], default="decode",
+                    help="decode: full 2B-shaped decode step (default); gdn / attn: isolated mixers")
+    ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets, round-robin")
+    ap.add_argument("--ctx-list", type=lambda s: [int(x) for x in s.split(",")], default=[2048, 8192, 32768])
+    ap.add_argument("--attn-splits", type=int, default=0)
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
               "(the multi-GPU sharding of the path is a design note, not built)", file=sys.stderr)
         sys.exit(2)
+    if a.workload != "decode":
+        result = bench_gdn(a) if a.workload == "gdn" else bench_attn(a)
+        if a.calibration_copy:
+            calibration_copy()
+        print(json.dumps(result), flush=True)
+        return
 
     import pyq35
 
@@ -190,6 +359,13 @@ def main() -> None:
         "device_ms_per_step": dev_ms / a.steps,
     }
     m.close()
+    if a.calibration_copy:
+        calibration_copy()
+    traffic_file = os.path.join(ROOT, "profiles", "attn_decode_traffic.json")
+    if os.path.exists(traffic_file) and a.ctx == 8192:
+        # HBM bytes per launch of the split-K kernel from the committed counter runs
+        with open(traffic_file) as f:
+            result["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(a.model_dir, d, a.ctx, a.cpu_steps)
     print(json.dumps(result), flush=True)

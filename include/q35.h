@@ -243,10 +243,11 @@ typedef struct q35_gdn_decode_args {
 } q35_gdn_decode_args;
 q35_status q35_gdn_decode(const q35_gdn_decode_args *args, q35_stream s);
 
-/* Gated GQA attention decode for one token of one layer (QwenModel::attn_step after its
- * projections, src/qwen_model.cpp:119-150): q_norm + RoPE on q, k_norm + RoPE on the new
- * key, K/V append at `pos`, softmax over positions 0..pos (split-K over the cache with a
- * combine pass), times sigmoid(gate).
+/* Gated GQA attention decode for one token (QwenModel::attn_step after its projections,
+ * src/qwen_model.cpp:119-150) of n_layers independent layers in one launch: q_norm + RoPE
+ * on q, k_norm + RoPE on the new key, K/V append at `pos`, softmax over positions 0..pos
+ * (split-K over the cache with a combine pass), times sigmoid(gate). Per layer l (arrays
+ * repeat with their natural stride):
  *   qg [NQ][2*HD] (per head: q then gate), k_new [NKV][HD], v_new [NKV][HD] (inputs)
  *   q_norm [HD], k_norm [HD]; k_cache, v_cache [NKV][max_context][HD]
  *   out [NQ][HD]; workspace: q35_attn_decode_workspace_bytes() bytes of device memory.
@@ -255,6 +256,8 @@ typedef struct q35_attn_decode_args {
     int32_t q_heads, kv_heads, head_dim, rotary_dim;
     int32_t pos;
     int32_t n_splits;      /* KV splits per kv head; 0 = automatic */
+    int32_t n_layers;      /* independent layers in one launch (0 or 1 = one) */
+    int32_t reserved;
     int64_t max_context;
     double rope_theta;
     float eps;

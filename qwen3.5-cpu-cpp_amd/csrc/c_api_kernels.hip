@@ -97,7 +97,8 @@ uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args* args) {
     if (!args || args->kv_heads <= 0 || args->q_heads <= 0) return 0;
     const int splits = args->n_splits > 0 ? args->n_splits
                                           : q35k::attn_default_splits(args->max_context, args->kv_heads, q35k::device_cu_count());
-    return static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
+    const uint64_t layers = args->n_layers > 0 ? static_cast<uint64_t>(args->n_layers) : 1;
+    return layers * static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
 }
 
 q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
@@ -141,8 +142,9 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
     a.k_cache = g.k_cache;
     a.v_cache = g.v_cache;
     a.out = g.out;
+    a.n_layers = g.n_layers > 0 ? g.n_layers : 1;
     a.part_o = static_cast<float*>(g.workspace);
-    a.part_ml = a.part_o + static_cast<int64_t>(g.kv_heads) * splits * grp * 256;
+    a.part_ml = a.part_o + static_cast<int64_t>(a.n_layers) * g.kv_heads * splits * grp * 256;
     hipStream_t st = as_stream(s);
     const q35_status r = launched(q35k::launch_attn_partial(a, st), "attn partial");
     if (r != Q35_OK) return r;

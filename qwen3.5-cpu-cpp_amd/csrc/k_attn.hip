@@ -74,6 +74,7 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
 
 template <int GRP, int LPP, int kBatch, bool DBUF>
 __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
+    attn_select_layer(a, blockIdx.z);
     constexpr int NF4 = 64 / LPP;   // float4 of one K row per lane in the score layout
     constexpr int PPW = 64 / LPP;   // positions per score pass (one per lane group)
     constexpr int QIT = kBatch / PPW;
@@ -310,6 +311,7 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
 
 // grid (NQ, HD / 64), 256 threads: wave w merges splits w, w+4, ... for 64 dims (one per lane)
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
+    attn_select_layer(a, blockIdx.z);
     const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = blockIdx.y * 64 + lane;
     const int grp = a.NQ / a.NKV, kh = h / grp, g = h - kh * grp;
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
 template <int GRP>
 hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
     constexpr int LPP = GRP <= 4 ? 16 : 32;
-    dim3 grid(a.n_splits, a.NKV);
+    dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
     constexpr int BATCH = GRP <= 4 ? 8 : GRP == 8 ? 4 : 2;
     attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8)><<<grid, kWaves * 64, 0, s>>>(a);
     return hipGetLastError();
@@ -387,7 +389,7 @@ int device_cu_count() {
 }
 
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s) {
-    dim3 grid(a.NQ, kHD / 64);
+    dim3 grid(a.NQ, kHD / 64, a.n_layers > 0 ? a.n_layers : 1);
     attn_combine_kernel<<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }

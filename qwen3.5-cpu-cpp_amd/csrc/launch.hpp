@@ -59,7 +59,27 @@ struct AttnDecodeArgs {
     float* part_o;              // [NKV][n_splits][GRP][HD]
     float* part_ml;             // [NKV][n_splits][GRP][2]
     float* out;                 // [NQ][HD]
+    // independent layers in one launch (grid.z); every array above repeats per layer with
+    // its natural stride, the caches with stride ls_cache (0 = NKV * max_ctx * HD)
+    int n_layers;
+    int64_t ls_cache;
 };
+// Advances the per-layer pointers of `a` to layer l (device side).
+__device__ __forceinline__ void attn_select_layer(AttnDecodeArgs& a, int l) {
+    if (l == 0) return;
+    const int grp = a.NQ / a.NKV;
+    const int64_t lc = a.ls_cache ? a.ls_cache : static_cast<int64_t>(a.NKV) * a.max_ctx * a.HD;
+    a.qg += static_cast<int64_t>(l) * 2 * a.NQ * a.HD;
+    a.k_new += static_cast<int64_t>(l) * a.NKV * a.HD;
+    a.v_new += static_cast<int64_t>(l) * a.NKV * a.HD;
+    a.q_norm += static_cast<int64_t>(l) * a.HD;
+    a.k_norm += static_cast<int64_t>(l) * a.HD;
+    a.k_cache += l * lc;
+    a.v_cache += l * lc;
+    a.part_o += static_cast<int64_t>(l) * a.NKV * a.n_splits * grp * a.HD;
+    a.part_ml += static_cast<int64_t>(l) * a.NKV * a.n_splits * grp * 2;
+    a.out += static_cast<int64_t>(l) * a.NQ * a.HD;
+}
 // split-K partials, with the q/k norm + RoPE + K/V append of position pos folded in
 hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s);
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s);

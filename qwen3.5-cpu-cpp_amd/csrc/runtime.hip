@@ -339,6 +339,7 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
             aa.part_o = m->part_o;
             aa.part_ml = m->part_ml;
             aa.out = m->mix;
+            aa.n_layers = 1;
             L.run(Q35_KT_ATTN_DECODE, [&] { return q35k::launch_attn_partial(aa, s); });
             L.run(Q35_KT_ATTN_COMBINE, [&] { return q35k::launch_attn_combine(aa, s); });
             q35k::GemvArgs o{};

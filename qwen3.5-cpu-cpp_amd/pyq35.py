@@ -65,7 +65,7 @@ class GdnDecodeArgs(C.Structure):
 class AttnDecodeArgs(C.Structure):
     _fields_ = [("q_heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("rotary_dim", C.c_int32), ("pos", C.c_int32), ("n_splits", C.c_int32),
-                ("max_context", C.c_int64), ("rope_theta", C.c_double), ("eps", C.c_float)] + [
+                ("n_layers", C.c_int32), ("reserved", C.c_int32), ("max_context", C.c_int64), ("rope_theta", C.c_double), ("eps", C.c_float)] + [
         (n, C.c_void_p) for n in ("qg", "k_new", "v_new", "q_norm", "k_norm", "k_cache",
                                   "v_cache", "out", "workspace")] + [
         ("workspace_bytes", C.c_uint64)]

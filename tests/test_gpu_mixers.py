@@ -168,3 +168,43 @@ def test_attn_decode_split_invariance(hip, n_splits):
     """The split-K combine equals the single-pass softmax for any number of splits."""
     out, ref, *_ = run_attn(hip, 16, 2, 3000, 4096, n_splits, seed=77)
     assert rel_l2(out, ref) < REL_L2
+
+
+def test_attn_decode_layer_batch(hip):
+    """Three independent layers in one launch (grid.z) equal three oracle calls."""
+    rng = np.random.default_rng(5)
+    L, nq, nkv, HD, pos, maxc = 3, 8, 2, 256, 700, 800
+    d = attn_dims(nq, nkv)
+    qg = rng.standard_normal((L, 2 * nq * HD)).astype(np.float32)
+    kn = rng.standard_normal((L, nkv * HD)).astype(np.float32)
+    vn = rng.standard_normal((L, nkv * HD)).astype(np.float32)
+    qw = (0.1 * rng.standard_normal((L, HD))).astype(np.float32)
+    kw = (0.1 * rng.standard_normal((L, HD))).astype(np.float32)
+    Kd = np.zeros((L, nkv, maxc, HD), np.float32)
+    Vd = np.zeros_like(Kd)
+    Kd[:, :, :pos] = rng.standard_normal((L, nkv, pos, HD))
+    Vd[:, :, :pos] = rng.standard_normal((L, nkv, pos, HD))
+    B = Bufs(hip)
+    try:
+        args = pyq35.AttnDecodeArgs(q_heads=nq, kv_heads=nkv, head_dim=HD, rotary_dim=64, pos=pos,
+                                    n_splits=0, n_layers=L, max_context=maxc, rope_theta=d.rope_theta,
+                                    eps=d.rms_norm_eps)
+        ws = pyq35.lib.q35_attn_decode_workspace_bytes(args)
+        args.qg, args.k_new, args.v_new = B.up("qg", qg), B.up("kn", kn), B.up("vn", vn)
+        args.q_norm, args.k_norm = B.up("qw", qw), B.up("kw", kw)
+        args.k_cache, args.v_cache = B.up("K", Kd), B.up("V", Vd)
+        args.out = B.alloc("out", L * nq * HD * 4)
+        args.workspace = B.alloc("ws", ws)
+        args.workspace_bytes = ws
+        pyq35.check(pyq35.lib.q35_attn_decode(args, None))
+        hip.sync()
+        out = hip.download(B.p["out"], (L, nq * HD))
+        Kdev = hip.download(B.p["K"], Kd.shape)
+    finally:
+        B.free()
+    for l in range(L):
+        Ko = np.ascontiguousarray(Kd[l].transpose(1, 0, 2))
+        Vo = np.ascontiguousarray(Vd[l].transpose(1, 0, 2))
+        ref = op.attn_core(d, pos, qg[l], kn[l], vn[l], qw[l], kw[l], Ko, Vo)
+        assert rel_l2(out[l], ref) < REL_L2, f"layer {l}"
+        np.testing.assert_allclose(Kdev[l, :, pos], Ko[pos], rtol=2e-6, atol=2e-6)
