@@ -80,8 +80,9 @@ typedef struct q35_budget {
 /* ------------------------------------------------------------------------------------ */
 const char *q35_last_error(void);  /* message for the last failed call on this thread */
 const char *q35_version(void);
-/* Number of device allocations the library has made since load (all of them happen in
- * q35_model_open / q35_model_create; a decode step must leave this unchanged). */
+/* Number of device allocations the library has made since load (they happen in
+ * q35_model_open / q35_model_create, plus the prompt arena of a model's first prefill; a
+ * decode step must leave this unchanged). */
 int64_t q35_device_alloc_count(void);
 
 /* ------------------------------------------------------------------------------------ */
@@ -161,8 +162,19 @@ q35_status q35_model_decode_greedy(q35_model *m, int32_t token, int32_t n_new, i
 /* Whole-prompt forward (QwenForward::prefill, src/qwen_forward.cpp:154-206): starts from a
  * zero state, runs the chunked GDN and flash attention prefill and leaves the model state
  * (GDN state, conv window, KV rows, pos = n) as n decode steps would. logits_host receives
- * n * vocab floats when not NULL. */
+ * n * vocab floats when not NULL. The first call makes the prompt arena (one more device
+ * allocation, kept for later calls): activations for one block of tokens. */
 q35_status q35_model_prefill(q35_model *m, const int32_t *ids, int32_t n, float *logits_host);
+/* The same chunked path continuing from the current position: ids are placed at positions
+ * pos .. pos + n - 1 (no reset). trace_host, when not NULL, receives the hidden state after
+ * every layer for every token, [n][n_layers_total][hidden_size]. Afterwards the last
+ * token's logits / argmax are where q35_model_step leaves them, so decoding continues with
+ * q35_model_decode_greedy. */
+q35_status q35_model_extend(q35_model *m, const int32_t *ids, int32_t n, float *logits_host,
+                            float *trace_host);
+/* Tokens per prefill block (0 = automatic: min(2048, max_context)). Larger blocks make
+ * larger GEMMs and a larger prompt arena. */
+q35_status q35_model_set_prefill_block(q35_model *m, int32_t tokens);
 
 /* Decode-step execution options. */
 q35_status q35_model_set_graph(q35_model *m, int32_t enable);        /* hipGraph replay */
@@ -208,6 +220,12 @@ q35_status q35_model_fill_synthetic(q35_model *m, int64_t pos, uint64_t seed, fl
 /* y = W x, W bf16 row-major [out_dim][in_dim] (forward_pass.cpp:65-75). in_dim % 8 == 0. */
 q35_status q35_matmul_bf16(const uint16_t *W, const float *x, float *y, int32_t out_dim,
                            int32_t in_dim, q35_stream s);
+/* Token-batched matmul for the prefill: Y[M][N] = (R ? R : 0) + X[M][K] . W[N][K]^T, fp32 X /
+ * R / Y with leading dimensions (elements), bf16 W row-major (forward_pass.cpp:65-75 for M
+ * rows at once). Requires K % 8 == 0, ldx % 4 == 0 and a 16-byte aligned X. R may alias Y. */
+q35_status q35_gemm_bf16(const float *X, int64_t ldx, const uint16_t *W, int32_t M, int32_t N,
+                         int32_t K, const float *R, int64_t ldr, float *Y, int64_t ldy,
+                         q35_stream s);
 /* Row-wise y = x * rsqrt(mean(x^2) + eps) * (1 + w) over rows of n (forward_pass.cpp:77-84). */
 q35_status q35_rmsnorm(const float *x, const float *w, float *y, int32_t rows, int32_t n,
                        float eps, q35_stream s);
@@ -268,6 +286,50 @@ typedef struct q35_attn_decode_args {
 } q35_attn_decode_args;
 uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args *args);
 q35_status q35_attn_decode(const q35_attn_decode_args *args, q35_stream s);
+
+/* GDN over a block of n_tokens prompt tokens at positions pos0 .. pos0 + n_tokens - 1, one
+ * layer, chunked (WY form, chunk 64); the replacement of the sequential recurrence of
+ * QwenForward::mix_gdn (src/qwen_forward.cpp:109-142). It continues from `state` and
+ * `conv_ring` (zeros for a fresh prompt: the reference's left zero pad and S = 0) and leaves
+ * them as n_tokens decode steps would. Token-major inputs with leading dimensions:
+ *   qkv [n][ld_qkv] (CONV pre-conv channels), z [n][ld_z] (VD), b, a [n][ld_ba] (VH each)
+ *   conv_w, A_log, dt_bias, norm_w, conv_ring, state as for q35_gdn_decode
+ *   out [n][VD]: gated-rmsnorm output (raw readout when norm_w is NULL)
+ * workspace: q35_gdn_prefill_workspace_bytes() bytes. Requires DK == DV == 128, KER == 4. */
+typedef struct q35_gdn_prefill_args {
+    int32_t n_tokens, pos0, k_heads, v_heads, head_dim_k, head_dim_v, conv_kernel;
+    float eps;
+    const float *qkv, *z, *b, *a;
+    int64_t ld_qkv, ld_z, ld_ba;
+    const float *conv_w, *A_log, *dt_bias, *norm_w;
+    float *conv_ring, *state, *out;
+    void *workspace;
+    uint64_t workspace_bytes;
+} q35_gdn_prefill_args;
+uint64_t q35_gdn_prefill_workspace_bytes(const q35_gdn_prefill_args *args);
+q35_status q35_gdn_prefill(const q35_gdn_prefill_args *args, q35_stream s);
+
+/* Causal gated attention over a block of n_tokens prompt tokens at positions pos0 .., one
+ * layer (QwenForward::mix_attention, src/qwen_forward.cpp:20-80, after its projections):
+ * q_norm + RoPE of every query, k_norm + RoPE of every key, the block's K / V rows appended
+ * to the caches at pos0 + t, softmax over positions [0, pos0 + t], times sigmoid(gate).
+ *   qkv [n][ld_qkv]: NQ x [q | gate] (2 HD each), then NKV x k, then NKV x v
+ *   k_cache, v_cache [NKV][max_context][HD]; out [n][NQ * HD]
+ * workspace: q35_attn_prefill_workspace_bytes() bytes. Requires HD == 256. */
+typedef struct q35_attn_prefill_args {
+    int32_t n_tokens, pos0, q_heads, kv_heads, head_dim, rotary_dim;
+    int64_t max_context;
+    double rope_theta;
+    float eps;
+    const float *qkv;
+    int64_t ld_qkv;
+    const float *q_norm, *k_norm;
+    float *k_cache, *v_cache, *out;
+    void *workspace;
+    uint64_t workspace_bytes;
+} q35_attn_prefill_args;
+uint64_t q35_attn_prefill_workspace_bytes(const q35_attn_prefill_args *args);
+q35_status q35_attn_prefill(const q35_attn_prefill_args *args, q35_stream s);
 
 #ifdef __cplusplus
 }

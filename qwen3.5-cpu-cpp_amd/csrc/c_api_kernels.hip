@@ -36,6 +36,16 @@ q35_status q35_matmul_bf16(const uint16_t* W, const float* x, float* y, int32_t 
     return launched(q35k::launch_gemv(a, q35k::kProPlain, as_stream(s)), "q35_matmul_bf16");
 }
 
+q35_status q35_gemm_bf16(const float* X, int64_t ldx, const uint16_t* W, int32_t M, int32_t N, int32_t K,
+                         const float* R, int64_t ldr, float* Y, int64_t ldy, q35_stream s) {
+    if (!X || !W || !Y || M <= 0 || N <= 0 || K <= 0 || ldx < K || ldy < N || (R && ldr < N))
+        return q35::fail(Q35_ERR_ARG, "q35_gemm_bf16: bad argument");
+    if (K % 8 != 0 || ldx % 4 != 0 || (reinterpret_cast<uintptr_t>(X) & 15) || (reinterpret_cast<uintptr_t>(W) & 15))
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_gemm_bf16: needs K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned X/W");
+    q35k::GemmArgs a{X, W, R, Y, M, N, K, ldx, R ? ldr : 0, ldy};
+    return launched(q35k::launch_gemm(a, as_stream(s)), "q35_gemm_bf16");
+}
+
 q35_status q35_rmsnorm(const float* x, const float* w, float* y, int32_t rows, int32_t n, float eps,
                        q35_stream s) {
     if (!x || !w || !y || rows <= 0 || n <= 0) return q35::fail(Q35_ERR_ARG, "q35_rmsnorm: bad argument");
@@ -149,6 +159,97 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
     const q35_status r = launched(q35k::launch_attn_partial(a, st), "attn partial");
     if (r != Q35_OK) return r;
     return launched(q35k::launch_attn_combine(a, st), "attn combine");
+}
+
+uint64_t q35_gdn_prefill_workspace_bytes(const q35_gdn_prefill_args* args) {
+    if (!args || args->k_heads <= 0 || args->v_heads <= 0 || args->n_tokens <= 0) return 0;
+    return static_cast<uint64_t>(q35k::gdn_prefill_workspace_floats(args->k_heads, args->v_heads, args->n_tokens)) * 4;
+}
+
+q35_status q35_gdn_prefill(const q35_gdn_prefill_args* args, q35_stream s) {
+    if (!args) return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: null args");
+    const q35_gdn_prefill_args& g = *args;
+    if (g.head_dim_k != 128 || g.head_dim_v != 128 || g.conv_kernel != 4)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_gdn_prefill: needs DK == DV == 128 and conv kernel 4");
+    if (g.n_tokens <= 0 || g.pos0 < 0 || g.k_heads <= 0 || g.v_heads <= 0 || g.v_heads % g.k_heads != 0)
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: bad token count, position or head counts");
+    if (!g.qkv || !g.b || !g.a || !g.conv_w || !g.A_log || !g.dt_bias || !g.conv_ring || !g.state || !g.out ||
+        !g.workspace)
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: null pointer");
+    if (g.norm_w && !g.z) return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: the gated norm needs z");
+    const int64_t CONV = 2LL * g.k_heads * 128 + g.v_heads * 128;
+    if (g.ld_qkv < CONV || (g.z && g.ld_z < g.v_heads * 128LL) || g.ld_ba < g.v_heads)
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: leading dimension too small");
+    if (g.workspace_bytes < q35_gdn_prefill_workspace_bytes(args))
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: workspace of %llu bytes, needs %llu",
+                         static_cast<unsigned long long>(g.workspace_bytes),
+                         static_cast<unsigned long long>(q35_gdn_prefill_workspace_bytes(args)));
+    q35k::GdnPrefillArgs a{};
+    a.T = g.n_tokens;
+    a.KH = g.k_heads;
+    a.VH = g.v_heads;
+    a.pos0 = g.pos0;
+    a.eps = g.eps;
+    a.qkv = g.qkv;
+    a.ld_qkv = g.ld_qkv;
+    a.z = g.z;
+    a.ld_z = g.ld_z;
+    a.b = g.b;
+    a.a = g.a;
+    a.ld_ba = g.ld_ba;
+    a.conv_w = g.conv_w;
+    a.A_log = g.A_log;
+    a.dt_bias = g.dt_bias;
+    a.norm_w = g.norm_w;
+    a.conv_ring = g.conv_ring;
+    a.state = g.state;
+    a.out = g.out;
+    q35k::gdn_prefill_carve(a, static_cast<float*>(g.workspace));
+    return launched(q35k::launch_gdn_prefill(a, as_stream(s)), "q35_gdn_prefill");
+}
+
+uint64_t q35_attn_prefill_workspace_bytes(const q35_attn_prefill_args* args) {
+    if (!args || args->q_heads <= 0 || args->n_tokens <= 0) return 0;
+    return static_cast<uint64_t>(q35k::attn_prefill_workspace_floats(args->q_heads, args->n_tokens)) * 4;
+}
+
+q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
+    if (!args) return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: null args");
+    const q35_attn_prefill_args& g = *args;
+    if (g.head_dim != 256) return q35::fail(Q35_ERR_UNSUPPORTED, "q35_attn_prefill: head_dim must be 256");
+    if (g.kv_heads <= 0 || g.q_heads <= 0 || g.q_heads % g.kv_heads != 0)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: bad head counts");
+    if (g.rotary_dim < 0 || g.rotary_dim > 256 || (g.rotary_dim & 1))
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: rotary_dim %d", g.rotary_dim);
+    if (g.n_tokens <= 0 || g.pos0 < 0 || g.pos0 + static_cast<int64_t>(g.n_tokens) > g.max_context)
+        return q35::fail(Q35_ERR_RANGE, "q35_attn_prefill: positions [%d, %lld) outside [0, %lld)", g.pos0,
+                         static_cast<long long>(g.pos0) + g.n_tokens, static_cast<long long>(g.max_context));
+    if (!g.qkv || !g.q_norm || !g.k_norm || !g.k_cache || !g.v_cache || !g.out || !g.workspace)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: null pointer");
+    if (g.ld_qkv < 2LL * g.q_heads * 256 + 2LL * g.kv_heads * 256)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: leading dimension too small");
+    if (g.workspace_bytes < q35_attn_prefill_workspace_bytes(args))
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: workspace of %llu bytes, needs %llu",
+                         static_cast<unsigned long long>(g.workspace_bytes),
+                         static_cast<unsigned long long>(q35_attn_prefill_workspace_bytes(args)));
+    q35k::AttnPrefillArgs a{};
+    a.T = g.n_tokens;
+    a.NQ = g.q_heads;
+    a.NKV = g.kv_heads;
+    a.ROT = g.rotary_dim;
+    a.pos0 = g.pos0;
+    a.max_ctx = g.max_context;
+    a.theta = g.rope_theta;
+    a.eps = g.eps;
+    a.qkv = g.qkv;
+    a.ld_qkv = g.ld_qkv;
+    a.q_norm = g.q_norm;
+    a.k_norm = g.k_norm;
+    a.k_cache = g.k_cache;
+    a.v_cache = g.v_cache;
+    a.Qa = static_cast<float*>(g.workspace);
+    a.out = g.out;
+    return launched(q35k::launch_attn_prefill(a, as_stream(s)), "q35_attn_prefill");
 }
 
 }  // extern "C"

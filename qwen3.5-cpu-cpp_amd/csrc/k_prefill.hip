@@ -1,0 +1,557 @@
+// Whole-prompt mixers (QwenForward::mix_gdn src/qwen_forward.cpp:83-152 and
+// QwenForward::mix_attention src/qwen_forward.cpp:20-80), on a block of T tokens that starts
+// at position pos0 and continues from the model's state (so prefill and decode hand over).
+//
+// Gated DeltaNet, chunked (chunk C = 64, the WY form of the gated delta rule):
+//   prep     conv window + SiLU per channel (inputs before the block come from the conv
+//            ring), l2norm of q and k per head, q scaled by DK^-1/2, beta = sigmoid(b),
+//            g = -exp(A_log) softplus(a + dt_bias); head-major outputs padded to whole chunks
+//            (padding rows have q = k = v = 0, beta = g = 0 and change nothing).
+//   ring     the last three raw inputs of the block go to their ring slots.
+//   chunk    per (v-head, chunk): gamma = cumsum(g);
+//              P[i][j] = q_i.k_j e^(gamma_i - gamma_j)      (j <= i)
+//              A[i][j] = beta_i k_i.k_j e^(gamma_i - gamma_j)  (j < i)
+//              [U | W] = (I + A)^-1 [beta v | beta e^gamma k]  (forward substitution, one
+//                                                               column per thread, in registers)
+//   scan     per (v-head, 16-column slice of the state), sequential over the chunks:
+//              v_new = U - W S;  o = e^gamma (Q S) + P v_new;
+//              S <- e^(gamma_last) S + K^T (e^(gamma_last - gamma) v_new)
+//            The delta rule is column-separable, so the 8 slices of a head are independent.
+//   norm     rmsnorm_gated per (token, v-head) (src/forward_pass.cpp:86-93).
+// Causal attention, flash form on the matrix cores (v_mfma_f32_16x16x4_f32):
+//   prep     q_norm + RoPE of every query row (head-major), k_norm + RoPE of every key and
+//            the values appended to the KV cache at pos0 + t (angles in double).
+//   flash    grid (query tiles of 64, NQ): 4 waves of 16 query rows with their q in
+//            registers; 32-position K / V tiles in LDS; S = Q K^T and O += P V on MFMA;
+//            running max / sum per row; epilogue O / l * sigmoid(gate).
+#include <math.h>
+
+#include "dev_common.hpp"
+#include "launch.hpp"
+
+namespace q35k {
+namespace {
+
+constexpr int kD = 128;   // GDN head dim
+constexpr int kC = 64;    // chunk length
+constexpr int kCW = 16;   // state columns per scan workgroup
+constexpr int kHD = 256;  // attention head dim
+
+// ------------------------------------------------------------------ GDN prep
+// grid (T, KH), 256 threads: conv + SiLU for the k-head's q, k and its rep v-heads' v
+// channels, l2norm of q and k, beta / g of the rep v-heads.
+__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnPrefillArgs a) {
+    const int t = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int rep = a.VH / a.KH;
+    const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
+    const int pos = a.pos0 + t;
+    __shared__ double red[4];
+    auto xin = [&](int s, int ch) -> float {  // raw input of token s (relative) for channel ch
+        if (s >= 0) return a.qkv[static_cast<int64_t>(s) * a.ld_qkv + ch];
+        return a.conv_ring[static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch];
+    };
+    auto conv = [&](int ch) -> float {
+        const float* w4 = a.conv_w + static_cast<int64_t>(ch) * 4;
+        float acc = 0.0f;
+        acc += w4[0] * xin(t - 3, ch);
+        acc += w4[1] * xin(t - 2, ch);
+        acc += w4[2] * xin(t - 1, ch);
+        acc += w4[3] * xin(t, ch);
+        return silu_f(acc);
+    };
+    (void)pos;
+    // q (threads 0..127) and k (128..255)
+    const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
+    const float v = conv(ch);
+    double ss = static_cast<double>(v) * v;
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const double sq = red[0] + red[1], sk = red[2] + red[3];
+    if (tid < kD) {
+        const float inv = 1.0f / sqrtf(static_cast<float>(sq) + 1e-6f);
+        a.Qg[(static_cast<int64_t>(kh) * a.Tp + t) * kD + tid] = (v * inv) * (1.0f / sqrtf(static_cast<float>(kD)));
+    } else {
+        const float inv = 1.0f / sqrtf(static_cast<float>(sk) + 1e-6f);
+        a.Kg[(static_cast<int64_t>(kh) * a.Tp + t) * kD + (tid - kD)] = v * inv;
+    }
+    // v channels and beta / g of the v-heads served by this k-head
+    for (int r = 0; r < rep; ++r) {
+        const int vh = kh * rep + r;
+        if (tid < kD) a.Vg[(static_cast<int64_t>(vh) * a.Tp + t) * kD + tid] = conv(2 * KD + vh * kD + tid);
+        if (tid == 0) {
+            const float bb = a.b[static_cast<int64_t>(t) * a.ld_ba + vh];
+            const float aa = a.a[static_cast<int64_t>(t) * a.ld_ba + vh];
+            a.Bg[static_cast<int64_t>(vh) * a.Tp + t] = sigmoid_f(bb);
+            a.Gg[static_cast<int64_t>(vh) * a.Tp + t] = -expf(a.A_log[vh]) * softplus_f(aa + a.dt_bias[vh]);
+        }
+    }
+}
+
+// zero the padding rows [T, Tp) of the head-major prep outputs
+__global__ __launch_bounds__(256) void gdn_pad_kernel(GdnPrefillArgs a) {
+    const int pad = a.Tp - a.T;
+    const int64_t n_qk = static_cast<int64_t>(a.KH) * pad * kD, n_v = static_cast<int64_t>(a.VH) * pad * kD;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_qk + n_v + 2 * a.VH * pad;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        if (i < n_qk) {
+            const int64_t h = i / (pad * kD), rest = i % (pad * kD);
+            const int64_t off = (h * a.Tp + a.T) * kD + rest;
+            a.Qg[off] = 0.0f;
+            a.Kg[off] = 0.0f;
+        } else if (i < n_qk + n_v) {
+            const int64_t j = i - n_qk, h = j / (pad * kD), rest = j % (pad * kD);
+            a.Vg[(h * a.Tp + a.T) * kD + rest] = 0.0f;
+        } else {
+            const int64_t j = i - n_qk - n_v;
+            const int64_t h = (j % (a.VH * pad)) / pad, r = j % pad;
+            float* dst = j < a.VH * pad ? a.Bg : a.Gg;
+            dst[h * a.Tp + a.T + r] = 0.0f;
+        }
+    }
+}
+
+// ring slots of the block's last three raw inputs
+__global__ __launch_bounds__(256) void gdn_ring_kernel(GdnPrefillArgs a) {
+    const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
+    const int t0 = a.T > 3 ? a.T - 3 : 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < (a.T - t0) * CONV; i += gridDim.x * 256) {
+        const int t = t0 + i / CONV, ch = i % CONV;
+        a.conv_ring[static_cast<int64_t>((a.pos0 + t) & 3) * CONV + ch] = a.qkv[static_cast<int64_t>(t) * a.ld_qkv + ch];
+    }
+}
+
+// ------------------------------------------------------------------ GDN chunk
+// grid (VH, Tp / 64), 256 threads.
+__global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
+    const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int kh = vh / (a.VH / a.KH);
+    const int64_t row0 = static_cast<int64_t>(c) * kC;
+    __shared__ float Ks[kC][kD + 1];
+    __shared__ float Qs[kC][kD + 1];
+    __shared__ float As[kC][kC + 1];
+    __shared__ float gam[kC], beta[kC];
+    const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+    const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+    for (int i = tid; i < kC * kD; i += 256) {
+        Ks[i / kD][i % kD] = K[i];
+        Qs[i / kD][i % kD] = Q[i];
+    }
+    if (tid < kC) beta[tid] = a.Bg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
+    if (tid == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < kC; ++i) {
+            s += a.Gg[static_cast<int64_t>(vh) * a.Tp + row0 + i];
+            gam[i] = s;
+        }
+    }
+    __syncthreads();
+    if (tid < kC) a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid] = gam[tid];
+    // P (j <= i) and A (j < i); thread: row i = tid / 4, columns j = (tid % 4) * 16 + u
+    {
+        const int i = tid >> 2, jb = (tid & 3) * 16;
+        float kk[16], qk[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) kk[u] = qk[u] = 0.0f;
+        for (int d = 0; d < kD; ++d) {
+            const float ki = Ks[i][d], qi = Qs[i][d];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float kj = Ks[jb + u][d];
+                kk[u] = fmaf(ki, kj, kk[u]);
+                qk[u] = fmaf(qi, kj, qk[u]);
+            }
+        }
+        float* P = a.P + ((static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kC + i) * kC;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int j = jb + u;
+            const float dec = j <= i ? expf(gam[i] - gam[j]) : 0.0f;
+            P[j] = j <= i ? qk[u] * dec : 0.0f;
+            As[i][j] = j < i ? beta[i] * kk[u] * dec : 0.0f;
+        }
+    }
+    __syncthreads();
+    // forward substitution on [beta v | beta e^gamma k], one column per thread
+    float col[kC];
+    if (tid < kD) {
+        const float* V = a.Vg + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + tid;
+#pragma unroll
+        for (int i = 0; i < kC; ++i) col[i] = beta[i] * V[static_cast<int64_t>(i) * kD];
+    } else {
+#pragma unroll
+        for (int i = 0; i < kC; ++i) col[i] = beta[i] * expf(gam[i]) * Ks[i][tid - kD];
+    }
+#pragma unroll
+    for (int i = 1; i < kC; ++i) {
+        float x = col[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) x = fmaf(-As[i][k], col[k], x);
+        col[i] = x;
+    }
+    float* dst = (tid < kD ? a.U : a.W) + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + (tid & (kD - 1));
+#pragma unroll
+    for (int i = 0; i < kC; ++i) dst[static_cast<int64_t>(i) * kD] = col[i];
+}
+
+// ------------------------------------------------------------------ GDN scan
+// grid (VH, 128 / kCW), 256 threads; sequential over the chunks.
+__global__ __launch_bounds__(256) void gdn_scan_kernel(GdnPrefillArgs a) {
+    const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
+    const int kh = vh / (a.VH / a.KH);
+    const int col0 = cs * kCW;
+    __shared__ float Ws[kC][kD + 1];
+    __shared__ float Qs[kC][kD + 1];
+    __shared__ float Ks[kC][kD + 1];
+    __shared__ float Ss[kD][kCW];
+    __shared__ float Vn[kC][kCW];
+    __shared__ float Ps[kC][kC + 1];
+    __shared__ float gam[kC];
+    float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
+    for (int i = tid; i < kD * kCW; i += 256) Ss[i / kCW][i % kCW] = S[(i / kCW) * kD + col0 + i % kCW];
+    const int nchunk = a.Tp / kC;
+    const int cc = tid % kCW, grp = tid / kCW;  // column, row group (16 groups)
+    for (int c = 0; c < nchunk; ++c) {
+        const int64_t row0 = static_cast<int64_t>(c) * kC;
+        __syncthreads();  // previous chunk done with the tiles
+        const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
+        const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+        const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+        for (int i = tid; i < kC * kD; i += 256) {
+            Ws[i / kD][i % kD] = W[i];
+            Qs[i / kD][i % kD] = Q[i];
+            Ks[i / kD][i % kD] = K[i];
+        }
+        const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
+        for (int i = tid; i < kC * kC; i += 256) Ps[i / kC][i % kC] = P[i];
+        if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
+        __syncthreads();
+        // v_new = U - W S and the inter-chunk readout e^gamma (Q S), rows grp*4 .. +3
+        float vn[4], oi[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vn[r] = oi[r] = 0.0f;
+        for (int k = 0; k < kD; ++k) {
+            const float s = Ss[k][cc];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                vn[r] = fmaf(Ws[grp * 4 + r][k], s, vn[r]);
+                oi[r] = fmaf(Qs[grp * 4 + r][k], s, oi[r]);
+            }
+        }
+        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0 + cc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = grp * 4 + r;
+            vn[r] = U[static_cast<int64_t>(i) * kD] - vn[r];
+            Vn[i][cc] = vn[r];
+            oi[r] *= expf(gam[i]);
+        }
+        __syncthreads();
+        // intra-chunk: o_i += sum_{j <= i} P[i][j] v_new_j
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = grp * 4 + r;
+            float o = oi[r];
+            for (int j = 0; j <= i; ++j) o = fmaf(Ps[i][j], Vn[j][cc], o);
+            const int64_t t = row0 + i;
+            if (t < a.T) a.O[t * (a.VH * kD) + vh * kD + col0 + cc] = o;
+        }
+        // state: S <- e^(gamma_last) S + K^T (e^(gamma_last - gamma) v_new); rows grp*8 .. +7
+        const float glast = gam[kC - 1];
+        float sn[8];
+        const float dlast = expf(glast);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) sn[r] = Ss[grp * 8 + r][cc] * dlast;
+        for (int i = 0; i < kC; ++i) {
+            const float w = expf(glast - gam[i]) * Vn[i][cc];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) sn[r] = fmaf(Ks[i][grp * 8 + r], w, sn[r]);
+        }
+        __syncthreads();  // every thread has read Ss for this chunk
+#pragma unroll
+        for (int r = 0; r < 8; ++r) Ss[grp * 8 + r][cc] = sn[r];
+    }
+    __syncthreads();
+    for (int i = tid; i < kD * kCW; i += 256) S[(i / kCW) * kD + col0 + i % kCW] = Ss[i / kCW][i % kCW];
+}
+
+// ------------------------------------------------------------------ GDN gated norm
+// grid (T, VH), 128 threads: out = w * (o * rsqrt(mean(o^2) + eps)) * silu(z)
+__global__ __launch_bounds__(128) void gdn_gated_norm_kernel(GdnPrefillArgs a) {
+    const int t = blockIdx.x, vh = blockIdx.y, i = threadIdx.x;
+    __shared__ double red[2];
+    const int64_t off = static_cast<int64_t>(t) * (a.VH * kD) + vh * kD + i;
+    const float o = a.O[off];
+    double ss = wave_sum(static_cast<double>(o) * o);
+    if ((i & 63) == 0) red[i >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(static_cast<float>((red[0] + red[1]) / kD) + a.eps);
+    const float z = a.z[static_cast<int64_t>(t) * a.ld_z + vh * kD + i];
+    a.out[off] = a.norm_w[i] * (o * inv) * silu_f(z);
+}
+
+// ------------------------------------------------------------------ attention prep
+// grid (T, NQ + NKV), 256 threads (one per dim)
+__global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs a) {
+    const int t = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
+    const int pos = a.pos0 + t;
+    __shared__ float buf[kHD];
+    __shared__ float cs[2][kHD / 2];
+    __shared__ double red[4];
+    const float* row = a.qkv + static_cast<int64_t>(t) * a.ld_qkv;
+    const float* src;
+    const float* w;
+    float* dst;
+    if (r < a.NQ) {
+        src = row + static_cast<int64_t>(r) * 2 * kHD;
+        w = a.q_norm;
+        dst = a.Qa + (static_cast<int64_t>(r) * a.T + t) * kHD;
+    } else {
+        const int kh = r - a.NQ;
+        src = row + static_cast<int64_t>(a.NQ) * 2 * kHD + kh * kHD;
+        w = a.k_norm;
+        dst = a.k_cache + (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD;
+        a.v_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + d] =
+            row[static_cast<int64_t>(a.NQ) * 2 * kHD + static_cast<int64_t>(a.NKV) * kHD + kh * kHD + d];
+    }
+    const int half = a.ROT / 2;
+    if (d < half) {
+        const double inv_freq = pow(a.theta, -static_cast<double>(2 * d) / a.ROT);
+        const double ang = static_cast<double>(pos) * inv_freq;
+        cs[0][d] = static_cast<float>(cos(ang));
+        cs[1][d] = static_cast<float>(sin(ang));
+    }
+    const float x = src[d];
+    const double ss = block_sum(static_cast<double>(x) * x, red);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + a.eps);
+    float y = x * inv * (1.0f + w[d]);
+    buf[d] = y;
+    __syncthreads();
+    if (d < a.ROT) {
+        const int i = d < half ? d : d - half;
+        const float c = cs[0][i], s = cs[1][i];
+        const float x1 = buf[i], x2 = buf[i + half];
+        y = d < half ? x1 * c - x2 * s : x2 * c + x1 * s;
+    }
+    dst[d] = y;
+}
+
+// ------------------------------------------------------------------ flash attention
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int kQT = 64;   // query rows per workgroup (16 per wave)
+constexpr int kKT = 32;   // key / value positions per tile
+constexpr int kLd = kHD + 4;
+
+__global__ __launch_bounds__(256) void flash_attn_kernel(AttnPrefillArgs a) {
+    const int qt = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = a.NQ / a.NKV, kh = h / grp;
+    const int t0 = qt * kQT;                  // first query row (block-relative)
+    __shared__ float KV[2][kKT][kLd];         // K tile, V tile (Q staging at the start)
+    __shared__ float Ps[4][16][kKT + 4];
+    const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
+    const int r16 = lane & 15, g4 = lane >> 4;
+
+    // stage this wave's 16 query rows through LDS, then keep the A-operand layout in registers:
+    // q[s] = Q[row r16][4 s + g4]
+    float q[64];
+    {
+        float* Qst = &KV[0][0][0];  // 64 rows x 256 would not fit kLd layout: stage per wave
+        const int rows = kQT;
+        for (int w = 0; w < 4; ++w) {
+            __syncthreads();
+            if (wave == w) {
+                for (int i = lane; i < 16 * kHD; i += 64) {
+                    const int rr = i / kHD, dd = i % kHD;
+                    const int t = t0 + w * 16 + rr;
+                    Qst[rr * kLd + dd] = t < a.T ? a.Qa[(static_cast<int64_t>(h) * a.T + t) * kHD + dd] : 0.0f;
+                }
+            }
+            __syncthreads();
+            if (wave == w) {
+#pragma unroll
+                for (int s = 0; s < 64; ++s) q[s] = Qst[r16 * kLd + 4 * s + g4];
+            }
+        }
+        (void)rows;
+    }
+    floatx4 o[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+    }
+    // this lane's query rows (C layout): 4 g4 + i, block-relative positions
+    const int qrow0 = t0 + wave * 16 + 4 * g4;
+    const int kv_end = a.pos0 + min(a.T, t0 + kQT);  // exclusive, causal for the tile
+    const float* K = a.k_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    const float* V = a.v_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
+        __syncthreads();
+        for (int i = tid; i < kKT * (kHD / 4); i += 256) {
+            const int rr = i / (kHD / 4), c4 = (i % (kHD / 4)) * 4;
+            const int p = kv0 + rr;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (p < kv_end) {
+                kv = *reinterpret_cast<const float4*>(K + static_cast<int64_t>(p) * kHD + c4);
+                vv = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(p) * kHD + c4);
+            }
+            *reinterpret_cast<float4*>(&KV[0][rr][c4]) = kv;
+            *reinterpret_cast<float4*>(&KV[1][rr][c4]) = vv;
+        }
+        __syncthreads();
+        // S = Q K^T: two 16 x 16 blocks of key positions
+        floatx4 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            s[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 64; ++st)
+                s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[st], KV[0][b * 16 + r16][4 * st + g4], s[b], 0, 0, 0);
+        }
+        // mask, scale, running softmax per row (rows 4 g4 + i, key column b * 16 + r16)
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qpos = a.pos0 + qrow0 + i;
+            float v0 = s[0][i] * sc, v1 = s[1][i] * sc;
+            if (kv0 + r16 > qpos) v0 = -INFINITY;
+            if (kv0 + 16 + r16 > qpos) v1 = -INFINITY;
+            float mx = fmaxf(v0, v1);
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m_new = fmaxf(m_run[i], mx);
+            // rows past the prompt end (or fully masked so far) keep m = -inf: no update
+            const bool live = m_new != -INFINITY;
+            const float e0 = live ? expf(v0 - m_new) : 0.0f, e1 = live ? expf(v1 - m_new) : 0.0f;
+            float es = e0 + e1;
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) es += __shfl_xor(es, off);
+            f[i] = live ? expf(m_run[i] - m_new) : 1.0f;
+            l_run[i] = l_run[i] * f[i] + es;
+            m_run[i] = live ? m_new : m_run[i];
+            Ps[wave][4 * g4 + i][r16] = e0;
+            Ps[wave][4 * g4 + i][16 + r16] = e1;
+        }
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[b][i] *= f[i];
+        // O += P V: A = P (row r16, key 4 st + g4), B = V (key 4 st + g4, dim 16 b + r16)
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+#pragma unroll
+        for (int st = 0; st < kKT / 4; ++st) {
+            const float pa = Ps[wave][r16][4 * st + g4];
+#pragma unroll
+            for (int b = 0; b < 16; ++b)
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, KV[1][4 * st + g4][16 * b + r16], o[b], 0, 0, 0);
+        }
+    }
+    // epilogue: rows 4 g4 + i, dims 16 b + r16
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = qrow0 + i;
+        if (t >= a.T) continue;
+        const float inv = 1.0f / l_run[i];
+        const float* gate = a.qkv + static_cast<int64_t>(t) * a.ld_qkv + static_cast<int64_t>(h) * 2 * kHD + kHD;
+        float* out = a.out + static_cast<int64_t>(t) * (a.NQ * kHD) + static_cast<int64_t>(h) * kHD;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int dd = 16 * b + r16;
+            out[dd] = (o[b][i] * inv) * sigmoid_f(gate[dd]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ small prefill helpers
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* gu, float* h, int T, int I) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < static_cast<int64_t>(T) * I;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t t = i / I, c = i % I;
+        const float g = gu[t * 2 * I + c], u = gu[t * 2 * I + I + c];
+        h[i] = silu_f(g) * u;
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint16_t* embed, const int* ids, float* hidden, int T,
+                                                         int H) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < static_cast<int64_t>(T) * H;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t t = i / H, c = i % H;
+        hidden[i] = bf16_to_f32(embed[static_cast<int64_t>(ids[t]) * H + c]);
+    }
+}
+
+int blocks_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return static_cast<int>(b < 8192 ? (b > 0 ? b : 1) : 8192);
+}
+
+}  // namespace
+
+int64_t gdn_prefill_workspace_floats(int KH, int VH, int T) {
+    const int64_t Tp = (T + kC - 1) / kC * kC;
+    return (2 * KH + 3 * static_cast<int64_t>(VH)) * Tp * kD  // Qg Kg Vg U W
+           + 3 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Gam
+           + static_cast<int64_t>(VH) * Tp * kC                // P
+           + static_cast<int64_t>(T) * VH * kD                 // O (raw readout)
+           + 64 * 8;                                           // alignment slack
+}
+
+void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
+    a.Tp = (a.T + kC - 1) / kC * kC;
+    auto take = [&](int64_t n) {
+        float* p = ws;
+        ws += (n + 63) / 64 * 64;
+        return p;
+    };
+    a.Qg = take(static_cast<int64_t>(a.KH) * a.Tp * kD);
+    a.Kg = take(static_cast<int64_t>(a.KH) * a.Tp * kD);
+    a.Vg = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
+    a.U = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
+    a.W = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
+    a.Bg = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.Gg = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.Gam = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.P = take(static_cast<int64_t>(a.VH) * a.Tp * kC);
+    a.O = take(static_cast<int64_t>(a.T) * a.VH * kD);
+}
+
+hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
+    gdn_prep_kernel<<<dim3(a.T, a.KH), 256, 0, s>>>(a);
+    if (a.Tp > a.T) gdn_pad_kernel<<<blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s>>>(a);
+    gdn_ring_kernel<<<blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s>>>(a);
+    gdn_chunk_kernel<<<dim3(a.VH, a.Tp / kC), 256, 0, s>>>(a);
+    gdn_scan_kernel<<<dim3(a.VH, kD / kCW), 256, 0, s>>>(a);
+    if (a.norm_w) {
+        gdn_gated_norm_kernel<<<dim3(a.T, a.VH), 128, 0, s>>>(a);
+    } else {
+        hipError_t e = hipMemcpyAsync(a.out, a.O, static_cast<size_t>(a.T) * a.VH * kD * 4, hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipGetLastError();
+}
+
+int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_t>(NQ) * T * kHD + 64; }
+
+hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
+    attn_prefill_prep_kernel<<<dim3(a.T, a.NQ + a.NKV), 256, 0, s>>>(a);
+    flash_attn_kernel<<<dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s) {
+    swiglu_rows_kernel<<<blocks_for(static_cast<int64_t>(T) * I), 256, 0, s>>>(gu, h, T, I);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s) {
+    embed_rows_kernel<<<blocks_for(static_cast<int64_t>(T) * H), 256, 0, s>>>(embed, ids, hidden, T, H);
+    return hipGetLastError();
+}
+
+}  // namespace q35k

@@ -31,6 +31,18 @@ hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s);
 // Largest in_dim the matvec stages in LDS.
 constexpr int kGemvMaxIn = 16384;
 
+// ---------------------------------------------------------------- token-batched GEMM
+// Y[M][N] = (R ? R : 0) + X[M][K] . W[N][K]^T; K % 8 == 0, ldx % 4 == 0, 16-byte aligned X.
+struct GemmArgs {
+    const float* X;
+    const uint16_t* W;
+    const float* R;  // may alias Y
+    float* Y;
+    int M, N, K;
+    int64_t ldx, ldr, ldy;
+};
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+
 // ---------------------------------------------------------------- GDN decode
 struct GdnDecodeArgs {
     int n_layers, KH, VH, KER;  // DK = DV = 128
@@ -97,6 +109,50 @@ inline int attn_default_splits(int64_t max_ctx, int NKV, int n_cu) {
 }
 // Compute units of the current device (256 on MI355X when the query fails).
 int device_cu_count();
+
+// ---------------------------------------------------------------- whole-prompt mixers
+// GDN over a block of T tokens at positions pos0 .. pos0 + T - 1, continuing from `state`
+// and the conv ring (both updated in place). Inputs are token-major rows with leading
+// dimensions; the workspace pointers (Qg .. O) are carved by gdn_prefill_carve.
+struct GdnPrefillArgs {
+    int T, Tp, KH, VH, pos0;  // Tp = T rounded up to whole chunks
+    float eps;
+    const float* qkv;  // [T][ld_qkv], CONV raw (pre-conv) channels
+    int64_t ld_qkv;
+    const float* z;    // [T][ld_z], VD
+    int64_t ld_z;
+    const float *b, *a;  // [T][ld_ba], VH each
+    int64_t ld_ba;
+    const float *conv_w, *A_log, *dt_bias, *norm_w;  // norm_w null: raw readout
+    float *conv_ring, *state;
+    float* out;        // [T][VH * 128]
+    // workspace (head-major, padded to Tp rows)
+    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Gam, *P, *O;
+};
+int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);
+void gdn_prefill_carve(GdnPrefillArgs& a, float* ws);
+hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s);
+
+// Causal gated attention over a block of T tokens at positions pos0 ..: the block's keys and
+// values are appended to the caches, every query attends to positions [0, pos0 + t].
+struct AttnPrefillArgs {
+    int T, NQ, NKV, ROT, pos0;  // HD = 256
+    int64_t max_ctx;
+    double theta;
+    float eps;
+    const float* qkv;  // [T][ld_qkv]: NQ x [q | gate] (2 HD each), NKV x k, NKV x v
+    int64_t ld_qkv;
+    const float *q_norm, *k_norm;
+    float *k_cache, *v_cache;  // [NKV][max_ctx][HD]
+    float* Qa;                 // workspace [NQ][T][HD]
+    float* out;                // [T][NQ * HD]
+};
+int64_t attn_prefill_workspace_floats(int NQ, int T);
+hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
+// h[t][i] = silu(gu[t][i]) * gu[t][I + i]
+hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s);
+// hidden[t][:] = bf16 embed[ids[t]][:]
+hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s);
 
 // ---------------------------------------------------------------- small kernels
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,

@@ -102,6 +102,13 @@ struct q35_model {
     int64_t pos = 0;  // host mirror of *pos_dev
     int32_t* pinned_token = nullptr;
 
+    // prompt arena: token-block activations of the chunked prefill, made by the first
+    // prefill (one hipMalloc) and kept; pf_block tokens per block
+    uint8_t* pf_arena = nullptr;
+    size_t pf_bytes = 0;
+    int pf_block = 0;        // requested block size (0 = automatic)
+    int pf_arena_block = 0;  // block size the arena was made for
+
     bool use_graph = true;
     bool graph_valid = false;
     bool trace_on = false;
@@ -455,6 +462,7 @@ void destroy(q35_model* m) {
     if (m->state_arena) (void)hipFree(m->state_arena);
     if (m->kv_arena) (void)hipFree(m->kv_arena);
     if (m->scratch) (void)hipFree(m->scratch);
+    if (m->pf_arena) (void)hipFree(m->pf_arena);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -681,6 +689,217 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->budget.activation_bytes = m->scratch_bytes;
     m->budget.vision_scratch_bytes = 0;
     *out = m.release();
+    return Q35_OK;
+}
+
+// ------------------------------------------------------------------ chunked prefill
+// Layout of the prompt arena for blocks of `tb` tokens (offsets in floats, 256-B aligned).
+struct PrefillPlan {
+    int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
+    int64_t hidden = 0, xn = 0, proj = 0, mix = 0, gu = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
+};
+
+int64_t proj_width(const q35_dims& d) {
+    const int64_t KD = d.gdn_k_heads * 128LL, VD = d.gdn_v_heads * 128LL;
+    return std::max<int64_t>(2 * KD + VD + VD + 2LL * d.gdn_v_heads,
+                             2LL * d.attn_q_heads * d.attn_head_dim + 2LL * d.attn_kv_heads * d.attn_head_dim);
+}
+
+PrefillPlan plan_prefill(const q35_dims& d, int tb) {
+    PrefillPlan p;
+    p.tb = tb;
+    p.lr = std::min(tb, 256);
+    const int64_t H = d.hidden_size, I = d.ffn_intermediate, T = tb;
+    const int64_t VD = d.gdn_v_heads * 128LL, QD = static_cast<int64_t>(d.attn_q_heads) * d.attn_head_dim;
+    int64_t cur = 0;
+    auto take = [&](int64_t n) {
+        const int64_t o = cur;
+        cur += (n + 63) / 64 * 64;
+        return o;
+    };
+    p.hidden = take(T * H);
+    p.xn = take(T * H);
+    p.proj = take(T * proj_width(d));
+    p.mix = take(T * std::max(VD, QD));
+    p.gu = take(T * 2 * I);
+    p.hb = take(T * I);
+    p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
+                         q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
+    p.logits = take(static_cast<int64_t>(p.lr) * d.vocab_size);
+    p.ids = take(T);
+    p.total = cur;
+    return p;
+}
+
+int prefill_block_tokens(const q35_model* m) {
+    const int64_t want = m->pf_block > 0 ? m->pf_block : 2048;
+    return static_cast<int>(std::min<int64_t>(want, m->max_ctx));
+}
+
+q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
+    const int tb = prefill_block_tokens(m);
+    *plan = plan_prefill(m->d, tb);
+    if (m->pf_arena && m->pf_arena_block == tb) return Q35_OK;
+    if (m->pf_arena) {
+        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(hipFree(m->pf_arena));
+        m->pf_arena = nullptr;
+        m->pf_bytes = 0;
+    }
+    void* p = nullptr;
+    const size_t bytes = static_cast<size_t>(plan->total) * 4;
+    HIPCHK(dev_alloc(&p, bytes));
+    m->pf_arena = static_cast<uint8_t*>(p);
+    m->pf_bytes = bytes;
+    m->pf_arena_block = tb;
+    std::cerr << "[q35] prompt arena: " << (bytes >> 20) << " MiB for blocks of " << tb << " tokens\n";
+    return Q35_OK;
+}
+
+q35_status gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, int K, const float* R, float* Y,
+                int64_t ldy, hipStream_t s) {
+    q35k::GemmArgs g{X, W, R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
+    const hipError_t e = q35k::launch_gemm(g, s);
+    return e == hipSuccess ? Q35_OK : q35::fail(Q35_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
+}
+
+#define QCHK(expr)                             \
+    do {                                       \
+        const q35_status s_ = (expr);          \
+        if (s_ != Q35_OK) return s_;           \
+    } while (0)
+#define KCHK(expr)                                                                               \
+    do {                                                                                         \
+        const hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess) return q35::fail(Q35_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// One block of T tokens at positions pos0 .. pos0 + T - 1 (ids already in the arena).
+// Row r of the block is prompt row base + r of logits_host / trace_host.
+q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, int64_t base, float* logits_host,
+                         float* trace_host) {
+    const q35_dims& d = m->d;
+    const hipStream_t s = m->stream;
+    const int H = d.hidden_size, I = d.ffn_intermediate, L = d.n_layers_total;
+    const int KH = d.gdn_k_heads, VH = d.gdn_v_heads, KD = KH * 128, VD = VH * 128, CONV = 2 * KD + VD;
+    const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    float* F = reinterpret_cast<float*>(m->pf_arena);
+    float *hidden = F + p.hidden, *xn = F + p.xn, *proj = F + p.proj, *mix = F + p.mix;
+    float *gu = F + p.gu, *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
+    const int* ids = reinterpret_cast<const int*>(F + p.ids);
+
+    KCHK(q35k::launch_embed_rows(m->embed, ids, hidden, T, H, s));
+    for (int li = 0; li < L; ++li) {
+        const LayerDev& ly = m->layers[static_cast<size_t>(li)];
+        KCHK(q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, d.rms_norm_eps, 0, nullptr, s));
+        QCHK(gemm(xn, H, ly.w_in, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s));
+        if (!ly.attn) {
+            q35k::GdnPrefillArgs g{};
+            g.T = T;
+            g.KH = KH;
+            g.VH = VH;
+            g.pos0 = pos0;
+            g.eps = d.rms_norm_eps;
+            g.qkv = proj;
+            g.ld_qkv = ly.in_rows;
+            g.z = proj + CONV;
+            g.ld_z = ly.in_rows;
+            g.b = proj + CONV + VD;
+            g.a = proj + CONV + VD + VH;
+            g.ld_ba = ly.in_rows;
+            g.conv_w = ly.conv_w;
+            g.A_log = ly.A_log;
+            g.dt_bias = ly.dt_bias;
+            g.norm_w = ly.gdn_norm;
+            g.conv_ring = m->conv_ring + static_cast<int64_t>(ly.idx) * 4 * CONV;
+            g.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
+            g.out = mix;
+            q35k::gdn_prefill_carve(g, ws);
+            KCHK(q35k::launch_gdn_prefill(g, s));
+            QCHK(gemm(mix, VD, ly.w_out, T, H, VD, hidden, hidden, H, s));
+        } else {
+            q35k::AttnPrefillArgs a{};
+            a.T = T;
+            a.NQ = NQ;
+            a.NKV = NKV;
+            a.ROT = rot_dims(d);
+            a.pos0 = pos0;
+            a.max_ctx = m->max_ctx;
+            a.theta = d.rope_theta;
+            a.eps = d.rms_norm_eps;
+            a.qkv = proj;
+            a.ld_qkv = ly.in_rows;
+            a.q_norm = ly.q_norm;
+            a.k_norm = ly.k_norm;
+            a.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
+            a.v_cache = a.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
+            a.Qa = ws;
+            a.out = mix;
+            KCHK(q35k::launch_attn_prefill(a, s));
+            QCHK(gemm(mix, NQ * HD, ly.w_out, T, H, NQ * HD, hidden, hidden, H, s));
+        }
+        KCHK(q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, d.rms_norm_eps, 0, nullptr, s));
+        QCHK(gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, gu, 2 * I, s));
+        KCHK(q35k::launch_swiglu_rows(gu, hb, T, I, s));
+        QCHK(gemm(hb, I, ly.w_down, T, H, I, hidden, hidden, H, s));
+        if (trace_host)
+            KCHK(hipMemcpy2DAsync(trace_host + (base * L + li) * H, static_cast<size_t>(L) * H * 4, hidden,
+                                  static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4, static_cast<size_t>(T),
+                                  hipMemcpyDeviceToHost, s));
+    }
+    if (logits_host) {
+        const int V = d.vocab_size;
+        for (int r0 = 0; r0 < T; r0 += p.lr) {
+            const int rows = std::min(p.lr, T - r0);
+            KCHK(q35k::launch_rmsnorm_rows(hidden + static_cast<int64_t>(r0) * H, m->final_norm, xn, rows, H,
+                                           d.rms_norm_eps, 0, nullptr, s));
+            QCHK(gemm(xn, H, m->head, rows, V, H, nullptr, lg, V, s));
+            KCHK(hipMemcpyAsync(logits_host + (base + r0) * V, lg, static_cast<size_t>(rows) * V * 4,
+                                hipMemcpyDeviceToHost, s));
+        }
+    }
+    // the block's last row becomes the decode residual (what the last step would leave)
+    KCHK(q35k::launch_copy_f32(m->hidden, hidden + static_cast<int64_t>(T - 1) * H, H, s));
+    return Q35_OK;
+}
+
+// Feeds ids[0 .. n) at positions pos .. pos + n - 1 through the chunked prefill and leaves the
+// model as n decode steps would: state, conv ring, KV rows, position, the residual and
+// logits of the last token, its argmax in token_dev and ids_dev[pos + n - 1].
+q35_status extend(q35_model* m, const int32_t* ids, int32_t n, float* logits_host, float* trace_host) {
+    if (!m || !ids || n <= 0) return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (m->pos + n > m->max_ctx)
+        return q35::fail(Q35_ERR_RANGE, "position %lld + %d tokens exceeds max_context %lld", (long long)m->pos, n,
+                         (long long)m->max_ctx);
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= m->d.vocab_size || ids[i] >= m->embed_rows)
+            return q35::fail(Q35_ERR_RANGE, "token %d at %d outside [0, %d)", ids[i], i, m->d.vocab_size);
+    PrefillPlan p;
+    QCHK(ensure_prefill_arena(m, &p));
+    float* F = reinterpret_cast<float*>(m->pf_arena);
+    const hipStream_t s = m->stream;
+    const int64_t start = m->pos;
+    for (int64_t r0 = 0; r0 < n; r0 += p.tb) {
+        const int T = static_cast<int>(std::min<int64_t>(p.tb, n - r0));
+        // the previous block's kernels read the ids buffer: order the upload after them
+        HIPCHK(hipMemcpyAsync(F + p.ids, ids + r0, static_cast<size_t>(T) * 4, hipMemcpyHostToDevice, s));
+        QCHK(prefill_block(m, p, static_cast<int>(start + r0), T, r0, logits_host, trace_host));
+        HIPCHK(hipStreamSynchronize(s));  // host ids / logits buffers are reused per block
+    }
+    const q35_dims& d = m->d;
+    q35k::GemvArgs hd{};
+    hd.W = m->head;
+    hd.x = m->hidden;
+    hd.norm_w = m->final_norm;
+    hd.y = m->logits;
+    hd.rows = d.vocab_size;
+    hd.in_dim = d.hidden_size;
+    hd.eps = d.rms_norm_eps;
+    HIPCHK(q35k::launch_gemv(hd, q35k::kProRmsNorm, s));
+    HIPCHK(q35k::launch_set_int(m->pos_dev, static_cast<int>(start + n - 1), s));
+    HIPCHK(q35k::launch_argmax(m->logits, d.vocab_size, m->argmax_part, m->token_dev, m->ids_dev, m->pos_dev, s));
+    HIPCHK(hipStreamSynchronize(s));
+    m->pos = start + n;
     return Q35_OK;
 }
 
@@ -1016,16 +1235,19 @@ q35_status q35_model_fill_synthetic(q35_model* m, int64_t pos, uint64_t seed, fl
 q35_status q35_model_prefill(q35_model* m, const int32_t* ids, int32_t n, float* logits_host) {
     if (!m || !ids || n <= 0) return q35::fail(Q35_ERR_ARG, "bad argument");
     if (n > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "prompt of %d exceeds max_context", n);
-    // Token-serial prefill through the decode kernels: the state it leaves is exactly
-    // what n decode steps leave. The chunked GDN / flash-attention prefill kernels
-    // replace this loop when built.
-    q35_status st = q35_model_reset(m);
+    const q35_status st = q35_model_reset(m);
     if (st != Q35_OK) return st;
-    for (int t = 0; t < n; ++t) {
-        st = q35_model_step(m, ids[t], logits_host ? logits_host + static_cast<int64_t>(t) * m->d.vocab_size : nullptr,
-                            nullptr);
-        if (st != Q35_OK) return st;
-    }
+    return extend(m, ids, n, logits_host, nullptr);
+}
+
+q35_status q35_model_extend(q35_model* m, const int32_t* ids, int32_t n, float* logits_host, float* trace_host) {
+    return extend(m, ids, n, logits_host, trace_host);
+}
+
+q35_status q35_model_set_prefill_block(q35_model* m, int32_t tokens) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (tokens < 0 || tokens > (1 << 20)) return q35::fail(Q35_ERR_RANGE, "prefill block %d", tokens);
+    m->pf_block = tokens;
     return Q35_OK;
 }
 

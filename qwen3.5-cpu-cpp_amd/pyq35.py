@@ -71,6 +71,24 @@ class AttnDecodeArgs(C.Structure):
         ("workspace_bytes", C.c_uint64)]
 
 
+class GdnPrefillArgs(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_tokens", "pos0", "k_heads", "v_heads", "head_dim_k",
+                                         "head_dim_v", "conv_kernel")] + [("eps", C.c_float)] + [
+        (n, C.c_void_p) for n in ("qkv", "z", "b", "a")] + [
+        (n, C.c_int64) for n in ("ld_qkv", "ld_z", "ld_ba")] + [
+        (n, C.c_void_p) for n in ("conv_w", "A_log", "dt_bias", "norm_w", "conv_ring", "state",
+                                  "out", "workspace")] + [("workspace_bytes", C.c_uint64)]
+
+
+class AttnPrefillArgs(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_tokens", "pos0", "q_heads", "kv_heads", "head_dim",
+                                         "rotary_dim")] + [
+        ("max_context", C.c_int64), ("rope_theta", C.c_double), ("eps", C.c_float),
+        ("qkv", C.c_void_p), ("ld_qkv", C.c_int64)] + [
+        (n, C.c_void_p) for n in ("q_norm", "k_norm", "k_cache", "v_cache", "out", "workspace")] + [
+        ("workspace_bytes", C.c_uint64)]
+
+
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built: run __graft_entry__.build() "
@@ -105,6 +123,8 @@ def _load():
         "q35_model_generate_greedy": (S, [P, P, I32, I32, P]),
         "q35_model_decode_greedy": (S, [P, I32, I32, P]),
         "q35_model_prefill": (S, [P, P, I32, P]),
+        "q35_model_extend": (S, [P, P, I32, P, P]),
+        "q35_model_set_prefill_block": (S, [P, I32]),
         "q35_model_set_graph": (S, [P, I32]),
         "q35_model_set_layer_trace": (S, [P, I32]),
         "q35_model_read_layer_trace": (S, [P, P]),
@@ -128,6 +148,11 @@ def _load():
         "q35_gdn_decode": (S, [C.POINTER(GdnDecodeArgs), P]),
         "q35_attn_decode_workspace_bytes": (U64, [C.POINTER(AttnDecodeArgs)]),
         "q35_attn_decode": (S, [C.POINTER(AttnDecodeArgs), P]),
+        "q35_gemm_bf16": (S, [P, I64, P, I32, I32, I32, P, I64, P, I64, P]),
+        "q35_gdn_prefill_workspace_bytes": (U64, [C.POINTER(GdnPrefillArgs)]),
+        "q35_gdn_prefill": (S, [C.POINTER(GdnPrefillArgs), P]),
+        "q35_attn_prefill_workspace_bytes": (U64, [C.POINTER(AttnPrefillArgs)]),
+        "q35_attn_prefill": (S, [C.POINTER(AttnPrefillArgs), P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -244,6 +269,19 @@ class Model:
         lg = np.zeros((len(ids), self.dims.vocab_size), np.float32) if want_logits else None
         check(lib.q35_model_prefill(self.h, ptr(ids), len(ids), ptr(lg) if want_logits else None))
         return lg
+
+    def extend(self, ids, want_logits: bool = True, want_trace: bool = False):
+        """Chunked prefill of ids at the current position; (logits [n][V], trace [n][L][H])."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        d = self.dims
+        lg = np.zeros((len(ids), d.vocab_size), np.float32) if want_logits else None
+        tr = np.zeros((len(ids), d.n_layers_total, d.hidden_size), np.float32) if want_trace else None
+        check(lib.q35_model_extend(self.h, ptr(ids), len(ids), ptr(lg) if want_logits else None,
+                                   ptr(tr) if want_trace else None))
+        return lg, tr
+
+    def set_prefill_block(self, tokens: int):
+        check(lib.q35_model_set_prefill_block(self.h, int(tokens)))
 
     def set_graph(self, on: bool):
         check(lib.q35_model_set_graph(self.h, int(on)))
