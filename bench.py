@@ -235,6 +235,101 @@ def bench_attn(a) -> dict:
             "contexts": res}
 
 
+FP32_MFMA_PEAK_TFS = 157.3
+GDN_CHUNK_FLOPS = 5 * 64 * 64 * 128 * 2 + 3 * 64 * 128 * 128 * 2 + 64 ** 3 // 3 * 2 + 128 * 128
+
+
+def projection_params(d) -> int:
+    """Weights multiplied per token by the prefill GEMMs (every layer matrix, no lm_head)."""
+    H, I = d.hidden_size, d.ffn_intermediate
+    KD, VD, VH = d.gdn_k_heads * 128, d.gdn_v_heads * 128, d.gdn_v_heads
+    NQ, NKV, HD = d.attn_q_heads, d.attn_kv_heads, d.attn_head_dim
+    gdn = ((2 * KD + VD) + VD + 2 * VH) * H + H * VD
+    attn = (2 * NQ * HD + 2 * NKV * HD) * H + H * NQ * HD
+    return d.n_layers_gdn * gdn + d.n_layers_attn * attn + d.n_layers_total * 3 * H * I
+
+
+def bench_prefill(a) -> dict:
+    """Whole-prompt prefill of a 4096-token prompt (ids uniform, seed 2) at the 2B shape:
+    the chunked GDN, the flash attention and the projection GEMMs of all 24 layers; the
+    last row's logits and argmax (what decoding continues from), not every row's logits."""
+    import pyq35
+
+    d = pyq35.dims_for("2b")
+    ensure_model(a.model_dir, d, pyq35)
+    T = a.prompt
+    ids = pyq35.synth_token_ids(2, d.vocab_size, T)
+    m = pyq35.Model(a.model_dir, T + 8)
+    if a.prefill_block:
+        m.set_prefill_block(a.prefill_block)
+    for _ in range(max(1, a.warmup)):
+        m.prefill(ids, want_logits=False)
+    walls = []
+    for _ in range(a.steps):
+        pyq35.check(pyq35.lib.q35_model_synchronize(m.h))
+        t0 = time.perf_counter()
+        m.prefill(ids, want_logits=False)
+        walls.append(time.perf_counter() - t0)
+    wall = float(np.median(walls))
+    m.set_kernel_timing(True)
+    m.prefill(ids, want_logits=False)
+    kt = m.kernel_times()
+    m.set_kernel_timing(False)
+    m.close()
+    NQ, HD = d.attn_q_heads, d.attn_head_dim
+    attn_flops = 4 * NQ * HD * T * (T + 1) / 2  # per layer, causal half
+    nchunk = (T + 63) // 64
+    gdn_flops = GDN_CHUNK_FLOPS * d.gdn_v_heads * nchunk  # per layer
+    gemm_flops = 2.0 * T * projection_params(d)
+    ms = {k: v[0] for k, v in kt.items()}
+    n = {k: v[1] for k, v in kt.items()}
+    attn_tfs = attn_flops * n["attn_prefill"] / (ms["attn_prefill"] / 1e3) / 1e12
+    gdn_tfs = gdn_flops * n["gdn_prefill"] / (ms["gdn_prefill"] / 1e3) / 1e12
+    gemm_tfs = gemm_flops / (ms["gemm"] / 1e3) / 1e12
+    kernels = {k: {"ms": v[0], "launches": v[1]} for k, v in kt.items() if v[1]}
+    dominant = max(("gemm", "attn_prefill", "gdn_prefill"), key=lambda k: ms[k])
+    ach = {"gemm": gemm_tfs, "attn_prefill": attn_tfs, "gdn_prefill": gdn_tfs}[dominant]
+    mixer_flops = d.n_layers_attn * attn_flops + d.n_layers_gdn * gdn_flops
+    mixer_ms = ms["attn_prefill"] + ms["gdn_prefill"]
+    res = {
+        "metric": "prefill tok/s + MFMA TFLOP/s, 2B-shaped 4096-token prompt, 1 MI355X",
+        "value": T / wall, "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic: random-init bf16 weights N(0,0.02) seed 0, ids uniform seed 2",
+        "config": {"workload": f"2B-shaped Qwen3.5 prefill of {T} tokens", "hidden": d.hidden_size,
+                   "layers": "24 = 18 GDN + 6 gated attention", "prompt": T,
+                   "block": a.prefill_block or min(2048, T + 8), "gdn_chunk": 64},
+        "roofline": {"bound": "mfma", "kernel": dominant, "achieved": ach, "peak": FP32_MFMA_PEAK_TFS,
+                     "unit": "TFLOP/s", "frac": ach / FP32_MFMA_PEAK_TFS, "traffic": None},
+        "mixers": {"attn_prefill_TFs": attn_tfs, "gdn_prefill_TFs": gdn_tfs, "gemm_TFs": gemm_tfs,
+                   "mixer_TFs": mixer_flops / (mixer_ms / 1e3) / 1e12,
+                   "mixer_ms": mixer_ms, "gemm_ms": ms["gemm"], "other_ms": ms["other"]},
+        "kernels": kernels,
+    }
+    if not a.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_prefill_baseline(a.model_dir, d, a.cpu_prompt)
+    return res
+
+
+def cpu_prefill_baseline(model_dir: str, dims, n_tok: int) -> dict:
+    """QwenForward::prefill (oracle/_ref when built, else the oracle port) on the first
+    n_tok ids of the same prompt."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_py as op
+    import pyq35
+
+    ids = pyq35.synth_token_ids(2, dims.vocab_size, n_tok)
+    kind = "reference" if op.ref_available() else "port"
+    r = op.Ref(model_dir, n_tok + 8) if kind == "reference" else op.Oracle(model_dir, n_tok + 8)
+    r.prefill(ids[:1])  # first touch of every weight (the reference widens them once, cached)
+    t0 = time.perf_counter()
+    r.prefill(ids)
+    dt = time.perf_counter() - t0
+    r.close()
+    return {"value": n_tok / dt, "unit": "tok/s", "cores": op.threads(), "kind": kind,
+            "sample": f"prefill of the first {n_tok} prompt ids (every row's logits), {dt:.1f} s"}
+
+
 def calibration_copy(nbytes: int = 256 << 20) -> None:
     """One device-to-device copy of a known size (the runtime's copy kernel), the reference
     for scaling FETCH_SIZE / WRITE_SIZE counters to bytes in counter runs."""
@@ -257,8 +352,12 @@ def main() -> None:
     ap.add_argument("--model-dir", default="/tmp/q35_synth_2b_seed0")
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "gdn", "attn"], default="decode",
-                    help="decode: full 2B-shaped decode step (default); gdn / attn: isolated mixers")
+    ap.add_argument("--workload", choices=["decode", "gdn", "attn", "prefill"], default="decode",
+                    help="decode: full 2B-shaped decode step (default); gdn / attn: isolated mixers; "
+                         "prefill: 2B-shaped whole-prompt prefill")
+    ap.add_argument("--prompt", type=int, default=4096, help="prefill: prompt tokens")
+    ap.add_argument("--prefill-block", type=int, default=0, help="prefill: tokens per block (0 = auto)")
+    ap.add_argument("--cpu-prompt", type=int, default=32, help="prefill: prompt tokens of the CPU sample")
     ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets, round-robin")
     ap.add_argument("--ctx-list", type=lambda s: [int(x) for x in s.split(",")], default=[2048, 8192, 32768])
     ap.add_argument("--attn-splits", type=int, default=0)
@@ -270,7 +369,7 @@ def main() -> None:
               "(the multi-GPU sharding of the path is a design note, not built)", file=sys.stderr)
         sys.exit(2)
     if a.workload != "decode":
-        result = bench_gdn(a) if a.workload == "gdn" else bench_attn(a)
+        result = {"gdn": bench_gdn, "attn": bench_attn, "prefill": bench_prefill}[a.workload](a)
         if a.calibration_copy:
             calibration_copy()
         print(json.dumps(result), flush=True)

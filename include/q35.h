@@ -184,14 +184,18 @@ q35_status q35_model_read_layer_trace(q35_model *m, float *host);
 /* Residual stream after the last layer of the last step (before the final norm). */
 q35_status q35_model_read_hidden(q35_model *m, float *host);
 
-/* Per-kernel-class device time of the decode steps run while timing is on (hipEvents on
- * the model stream around each launch; graph replay is bypassed while it is on). */
+/* Per-kernel-class device time of the decode steps and prefills run while timing is on
+ * (hipEvents on the model stream around each launch; graph replay is bypassed while it is
+ * on). */
 #define Q35_KT_GEMV 0
 #define Q35_KT_GDN_DECODE 1
 #define Q35_KT_ATTN_DECODE 2   /* split-K kernel (q/k norm + RoPE + KV append folded in) */
 #define Q35_KT_ATTN_COMBINE 3
 #define Q35_KT_OTHER 4
-#define Q35_KT_COUNT 5
+#define Q35_KT_GEMM 5          /* prefill projections */
+#define Q35_KT_GDN_PREFILL 6   /* one layer's chunked GDN (prep, chunk, scan, gated norm) */
+#define Q35_KT_ATTN_PREFILL 7  /* one layer's q/k norm + RoPE + append and flash kernel */
+#define Q35_KT_COUNT 8
 q35_status q35_model_set_kernel_timing(q35_model *m, int32_t enable);
 /* ms[Q35_KT_COUNT] total milliseconds, launches[Q35_KT_COUNT]; resets the counters. */
 q35_status q35_model_kernel_times(q35_model *m, double *ms, int64_t *launches);

@@ -316,3 +316,11 @@ class Ref:
 
     def hidden(self):
         return view(self.lib().ref_hidden(self.h), (self.H,)).copy()
+
+    def prefill(self, ids) -> np.ndarray:
+        """QwenForward::prefill: logits of every row, [n][vocab]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        lg = np.zeros((len(ids), self.vocab), np.float32)
+        if self.lib().ref_prefill(self.h, _p(ids), len(ids), _p(lg)) != 0:
+            raise RuntimeError("reference prefill failed")
+        return lg

@@ -756,23 +756,11 @@ q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
     return Q35_OK;
 }
 
-q35_status gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, int K, const float* R, float* Y,
+hipError_t gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, int K, const float* R, float* Y,
                 int64_t ldy, hipStream_t s) {
-    q35k::GemmArgs g{X, W, R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
-    const hipError_t e = q35k::launch_gemm(g, s);
-    return e == hipSuccess ? Q35_OK : q35::fail(Q35_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
+    const q35k::GemmArgs g{X, W, R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
+    return q35k::launch_gemm(g, s);
 }
-
-#define QCHK(expr)                             \
-    do {                                       \
-        const q35_status s_ = (expr);          \
-        if (s_ != Q35_OK) return s_;           \
-    } while (0)
-#define KCHK(expr)                                                                               \
-    do {                                                                                         \
-        const hipError_t e_ = (expr);                                                            \
-        if (e_ != hipSuccess) return q35::fail(Q35_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
-    } while (0)
 
 // One block of T tokens at positions pos0 .. pos0 + T - 1 (ids already in the arena).
 // Row r of the block is prompt row base + r of logits_host / trace_host.
@@ -783,23 +771,25 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
     const int H = d.hidden_size, I = d.ffn_intermediate, L = d.n_layers_total;
     const int KH = d.gdn_k_heads, VH = d.gdn_v_heads, KD = KH * 128, VD = VH * 128, CONV = 2 * KD + VD;
     const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    const float eps = d.rms_norm_eps;
     float* F = reinterpret_cast<float*>(m->pf_arena);
     float *hidden = F + p.hidden, *xn = F + p.xn, *proj = F + p.proj, *mix = F + p.mix;
     float *gu = F + p.gu, *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
     const int* ids = reinterpret_cast<const int*>(F + p.ids);
+    Launcher Lr{m, s, m->timing_on};
 
-    KCHK(q35k::launch_embed_rows(m->embed, ids, hidden, T, H, s));
+    Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_embed_rows(m->embed, ids, hidden, T, H, s); });
     for (int li = 0; li < L; ++li) {
         const LayerDev& ly = m->layers[static_cast<size_t>(li)];
-        KCHK(q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, d.rms_norm_eps, 0, nullptr, s));
-        QCHK(gemm(xn, H, ly.w_in, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s));
+        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_in, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s); });
         if (!ly.attn) {
             q35k::GdnPrefillArgs g{};
             g.T = T;
             g.KH = KH;
             g.VH = VH;
             g.pos0 = pos0;
-            g.eps = d.rms_norm_eps;
+            g.eps = eps;
             g.qkv = proj;
             g.ld_qkv = ly.in_rows;
             g.z = proj + CONV;
@@ -815,8 +805,8 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             g.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
             g.out = mix;
             q35k::gdn_prefill_carve(g, ws);
-            KCHK(q35k::launch_gdn_prefill(g, s));
-            QCHK(gemm(mix, VD, ly.w_out, T, H, VD, hidden, hidden, H, s));
+            Lr.run(Q35_KT_GDN_PREFILL, [&] { return q35k::launch_gdn_prefill(g, s); });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm(mix, VD, ly.w_out, T, H, VD, hidden, hidden, H, s); });
         } else {
             q35k::AttnPrefillArgs a{};
             a.T = T;
@@ -826,7 +816,7 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.pos0 = pos0;
             a.max_ctx = m->max_ctx;
             a.theta = d.rope_theta;
-            a.eps = d.rms_norm_eps;
+            a.eps = eps;
             a.qkv = proj;
             a.ld_qkv = ly.in_rows;
             a.q_norm = ly.q_norm;
@@ -835,32 +825,38 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.v_cache = a.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
             a.Qa = ws;
             a.out = mix;
-            KCHK(q35k::launch_attn_prefill(a, s));
-            QCHK(gemm(mix, NQ * HD, ly.w_out, T, H, NQ * HD, hidden, hidden, H, s));
+            Lr.run(Q35_KT_ATTN_PREFILL, [&] { return q35k::launch_attn_prefill(a, s); });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm(mix, NQ * HD, ly.w_out, T, H, NQ * HD, hidden, hidden, H, s); });
         }
-        KCHK(q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, d.rms_norm_eps, 0, nullptr, s));
-        QCHK(gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, gu, 2 * I, s));
-        KCHK(q35k::launch_swiglu_rows(gu, hb, T, I, s));
-        QCHK(gemm(hb, I, ly.w_down, T, H, I, hidden, hidden, H, s));
+        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, gu, 2 * I, s); });
+        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_swiglu_rows(gu, hb, T, I, s); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm(hb, I, ly.w_down, T, H, I, hidden, hidden, H, s); });
         if (trace_host)
-            KCHK(hipMemcpy2DAsync(trace_host + (base * L + li) * H, static_cast<size_t>(L) * H * 4, hidden,
-                                  static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4, static_cast<size_t>(T),
-                                  hipMemcpyDeviceToHost, s));
+            Lr.run(Q35_KT_OTHER, [&] {
+                return hipMemcpy2DAsync(trace_host + (base * L + li) * H, static_cast<size_t>(L) * H * 4, hidden,
+                                        static_cast<size_t>(H) * 4, static_cast<size_t>(H) * 4,
+                                        static_cast<size_t>(T), hipMemcpyDeviceToHost, s);
+            });
     }
     if (logits_host) {
         const int V = d.vocab_size;
         for (int r0 = 0; r0 < T; r0 += p.lr) {
             const int rows = std::min(p.lr, T - r0);
-            KCHK(q35k::launch_rmsnorm_rows(hidden + static_cast<int64_t>(r0) * H, m->final_norm, xn, rows, H,
-                                           d.rms_norm_eps, 0, nullptr, s));
-            QCHK(gemm(xn, H, m->head, rows, V, H, nullptr, lg, V, s));
-            KCHK(hipMemcpyAsync(logits_host + (base + r0) * V, lg, static_cast<size_t>(rows) * V * 4,
-                                hipMemcpyDeviceToHost, s));
+            Lr.run(Q35_KT_OTHER, [&] {
+                return q35k::launch_rmsnorm_rows(hidden + static_cast<int64_t>(r0) * H, m->final_norm, xn, rows, H,
+                                                 eps, 0, nullptr, s);
+            });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, m->head, rows, V, H, nullptr, lg, V, s); });
+            Lr.run(Q35_KT_OTHER, [&] {
+                return hipMemcpyAsync(logits_host + (base + r0) * V, lg, static_cast<size_t>(rows) * V * 4,
+                                      hipMemcpyDeviceToHost, s);
+            });
         }
     }
     // the block's last row becomes the decode residual (what the last step would leave)
-    KCHK(q35k::launch_copy_f32(m->hidden, hidden + static_cast<int64_t>(T - 1) * H, H, s));
-    return Q35_OK;
+    Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_copy_f32(m->hidden, hidden + static_cast<int64_t>(T - 1) * H, H, s); });
+    return Lr.st;
 }
 
 // Feeds ids[0 .. n) at positions pos .. pos + n - 1 through the chunked prefill and leaves the
@@ -875,7 +871,8 @@ q35_status extend(q35_model* m, const int32_t* ids, int32_t n, float* logits_hos
         if (ids[i] < 0 || ids[i] >= m->d.vocab_size || ids[i] >= m->embed_rows)
             return q35::fail(Q35_ERR_RANGE, "token %d at %d outside [0, %d)", ids[i], i, m->d.vocab_size);
     PrefillPlan p;
-    QCHK(ensure_prefill_arena(m, &p));
+    const q35_status pa = ensure_prefill_arena(m, &p);
+    if (pa != Q35_OK) return pa;
     float* F = reinterpret_cast<float*>(m->pf_arena);
     const hipStream_t s = m->stream;
     const int64_t start = m->pos;
@@ -883,8 +880,11 @@ q35_status extend(q35_model* m, const int32_t* ids, int32_t n, float* logits_hos
         const int T = static_cast<int>(std::min<int64_t>(p.tb, n - r0));
         // the previous block's kernels read the ids buffer: order the upload after them
         HIPCHK(hipMemcpyAsync(F + p.ids, ids + r0, static_cast<size_t>(T) * 4, hipMemcpyHostToDevice, s));
-        QCHK(prefill_block(m, p, static_cast<int>(start + r0), T, r0, logits_host, trace_host));
+        const q35_status st = prefill_block(m, p, static_cast<int>(start + r0), T, r0, logits_host, trace_host);
+        if (st != Q35_OK) return st;
         HIPCHK(hipStreamSynchronize(s));  // host ids / logits buffers are reused per block
+        const q35_status tt = collect_timing(m);
+        if (tt != Q35_OK) return tt;
     }
     const q35_dims& d = m->d;
     q35k::GemvArgs hd{};

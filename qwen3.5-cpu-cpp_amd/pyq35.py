@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libq35.so")
 
 Q35_OK = 0
-KT_NAMES = ["gemv", "gdn_decode", "attn_decode", "attn_combine", "other"]
+KT_NAMES = ["gemv", "gdn_decode", "attn_decode", "attn_combine", "other", "gemm", "gdn_prefill",
+            "attn_prefill"]
 
 
 class Q35Error(RuntimeError):
