@@ -29,6 +29,21 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+class stdout_to_stderr:
+    """Points file descriptor 1 at stderr for the block: the reference engine prints its
+    arena plan on stdout, and stdout carries only the JSON result line."""
+
+    def __enter__(self):
+        sys.stdout.flush()
+        self.saved = os.dup(1)
+        os.dup2(2, 1)
+
+    def __exit__(self, *exc):
+        sys.stdout.flush()
+        os.dup2(self.saved, 1)
+        os.close(self.saved)
+
+
 def ensure_model(path: str, dims, pyq35) -> None:
     st = os.path.join(path, "model.safetensors")
     if os.path.exists(st) and os.path.exists(os.path.join(path, "config.json")):
@@ -283,8 +298,9 @@ def bench_prefill(a) -> dict:
     gemm_flops = 2.0 * T * projection_params(d)
     ms = {k: v[0] for k, v in kt.items()}
     n = {k: v[1] for k, v in kt.items()}
-    attn_tfs = attn_flops * n["attn_prefill"] / (ms["attn_prefill"] / 1e3) / 1e12
-    gdn_tfs = gdn_flops * n["gdn_prefill"] / (ms["gdn_prefill"] / 1e3) / 1e12
+    # launches are per (block, layer); the flop counts above are per layer over the prompt
+    attn_tfs = attn_flops * d.n_layers_attn / (ms["attn_prefill"] / 1e3) / 1e12
+    gdn_tfs = gdn_flops * d.n_layers_gdn / (ms["gdn_prefill"] / 1e3) / 1e12
     gemm_tfs = gemm_flops / (ms["gemm"] / 1e3) / 1e12
     kernels = {k: {"ms": v[0], "launches": v[1]} for k, v in kt.items() if v[1]}
     dominant = max(("gemm", "attn_prefill", "gdn_prefill"), key=lambda k: ms[k])
@@ -307,7 +323,8 @@ def bench_prefill(a) -> dict:
         "kernels": kernels,
     }
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_prefill_baseline(a.model_dir, d, a.cpu_prompt)
+        with stdout_to_stderr():
+            res["cpu_baseline"] = cpu_prefill_baseline(a.model_dir, d, a.cpu_prompt)
     return res
 
 
@@ -466,7 +483,8 @@ def main() -> None:
         with open(traffic_file) as f:
             result["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     if not a.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(a.model_dir, d, a.ctx, a.cpu_steps)
+        with stdout_to_stderr():
+            result["cpu_baseline"] = cpu_baseline(a.model_dir, d, a.ctx, a.cpu_steps)
     print(json.dumps(result), flush=True)
 
 
