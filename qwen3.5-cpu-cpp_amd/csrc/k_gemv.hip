@@ -2,16 +2,21 @@
 // (the reference's matmul(WeightView), src/forward_pass.cpp:44-75), with the elementwise
 // work that feeds or follows each projection fused in:
 //   prologue  rmsnorm (1+w)       input_layernorm / post_attention_layernorm / final norm
-//             silu(g) * u         SwiGLU before mlp.down_proj
+//             silu(g) * u         SwiGLU of a [gate | up] input vector
 //             gated rmsnorm        GDN rmsnorm_gated before linear_attn.out_proj
 //   epilogue  y = resid + W x     residual add of the mixer / FFN output
+//             silu(y_2i) y_2i+1   SwiGLU of the interleaved gate / up projection (the
+//                                 down_proj matvec then reads silu(gate) * up directly)
 //
 // HBM-bound: every weight byte is read exactly once per step. A 256-thread workgroup
 // stages the transformed input vector in LDS once, then each 64-lane wave streams RPW
 // weight rows at a time with 16-byte loads (8 bf16 per lane, 1 KiB per wave per row and
-// chunk), issuing up to 4 chunks of loads before consuming them. bf16 is widened exactly
-// (shift into the upper half of an fp32) and accumulated in fp32 FMA; the 64 lane partials
-// are summed with a butterfly.
+// chunk), issuing up to 4 chunks of loads before consuming them. The first row group's
+// loads are issued before the prologue, which they do not depend on, so the HBM latency
+// overlaps the input staging. bf16 is widened exactly (shift into the upper half of an
+// fp32) and accumulated in fp32 FMA; the 64 lane partials are summed with a butterfly.
+#include <cstdlib>
+
 #include "dev_common.hpp"
 #include "launch.hpp"
 
@@ -88,97 +93,277 @@ __device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs) {
     __syncthreads();
 }
 
-template <int PRO, bool RESID, int RPW>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-    extern __shared__ float xs[];
-    stage_input<PRO>(a, xs);
+// Number of 512-element chunks prefetched for the first row group: all KC of them when the
+// width is known at compile time (KC > 0), else the first 4.
+constexpr int pf_chunks(int KC) { return KC > 0 ? KC : 4; }
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n = a.in_dim;
-    const int nfull = n >> 9;              // 512-element chunks: 64 lanes x 8
-    const int tail = n - (nfull << 9);     // multiple of 8
-    const int row_step = gridDim.x * 4 * RPW;
-    for (int r0 = (blockIdx.x * 4 + wave) * RPW; r0 < a.rows; r0 += row_step) {
-        const uint16_t* wr[RPW];
-        float acc[RPW];
+// Loads the first row group's chunks (the part that can be in flight before the input).
+template <int RPW, int KC>
+__device__ __forceinline__ void load_rows(const GemvArgs& a, int r0, u32x4 (&w)[pf_chunks(KC)][RPW]) {
+    const int lane = threadIdx.x & 63, n = a.in_dim, nfull = n >> 9;
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int row = min(r0 + r, a.rows - 1);
-            wr[r] = a.W + static_cast<size_t>(row) * n + lane * 8;
-            acc[r] = 0.0f;
+    for (int r = 0; r < RPW; ++r) {
+        const uint16_t* p = a.W + static_cast<size_t>(min(r0 + r, a.rows - 1)) * n + lane * 8;
+#pragma unroll
+        for (int u = 0; u < pf_chunks(KC); ++u)
+            if (KC > 0 || u < nfull) w[u][r] = load_w(p + (u << 9));
+    }
+}
+
+template <int EPI, int RPW>
+__device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const float (&acc)[RPW]) {
+    const int lane = threadIdx.x & 63;
+    float sum[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) sum[r] = wave_sum(acc[r]);
+    if (lane != 0) return;
+    if (EPI == kEpiSwiGluPair) {
+        // rows (2i, 2i + 1) = (gate_i, up_i) of the interleaved [gate|up] matrix
+        if (r0 + 1 < a.rows) a.y[r0 >> 1] = silu_f(sum[0]) * sum[RPW - 1];
+    } else {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            if (r0 + r < a.rows) a.y[r0 + r] = EPI == kEpiResidual ? a.resid[r0 + r] + sum[r] : sum[r];
+    }
+}
+
+// RPW consecutive rows of one wave from `r0`. With PF the first pf_chunks(KC) chunks come
+// from `pf` (loaded before the input prologue). With KC > 0 the width is KC * 512 and every
+// chunk of the group is in flight at once.
+template <int EPI, int RPW, int KC, bool PF>
+__device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, int r0,
+                                          const u32x4 (&pf)[pf_chunks(KC)][RPW]) {
+    const int lane = threadIdx.x & 63;
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+    if (KC > 0) {
+        u32x4 w[pf_chunks(KC)][RPW];
+        if (PF) {
+#pragma unroll
+            for (int u = 0; u < pf_chunks(KC); ++u)
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) w[u][r] = pf[u][r];
+        } else {
+            load_rows<RPW, KC>(a, r0, w);
         }
-        int k = 0;
-        for (; k + 4 <= nfull; k += 4) {
-            u32x4 w[4][RPW];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < pf_chunks(KC); ++u) {
+            const int c = (u << 9) + lane * 8;
+            const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
+            const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
 #pragma unroll
-                for (int r = 0; r < RPW; ++r)
-                    w[u][r] = load_w(wr[r] + ((k + u) << 9));
+            for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[u][r], x0, x1, acc[r]);
+        }
+        store_rows<EPI, RPW>(a, r0, acc);
+        return;
+    }
+    const int n = a.in_dim;
+    const int nfull = n >> 9;           // 512-element chunks: 64 lanes x 8
+    const int tail = n - (nfull << 9);  // multiple of 8
+    const uint16_t* wr[RPW];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int c = ((k + u) << 9) + lane * 8;
+    for (int r = 0; r < RPW; ++r) wr[r] = a.W + static_cast<size_t>(min(r0 + r, a.rows - 1)) * n + lane * 8;
+    int k = 0;
+    if (PF) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (u < nfull) {
+                const int c = (u << 9) + lane * 8;
                 const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
                 const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
 #pragma unroll
-                for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[u][r], x0, x1, acc[r]);
+                for (int r = 0; r < RPW; ++r) acc[r] = dot8(pf[u][r], x0, x1, acc[r]);
             }
         }
-        for (; k < nfull; ++k) {
-            u32x4 w[RPW];
+        k = min(nfull, 4);
+    }
+    for (; k + 4 <= nfull; k += 4) {
+        u32x4 w[4][RPW];
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) w[r] = load_w(wr[r] + (k << 9));
-            const int c = (k << 9) + lane * 8;
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) w[u][r] = load_w(wr[r] + ((k + u) << 9));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = ((k + u) << 9) + lane * 8;
             const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
             const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[r], x0, x1, acc[r]);
+            for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[u][r], x0, x1, acc[r]);
         }
-        if (lane * 8 < tail) {
-            const int c = (nfull << 9) + lane * 8;
-            const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
-            const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
+    }
+    for (; k < nfull; ++k) {
+        u32x4 w[RPW];
 #pragma unroll
-            for (int r = 0; r < RPW; ++r) {
-                const u32x4 w = load_w(wr[r] + (nfull << 9));
-                acc[r] = dot8(w, x0, x1, acc[r]);
-            }
-        }
+        for (int r = 0; r < RPW; ++r) w[r] = load_w(wr[r] + (k << 9));
+        const int c = (k << 9) + lane * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
+        const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[r], x0, x1, acc[r]);
+    }
+    if (lane * 8 < tail) {
+        const int c = (nfull << 9) + lane * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(xs + c);
+        const float4 x1 = *reinterpret_cast<const float4*>(xs + c + 4);
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            const float s = wave_sum(acc[r]);
-            if (lane == 0 && r0 + r < a.rows) a.y[r0 + r] = RESID ? a.resid[r0 + r] + s : s;
+            const u32x4 w = load_w(wr[r] + (nfull << 9));
+            acc[r] = dot8(w, x0, x1, acc[r]);
+        }
+    }
+    store_rows<EPI, RPW>(a, r0, acc);
+}
+
+// Input staged through registers (n <= 1024 NX): the input loads are issued first, then
+// the first row group's weight loads, then the prologue arithmetic. Loads complete in
+// order for the wait counter, so issuing the input first lets the prologue wait for the
+// input alone while the weights are still in flight.
+template <int PRO, int NX>
+__device__ __forceinline__ void load_input(const GemvArgs& a, float4 (&xv)[NX], float4 (&gv)[NX],
+                                           float4 (&wv)[NX]) {
+    const int tid = threadIdx.x, n = a.in_dim;
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+        const int i = (tid + j * 256) * 4;
+        if (i < n) {
+            xv[j] = *reinterpret_cast<const float4*>(a.x + i);
+            if (PRO == kProRmsNorm) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i);
+            if (PRO == kProGatedNorm) {
+                gv[j] = *reinterpret_cast<const float4*>(a.gate + i);
+                wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i % a.head_dim);
+            }
         }
     }
 }
 
-template <int PRO, bool RESID>
-hipError_t launch_rpw(const GemvArgs& a, hipStream_t s) {
+template <int PRO, int NX>
+__device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX], const float4 (&gv)[NX],
+                                             const float4 (&wv)[NX], float* xs) {
+    const int tid = threadIdx.x, n = a.in_dim;
+    __shared__ double red[4];
+    if (PRO == kProRmsNorm) {
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < NX; ++j)
+            if ((tid + j * 256) * 4 < n)
+                ss += static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
+                      static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
+        ss = block_sum(ss, red);
+        const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + a.eps);
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            xv[j].x = xv[j].x * inv * (1.0f + wv[j].x);
+            xv[j].y = xv[j].y * inv * (1.0f + wv[j].y);
+            xv[j].z = xv[j].z * inv * (1.0f + wv[j].z);
+            xv[j].w = xv[j].w * inv * (1.0f + wv[j].w);
+        }
+    }
+    if (PRO == kProGatedNorm) {
+        // head_dim == 128: a head is 32 consecutive threads' float4s (half a wave)
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+            double ss = static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
+                        static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) ss += __shfl_xor(ss, o);
+            const float inv = 1.0f / sqrtf(static_cast<float>(ss / a.head_dim) + a.eps);
+            xv[j].x = wv[j].x * (xv[j].x * inv) * silu_f(gv[j].x);
+            xv[j].y = wv[j].y * (xv[j].y * inv) * silu_f(gv[j].y);
+            xv[j].z = wv[j].z * (xv[j].z * inv) * silu_f(gv[j].z);
+            xv[j].w = wv[j].w * (xv[j].w * inv) * silu_f(gv[j].w);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+        const int i = (tid + j * 256) * 4;
+        if (i < n) *reinterpret_cast<float4*>(xs + i) = xv[j];
+    }
+    __syncthreads();
+}
+
+template <int PRO, int EPI, int RPW, int NX, int KC>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    extern __shared__ float xs[];
+    const int wave = threadIdx.x >> 6;
+    const int row_step = gridDim.x * 4 * RPW;
+    int r0 = (blockIdx.x * 4 + wave) * RPW;
+    float4 xv[NX > 0 ? NX : 1], gv[NX > 0 ? NX : 1], wv[NX > 0 ? NX : 1];
+    if (NX > 0) load_input<PRO>(a, xv, gv, wv);
+    // The first row group's weights do not depend on the input: their loads are in flight
+    // while the prologue works.
+    u32x4 pf[pf_chunks(KC)][RPW];
+    if (r0 < a.rows) load_rows<RPW, KC>(a, r0, pf);
+    if (NX > 0) finish_input<PRO>(a, xv, gv, wv, xs);
+    else stage_input<PRO>(a, xs);
+    if (r0 >= a.rows) return;
+    if (KC > 0) {
+        // one register set: compute the group in `pf`, then load the next one into it
+        for (;;) {
+            row_group<EPI, RPW, KC, true>(a, xs, r0, pf);
+            r0 += row_step;
+            if (r0 >= a.rows) break;
+            load_rows<RPW, KC>(a, r0, pf);
+        }
+        return;
+    }
+    row_group<EPI, RPW, KC, true>(a, xs, r0, pf);
+    for (r0 += row_step; r0 < a.rows; r0 += row_step) row_group<EPI, RPW, KC, false>(a, xs, r0, pf);
+}
+
+int gemv_max_blocks() {
+    static const int v = [] {
+        const char* e = getenv("Q35_GEMV_MAX_BLOCKS");
+        const int x = e ? atoi(e) : 0;
+        return x > 0 ? x : 2048;
+    }();
+    return v;
+}
+
+template <int PRO, int EPI, int NX, int KC>
+hipError_t launch_kc(const GemvArgs& a, hipStream_t s) {
     const size_t lds = static_cast<size_t>(a.in_dim) * sizeof(float);
-    constexpr int kMaxBlocks = 2048;
-    if (a.rows >= 8192) {
-        const int blocks = min(kMaxBlocks, (a.rows + 7) / 8);
-        gemv_kernel<PRO, RESID, 2><<<blocks, 256, lds, s>>>(a);
+    const int max_blocks = gemv_max_blocks();
+    if (EPI == kEpiSwiGluPair || a.rows >= 8192) {
+        const int blocks = min(max_blocks, (a.rows + 7) / 8);
+        gemv_kernel<PRO, EPI, 2, NX, KC><<<blocks, 256, lds, s>>>(a);
     } else {
-        const int blocks = min(kMaxBlocks, (a.rows + 3) / 4);
-        gemv_kernel<PRO, RESID, 1><<<blocks, 256, lds, s>>>(a);
+        const int blocks = min(max_blocks, (a.rows + 3) / 4);
+        gemv_kernel<PRO, EPI, 1, NX, KC><<<blocks, 256, lds, s>>>(a);
     }
     return hipGetLastError();
 }
 
+// Widths of the model (2048, 4096, 6144) get compile-time chunk counts; the input is
+// staged through registers for widths up to 2048 (the SwiGLU prologue, whose input is
+// twice as wide, and wider inputs stage through LDS directly).
+template <int PRO, int EPI>
+hipError_t launch_rpw(const GemvArgs& a, hipStream_t s) {
+    const bool gated_ok = PRO != kProGatedNorm || a.head_dim == 128;
+    if (PRO != kProSwiGlu) {
+        if (a.in_dim == 2048 && gated_ok) return launch_kc<PRO, EPI, 2, 4>(a, s);
+        if (a.in_dim == 4096) return launch_kc<PRO, EPI, 0, 8>(a, s);
+        if (a.in_dim == 6144) return launch_kc<PRO, EPI, 0, 12>(a, s);
+        if (a.in_dim <= 2048 && gated_ok) return launch_kc<PRO, EPI, 2, 0>(a, s);
+    }
+    return launch_kc<PRO, EPI, 0, 0>(a, s);
+}
+
 template <int PRO>
-hipError_t launch_pro(const GemvArgs& a, hipStream_t s) {
-    return a.resid ? launch_rpw<PRO, true>(a, s) : launch_rpw<PRO, false>(a, s);
+hipError_t launch_pro(const GemvArgs& a, int epi, hipStream_t s) {
+    if (epi == kEpiSwiGluPair) return launch_rpw<PRO, kEpiSwiGluPair>(a, s);
+    return a.resid ? launch_rpw<PRO, kEpiResidual>(a, s) : launch_rpw<PRO, kEpiStore>(a, s);
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s) {
+hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue) {
     switch (prologue) {
-        case kProPlain: return launch_pro<kProPlain>(a, s);
-        case kProRmsNorm: return launch_pro<kProRmsNorm>(a, s);
-        case kProSwiGlu: return launch_pro<kProSwiGlu>(a, s);
-        case kProGatedNorm: return launch_pro<kProGatedNorm>(a, s);
+        case kProPlain: return launch_pro<kProPlain>(a, epilogue, s);
+        case kProRmsNorm: return launch_pro<kProRmsNorm>(a, epilogue, s);
+        case kProSwiGlu: return launch_pro<kProSwiGlu>(a, epilogue, s);
+        case kProGatedNorm: return launch_pro<kProGatedNorm>(a, epilogue, s);
         default: return hipErrorInvalidValue;
     }
 }

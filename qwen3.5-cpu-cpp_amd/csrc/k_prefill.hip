@@ -471,8 +471,8 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnPrefillArgs a) {
 __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* gu, float* h, int T, int I) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < static_cast<int64_t>(T) * I;
          i += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t t = i / I, c = i % I;
-        const float g = gu[t * 2 * I + c], u = gu[t * 2 * I + I + c];
+        const int64_t t = i / I, c = i % I;  // gate / up columns interleaved
+        const float g = gu[t * 2 * I + 2 * c], u = gu[t * 2 * I + 2 * c + 1];
         h[i] = silu_f(g) * u;
     }
 }

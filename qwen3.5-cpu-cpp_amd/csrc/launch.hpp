@@ -27,7 +27,10 @@ struct GemvArgs {
     int rows, in_dim, head_dim;
     float eps;
 };
-hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s);
+// Epilogue: store y, add the residual (the default when resid is set), or, for an
+// interleaved [gate_0; up_0; gate_1; up_1; ...] matrix, y[i] = silu(row 2i) * row 2i+1.
+enum GemvEpilogue : int { kEpiAuto = -1, kEpiStore = 0, kEpiResidual = 1, kEpiSwiGluPair = 2 };
+hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue = kEpiAuto);
 // Largest in_dim the matvec stages in LDS.
 constexpr int kGemvMaxIn = 16384;
 
@@ -149,7 +152,7 @@ struct AttnPrefillArgs {
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
-// h[t][i] = silu(gu[t][i]) * gu[t][I + i]
+// h[t][i] = silu(gu[t][2i]) * gu[t][2i + 1] (gate / up columns interleaved)
 hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s);
 // hidden[t][:] = bf16 embed[ids[t]][:]
 hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s);

@@ -55,7 +55,7 @@ struct LayerDev {
     int idx = 0;
     const uint16_t* w_in = nullptr;   // GDN [qkv|z|b|a] or attention [q|k|v], rows x H
     const uint16_t* w_out = nullptr;  // out_proj / o_proj
-    const uint16_t* w_gu = nullptr;   // [gate|up] 2I x H
+    const uint16_t* w_gu = nullptr;   // gate / up rows interleaved, 2I x H
     const uint16_t* w_down = nullptr; // H x I
     const float* input_ln = nullptr;
     const float* post_ln = nullptr;
@@ -164,6 +164,10 @@ struct Piece {
     const q35_tensor* src;
     size_t off;   // byte offset in the arena
     bool to_f32;  // widen to fp32 (small vectors) instead of keeping bf16
+    // rows interleaved with a second matrix of the same shape: src row i goes to arena row
+    // 2i, partner row i to row 2i + 1
+    const q35_tensor* partner = nullptr;
+    int64_t cols = 0;
 };
 
 int64_t numel_of(const q35_tensor* t) {
@@ -205,6 +209,35 @@ public:
         }
         cursor_ = align256(cursor_ + static_cast<size_t>(rows * cols) * 2);
         if (rows_out) *rows_out = rows;
+        return off;
+    }
+    // Two matrices of equal shape with their rows interleaved (a row, b row, a row, ...):
+    // [gate_proj; up_proj] for the matvec whose epilogue is silu(gate_i) * up_i.
+    size_t mat_interleaved(const std::string& a, const std::string& b, int64_t cols, int64_t* rows_out,
+                           q35_status* st) {
+        const q35_tensor* ta = find(a);
+        const q35_tensor* tb = find(b);
+        if (!ta || !tb) {
+            *st = q35::fail(Q35_ERR_MISSING, "missing weight: %s", (ta ? b : a).c_str());
+            return SIZE_MAX;
+        }
+        if (ta->dtype != 0 || tb->dtype != 0) {
+            *st = q35::fail(Q35_ERR_UNSUPPORTED, "weights %s / %s must be BF16", a.c_str(), b.c_str());
+            return SIZE_MAX;
+        }
+        const int64_t na = numel_of(ta), nb = numel_of(tb);
+        if (na != nb || na % cols != 0 || ta->shape[ta->ndim - 1] != cols) {
+            *st = q35::fail(Q35_ERR_FORMAT, "weights %s / %s: shapes differ or are not [rows][%lld]", a.c_str(),
+                            b.c_str(), static_cast<long long>(cols));
+            return SIZE_MAX;
+        }
+        const size_t off = cursor_;
+        Piece pc{ta, off, false};
+        pc.partner = tb;
+        pc.cols = cols;
+        pieces_.push_back(pc);
+        cursor_ = align256(cursor_ + static_cast<size_t>(2 * na) * 2);
+        if (rows_out) *rows_out = 2 * na / cols;
         return off;
     }
     size_t vec(const std::string& name, int64_t expect, q35_status* st) {
@@ -366,15 +399,15 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
         f1.rows = 2 * I;
         f1.in_dim = H;
         f1.eps = d.rms_norm_eps;
-        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f1, q35k::kProRmsNorm, s); });
+        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f1, q35k::kProRmsNorm, s, q35k::kEpiSwiGluPair); });
         q35k::GemvArgs f2{};
         f2.W = ly.w_down;
-        f2.x = m->gu;
+        f2.x = m->gu;  // silu(gate) * up, I floats
         f2.resid = m->hidden;
         f2.y = m->hidden;
         f2.rows = H;
         f2.in_dim = I;
-        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f2, q35k::kProSwiGlu, s); });
+        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(f2, q35k::kProPlain, s); });
         if (m->trace_on)
             L.run(Q35_KT_OTHER, [&] {
                 return q35k::launch_copy_f32(m->trace + li * H, m->hidden, H, s);
@@ -502,7 +535,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
         o.post_ln = plan.vec(p + "post_attention_layernorm.weight", H, &st);
         if (bad(o.post_ln)) return st;
         int64_t r = 0;
-        o.w_gu = plan.mat({p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"}, H, &r, &st);
+        o.w_gu = plan.mat_interleaved(p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight", H, &r, &st);
         if (bad(o.w_gu)) return st;
         if (r != 2 * I) return q35::fail(Q35_ERR_FORMAT, "layer %d: gate/up rows %lld != 2*%d", l, (long long)r, I);
         o.w_down = plan.mat({p + "mlp.down_proj.weight"}, I, &r, &st);
@@ -615,7 +648,17 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     std::vector<float> tmp;
     for (const Piece& pc : plan.pieces()) {
         const int64_t n = numel_of(pc.src);
-        if (!pc.to_f32) {
+        if (pc.partner) {
+            const int64_t rows = n / pc.cols;
+            const auto* ra = static_cast<const uint16_t*>(pc.src->data);
+            const auto* rb = static_cast<const uint16_t*>(pc.partner->data);
+            std::vector<uint16_t> il(static_cast<size_t>(2 * n));
+            for (int64_t r = 0; r < rows; ++r) {
+                std::memcpy(il.data() + (2 * r) * pc.cols, ra + r * pc.cols, static_cast<size_t>(pc.cols) * 2);
+                std::memcpy(il.data() + (2 * r + 1) * pc.cols, rb + r * pc.cols, static_cast<size_t>(pc.cols) * 2);
+            }
+            HIPCHK(hipMemcpy(m->w_arena + pc.off, il.data(), il.size() * 2, hipMemcpyHostToDevice));
+        } else if (!pc.to_f32) {
             HIPCHK(hipMemcpy(m->w_arena + pc.off, pc.src->data, static_cast<size_t>(n) * 2, hipMemcpyHostToDevice));
         } else {
             tmp.resize(static_cast<size_t>(n));
