@@ -120,38 +120,61 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
             vr[j] = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(row) * kHD + lane * 4);
         }
     };
-    if (w0 < w1) load(kA, vA, w0);  // first batch in flight during the prologue
-
-    // ---- prologue: q_norm + RoPE of the GRP query rows (and k_norm + RoPE of the new key)
+    // ---- prologue loads, then the first two K / V batches, all unconditional (rows clamped
+    // into valid ones): a load under a branch makes the wait-count insertion wait for every
+    // outstanding load, so the prologue would wait for the K / V batches.
     const int half = a.ROT / 2;
-    if (tid < half) {
-        const double inv_freq = pow(a.theta, -static_cast<double>(2 * tid) / a.ROT);
-        const double ang = static_cast<double>(pos) * inv_freq;
-        cs_s[0][tid] = static_cast<float>(cos(ang));
-        cs_s[1][tid] = static_cast<float>(sin(ang));
-    }
     const int nrow = owns_new ? NROW : GRP;
-    for (int r = wave; r < nrow; r += kWaves) {
+    constexpr int RW = (NROW + kWaves - 1) / kWaves;  // prologue rows per wave
+    float4 px[RW], pw[RW];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+        const int r = min(wave + i * kWaves, nrow - 1);
         const bool is_q = r < GRP;
         const float* src = is_q ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
                                 : a.k_new + static_cast<int64_t>(kh) * kHD;
         const float* w = is_q ? a.q_norm : a.k_norm;
-        const float4 x = *reinterpret_cast<const float4*>(src + lane * 4);
+        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
+        pw[i] = *reinterpret_cast<const float4*>(w + lane * 4);
+    }
+    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    float csv0 = 0.0f, csv1 = 0.0f;
+    if (a.rope_cs) {  // uniform: the table row of this position
+        const int i = min(lane, max(half - 1, 0));
+        csv0 = a.rope_cs[static_cast<int64_t>(pos) * a.ROT + i];
+        csv1 = a.rope_cs[static_cast<int64_t>(pos) * a.ROT + half + i];
+    }
+    load(kA, vA, w0);
+    if constexpr (DBUF) load(kB, vB, w0 + kBatch);
+
+    // ---- prologue: q_norm + RoPE of the GRP query rows (and k_norm + RoPE of the new key)
+    if (tid < half) {
+        if (a.rope_cs) {  // precomputed with the same double-precision formula
+            cs_s[0][tid] = csv0;
+            cs_s[1][tid] = csv1;
+        } else {
+            const double inv_freq = pow(a.theta, -static_cast<double>(2 * tid) / a.ROT);
+            const double ang = static_cast<double>(pos) * inv_freq;
+            cs_s[0][tid] = static_cast<float>(cos(ang));
+            cs_s[1][tid] = static_cast<float>(sin(ang));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+        const int r = wave + i * kWaves;
+        const float4 x = px[i], wv = pw[i];
         double ss = static_cast<double>(x.x) * x.x + static_cast<double>(x.y) * x.y +
                     static_cast<double>(x.z) * x.z + static_cast<double>(x.w) * x.w;
         ss = wave_sum(ss);
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + a.eps);
-        const float4 wv = *reinterpret_cast<const float4*>(w + lane * 4);
         float4 y;
         y.x = x.x * inv * (1.0f + wv.x);
         y.y = x.y * inv * (1.0f + wv.y);
         y.z = x.z * inv * (1.0f + wv.z);
         y.w = x.w * inv * (1.0f + wv.w);
-        *reinterpret_cast<float4*>(&rows_s[r][lane * 4]) = y;
+        if (r < nrow) *reinterpret_cast<float4*>(&rows_s[r][lane * 4]) = y;
     }
-    if (owns_new && tid < kHD / 4)
-        *reinterpret_cast<float4*>(&vnew_s[tid * 4]) =
-            *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + tid * 4);
+    if (owns_new && wave == 0) *reinterpret_cast<float4*>(&vnew_s[lane * 4]) = vn4;
     __syncthreads();
     for (int t = tid; t < nrow * half; t += kWaves * 64) {
         const int r = t / half, i = t - r * half;
@@ -245,7 +268,7 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     if constexpr (DBUF) {
         for (int b0 = w0; b0 < w1; b0 += 2 * kBatch) {
             const int b1 = b0 + kBatch;
-            if (b1 < w1) load(kB, vB, b1);
+            if (b0 != w0 && b1 < w1) load(kB, vB, b1);  // the first B batch is loaded above
             consume(kA, vA, b0);
             if (b1 >= w1) break;
             if (b1 + kBatch < w1) load(kA, vA, b1 + kBatch);
@@ -263,39 +286,60 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
         ml_s[wave][pl / OWN][0] = m_run;
         ml_s[wave][pl / OWN][1] = l_run;
     }
-    __syncthreads();
+    const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
+    if constexpr (GRP <= 8) {
+        // every wave's accumulators to LDS, one barrier, each thread merges its outputs
+        __shared__ float redw[kWaves][GRP][kHD];
 #pragma unroll
-    for (int h = 0; h < GRP; ++h) {
-        float M = ml_s[0][h][0];
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][h][0]);
-        const float mw = ml_s[wave][h][0];
-        const float g = mw == -INFINITY ? 0.0f : expf(mw - M);
-        acc[h].x *= g;
-        acc[h].y *= g;
-        acc[h].z *= g;
-        acc[h].w *= g;
-    }
-    for (int w = 0; w < kWaves; ++w) {
-        if (wave == w) {
+        for (int h = 0; h < GRP; ++h) *reinterpret_cast<float4*>(&redw[wave][h][lane * 4]) = acc[h];
+        __syncthreads();
+        for (int i = tid; i < GRP * kHD; i += kWaves * 64) {
+            const int h = i / kHD, dd = i - h * kHD;
+            float M = ml_s[0][h][0];
 #pragma unroll
-            for (int h = 0; h < GRP; ++h) {
-                float4* r = reinterpret_cast<float4*>(&red[h][lane * 4]);
-                if (w == 0) {
-                    *r = acc[h];
-                } else {
-                    float4 t = *r;
-                    t.x += acc[h].x;
-                    t.y += acc[h].y;
-                    t.z += acc[h].z;
-                    t.w += acc[h].w;
-                    *r = t;
+            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            float o = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float mw = ml_s[w][h][0];
+                if (mw != -INFINITY) o = fmaf(redw[w][h][dd], expf(mw - M), o);
+            }
+            a.part_o[base * kHD + i] = o;
+        }
+    } else {
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            float M = ml_s[0][h][0];
+            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            const float mw = ml_s[wave][h][0];
+            const float g = mw == -INFINITY ? 0.0f : expf(mw - M);
+            acc[h].x *= g;
+            acc[h].y *= g;
+            acc[h].z *= g;
+            acc[h].w *= g;
+        }
+        for (int w = 0; w < kWaves; ++w) {
+            if (wave == w) {
+#pragma unroll
+                for (int h = 0; h < GRP; ++h) {
+                    float4* r = reinterpret_cast<float4*>(&red[h][lane * 4]);
+                    if (w == 0) {
+                        *r = acc[h];
+                    } else {
+                        float4 t = *r;
+                        t.x += acc[h].x;
+                        t.y += acc[h].y;
+                        t.z += acc[h].z;
+                        t.w += acc[h].w;
+                        *r = t;
+                    }
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
+        for (int i = tid; i < GRP * kHD; i += kWaves * 64) a.part_o[base * kHD + i] = red[i / kHD][i % kHD];
     }
-    const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
-    for (int i = tid; i < GRP * kHD; i += kWaves * 64) a.part_o[base * kHD + i] = red[i / kHD][i % kHD];
     if (tid < GRP) {
         float M = ml_s[0][tid][0];
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, ml_s[w][tid][0]);

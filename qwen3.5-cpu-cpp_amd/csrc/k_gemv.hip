@@ -224,16 +224,17 @@ template <int PRO, int NX>
 __device__ __forceinline__ void load_input(const GemvArgs& a, float4 (&xv)[NX], float4 (&gv)[NX],
                                            float4 (&wv)[NX]) {
     const int tid = threadIdx.x, n = a.in_dim;
+    // Unconditional loads (indices clamped into the vector, surplus lanes masked later): a
+    // load under a branch makes the wait-count insertion fall back to waiting for every
+    // outstanding load, the weight prefetch included.
 #pragma unroll
     for (int j = 0; j < NX; ++j) {
-        const int i = (tid + j * 256) * 4;
-        if (i < n) {
-            xv[j] = *reinterpret_cast<const float4*>(a.x + i);
-            if (PRO == kProRmsNorm) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i);
-            if (PRO == kProGatedNorm) {
-                gv[j] = *reinterpret_cast<const float4*>(a.gate + i);
-                wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i % a.head_dim);
-            }
+        const int i = min((tid + j * 256) * 4, n - 4);
+        xv[j] = *reinterpret_cast<const float4*>(a.x + i);
+        if (PRO == kProRmsNorm) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i);
+        if (PRO == kProGatedNorm) {
+            gv[j] = *reinterpret_cast<const float4*>(a.gate + i);
+            wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i % a.head_dim);
         }
     }
 }
@@ -294,7 +295,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     // The first row group's weights do not depend on the input: their loads are in flight
     // while the prologue works.
     u32x4 pf[pf_chunks(KC)][RPW];
-    if (r0 < a.rows) load_rows<RPW, KC>(a, r0, pf);
+    load_rows<RPW, KC>(a, r0, pf);  // rows clamped: unconditional, see load_input
     if (NX > 0) finish_input<PRO>(a, xv, gv, wv, xs);
     else stage_input<PRO>(a, xs);
     if (r0 >= a.rows) return;

@@ -157,6 +157,19 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float* dst, int64_t n,
         dst[i] = static_cast<float>(std * normal_at(key, static_cast<uint64_t>(i)));
 }
 
+__global__ __launch_bounds__(256) void rope_table_kernel(float* t, int64_t n_pos, int rot, double theta) {
+    const int half = rot / 2;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_pos * half;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t p = i / half;
+        const int k = static_cast<int>(i - p * half);
+        const double inv_freq = pow(theta, -static_cast<double>(2 * k) / rot);
+        const double ang = static_cast<double>(p) * inv_freq;
+        t[p * rot + k] = static_cast<float>(cos(ang));
+        t[p * rot + half + k] = static_cast<float>(sin(ang));
+    }
+}
+
 int grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return static_cast<int>(b < 4096 ? (b > 0 ? b : 1) : 4096);
@@ -218,6 +231,12 @@ hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s) {
 
 hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s) {
     fill_normal_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, key, std);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_table(float* t, int64_t n_pos, int rot, double theta, hipStream_t s) {
+    if (rot <= 0) return hipSuccess;
+    rope_table_kernel<<<grid_for(n_pos * (rot / 2)), 256, 0, s>>>(t, n_pos, rot, theta);
     return hipGetLastError();
 }
 

@@ -70,6 +70,7 @@ struct AttnDecodeArgs {
     double theta;
     float eps;
     const float *qg, *k_new, *v_new, *q_norm, *k_norm;
+    const float* rope_cs;       // optional [max_ctx][ROT]: cos (ROT/2) then sin (ROT/2) per position
     float *k_cache, *v_cache;   // [NKV][max_ctx][HD]
     float* part_o;              // [NKV][n_splits][GRP][HD]
     float* part_ml;             // [NKV][n_splits][GRP][2]
@@ -178,5 +179,8 @@ hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t 
 hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s);
 // dst[i] = std * N(0,1)(key, i)
 hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s);
+// t[p][i] = cos(p * theta^(-2i/rot)), t[p][rot/2 + i] = sin(...) for i < rot/2, in double
+// rounded to float (the apply_rope formula, src/forward_pass.cpp:102-112)
+hipError_t launch_rope_table(float* t, int64_t n_pos, int rot, double theta, hipStream_t s);
 
 }  // namespace q35k

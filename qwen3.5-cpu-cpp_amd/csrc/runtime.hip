@@ -94,6 +94,7 @@ struct q35_model {
 
     float *hidden = nullptr, *proj = nullptr, *mix = nullptr, *gu = nullptr;
     float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr, *trace = nullptr;
+    float* rope_cs = nullptr;  // [max_context][ROT] RoPE cos / sin table
     void* argmax_part = nullptr;
     int *token_dev = nullptr, *pos_dev = nullptr, *ids_dev = nullptr;
     int n_splits = 0;
@@ -374,6 +375,7 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
             aa.v_new = m->proj + 2 * NQ * HD + NKV * HD;
             aa.q_norm = ly.q_norm;
             aa.k_norm = ly.k_norm;
+            aa.rope_cs = m->rope_cs;
             aa.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
             aa.v_cache = aa.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
             aa.part_o = m->part_o;
@@ -626,6 +628,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     const size_t o_am = take(static_cast<size_t>(2) * q35k::kArgmaxBlocks * 4);
     const size_t o_ints = take(16 * 4);
     const size_t o_ids = take(static_cast<size_t>(max_ctx) * 4);
+    const size_t o_rope = take(static_cast<size_t>(max_ctx) * std::max(1, rot_dims(d)) * 4);
     m->scratch_bytes = sc;
     m->w_bytes = plan.bytes();
 
@@ -718,11 +721,13 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->token_dev = ints;
     m->pos_dev = ints + 1;
     m->ids_dev = reinterpret_cast<int*>(m->scratch + o_ids);
+    m->rope_cs = S32(o_rope);
 
     // reset: zero state, kv and scratch with fill kernels
     HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
     HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
     HIPCHK(q35k::launch_fill_f32(reinterpret_cast<float*>(m->scratch), static_cast<int64_t>(m->scratch_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_rope_table(m->rope_cs, max_ctx, rot_dims(d), d.rope_theta, m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
 
     m->budget.weight_bytes = m->w_bytes;
