@@ -37,28 +37,51 @@ __device__ __forceinline__ int split_len(int n, int n_splits) { return (n + n_sp
 
 // Reduce GRP per-lane partial sums over groups of LPP lanes. On return lane l holds in v[0]
 // the full sum of query head `head`.
-template <int GRP, int LPP>
-__device__ __forceinline__ void butterfly(float (&v)[GRP], int lane, int& head) {
-    head = 0;
-    int cnt = GRP;
+// Value of the partner lane of the butterfly stage on lane bit `o`. The partner differs
+// from this lane in bit o (and for o = 4, 8 also in the lower bits: the half-row and row
+// mirrors i <-> 7-i, i <-> 15-i); the pairings of the five stages (xor 16, 15, 7, 2, 1)
+// span all 32 lanes of a group, so the butterfly still sums every lane exactly once.
+// DPP and swizzle move data without the address arithmetic of a generic shuffle.
+__device__ __forceinline__ float xchg(float v, int o) {
+    const int x = __builtin_bit_cast(int, v);
+    int r;
+    switch (o) {
+        case 1: r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;   // quad xor 1
+        case 2: r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;   // quad xor 2
+        case 4: r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;  // half-row mirror
+        case 8: r = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break;  // row mirror
+        case 16: r = __builtin_amdgcn_ds_swizzle(x, 0x401F); break;                      // xor 16 in 32
+        default: r = __builtin_bit_cast(int, __shfl_xor(v, o)); break;
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+template <int N>
+using fvec = float __attribute__((ext_vector_type(N)));
+
+// Halving butterfly over lane bits O, O/2, ..., 1 (O = LPP / 2): each lane starts with the
+// partial dots of N query heads; at each stage the lane keeps the half of the heads its
+// bit selects, adds the partner's partials of that half and sends the other half. After
+// log2(N) stages a lane holds one head (bits of the lane give its index), the remaining
+// stages finish the sum over the LPP lanes. The halves are whole vectors selected by a
+// scalar condition, so no per-element dynamic indexing is generated.
+template <int N, int O>
+__device__ __forceinline__ float butterfly(fvec<N> v, int lane) {
+    if constexpr (O == 0) {
+        return v[0];
+    } else if constexpr (N == 1) {
+        fvec<1> t;
+        t[0] = v[0] + xchg(v[0], O);
+        return butterfly<1, O / 2>(t, lane);
+    } else {
+        const bool up = (lane & O) != 0;
+        const fvec<N / 2> lo = v.lo, hi = v.hi;
+        const fvec<N / 2> send = up ? lo : hi;
+        const fvec<N / 2> keep = up ? hi : lo;
+        fvec<N / 2> r;
 #pragma unroll
-    for (int o = LPP / 2; o >= 1; o >>= 1) {
-        if (cnt > 1) {
-            const int half = cnt / 2;
-            const bool up = (lane & o) != 0;
-#pragma unroll
-            for (int i = 0; i < GRP / 2; ++i) {
-                if (i < half) {
-                    const float send = up ? v[i] : v[i + half];
-                    const float keep = up ? v[i + half] : v[i];
-                    v[i] = keep + __shfl_xor(send, o);
-                }
-            }
-            if (up) head += half;
-            cnt = half;
-        } else {
-            v[0] += __shfl_xor(v[0], o);
-        }
+        for (int i = 0; i < N / 2; ++i) r[i] = keep[i] + xchg(send[i], O);
+        return butterfly<N / 2, O / 2>(r, lane);
     }
 }
 
@@ -67,6 +90,16 @@ constexpr int kWaves = 8;   // waves per workgroup
 // lane holding the full score of query head h (for lane group `sub`) after the butterfly
 template <int GRP, int LPP>
 __device__ __forceinline__ constexpr int head_lane(int sub, int h) { return sub * LPP + h * (LPP / GRP); }
+
+// K / V rows are streamed with non-temporal loads: they are read once per token, and
+// allocating them in the caches evicts dirty lines whose write-back competes with the
+// stream (measured: 2.7 TB/s with plain loads against 6.2 TB/s non-temporal for the same
+// K + V stream behind a cache full of dirty data).
+__device__ __forceinline__ float4 load_stream(const float* p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -112,12 +145,12 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
             const int row = min(b0 + it * PPW + sub, w1 - 1);
             const float* src = K + static_cast<int64_t>(row) * kHD + pl * 4;
 #pragma unroll
-            for (int m = 0; m < NF4; ++m) kr[it][m] = *reinterpret_cast<const float4*>(src + m * LPP * 4);
+            for (int m = 0; m < NF4; ++m) kr[it][m] = load_stream(src + m * LPP * 4);
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const int row = min(b0 + j, w1 - 1);
-            vr[j] = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(row) * kHD + lane * 4);
+            vr[j] = load_stream(V + static_cast<int64_t>(row) * kHD + lane * 4);
         }
     };
     // ---- prologue loads, then the first two K / V batches, all unconditional (rows clamped
@@ -209,7 +242,7 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
 #pragma unroll
                 for (int m = 0; m < NF4; ++m)
                     kr[it][m] = *reinterpret_cast<const float4*>(&rows_s[GRP][pl * 4 + m * LPP * 4]);
-            float d[GRP];
+            fvec<GRP> d;
 #pragma unroll
             for (int h = 0; h < GRP; ++h) {
                 float t = 0.0f;
@@ -222,9 +255,8 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
                 }
                 d[h] = t;
             }
-            int head;
-            butterfly<GRP, LPP>(d, lane, head);
-            s[it] = p < w1 ? d[0] * sc : -INFINITY;
+            const float score = butterfly<GRP, LPP / 2>(d, lane);
+            s[it] = p < w1 ? score * sc : -INFINITY;
         }
         float cmax = s[0];
 #pragma unroll
