@@ -1,18 +1,25 @@
-// Token-batched projection GEMM for the prefill: Y[M][N] = (R ?) + X[M][K] . W[N][K]^T (K % 8 == 0) with
-// fp32 activations X, bf16 weights W (nn.Linear row-major layout, widened exactly) and fp32
-// accumulation on the matrix cores (v_mfma_f32_32x32x2_f32). This is the reference's
-// per-token matmul (src/forward_pass.cpp:44-75) for all prompt tokens at once.
+// Token-batched projection GEMM for the prefill: Y[M][N] = (R ?) + X[M][K] . W[N][K]^T (K % 8 == 0)
+// with fp32 activations X, bf16 weights W (nn.Linear row-major layout) and fp32 results: the
+// reference's per-token matmul (src/forward_pass.cpp:44-75) for all prompt tokens at once.
+//
+// Exact three-way bf16 split on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16). Every fp32
+// x is the exact sum of three bf16 values: hi = x with its low 16 bits cleared, r = x - hi
+// (exact, at most 16 significant bits), mid = r with its low 16 bits cleared, lo = r - mid
+// (exact, at most 8 significant bits, so a bf16). A bf16 x bf16 product has at most 16
+// significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul with
+// fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one fp32 MFMA.
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, 4 waves in a 2 x 2 arrangement of
 // 64 x 64 quadrants, each quadrant 2 x 2 MFMA blocks of 32 x 32 (64 accumulator registers
-// per lane). K advances in stages of 32: the X and W tiles of the next stage are loaded
-// into registers while the current stage runs from LDS. LDS keeps both tiles k-major
-// ([k][m], [k][n]) so every operand read is 32 consecutive floats across lanes.
+// per lane). K advances in stages of 32: the X and W tiles of the next stage are loaded into
+// registers while the current stage runs from LDS. LDS holds the three bf16 parts of the X
+// tile and the W tile k-contiguous ([row][k], rows padded to 40 elements), so each MFMA
+// operand is one 16-byte read of 8 consecutive k.
 //
-// MFMA operand layout (32x32x2, one block): lane l supplies A[l % 32][l / 32] and
-// B[l / 32][l % 32]; the result register v of lane l is D[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
-// The two k slots of each instruction take k = 16 (l / 32) + s at step s, a fixed
-// permutation of the stage's 32 k values applied to both operands.
+// MFMA operand layout (32x32x16 bf16, one block): lane l supplies row / column l % 32 and the 8
+// k values 8 (l / 32) .. 8 (l / 32) + 7 of the 16-k step; both operands use the same k
+// assignment, so the sum covers all 16. The result register v of lane l is
+// D[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
 #include "dev_common.hpp"
 #include "launch.hpp"
 
@@ -20,13 +27,26 @@ namespace q35k {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kLd = kBK + 8;  // padded row (bf16 elements): 80 B, rows start on distinct banks
+
+// x = hi + mid + lo exactly, each a bf16 (returned as its 16-bit pattern)
+__device__ __forceinline__ void split3(float x, uint32_t& h, uint32_t& m, uint32_t& l) {
+    const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+    const float r1 = x - __uint_as_float(hb);
+    const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+    const float r2 = r1 - __uint_as_float(mb);
+    h = hb >> 16;
+    m = mb >> 16;
+    l = __float_as_uint(r2) >> 16;
+}
 
 template <bool RESID>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-    __shared__ float As[kBK][kBM + 4];
-    __shared__ float Bs[kBK][kBN + 4];
+    __shared__ __align__(16) uint16_t Xs[3][kBM][kLd];
+    __shared__ __align__(16) uint16_t Ws[kBN][kLd];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
@@ -50,21 +70,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                                                   : make_uint4(0u, 0u, 0u, 0u);
     };
     auto store_stage = [&]() {
+        uint32_t hp[8], mp[8], lp[8];  // pairs of bf16 packed in a word
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            As[lk + 4 * i + 0][lr] = ra[i].x;
-            As[lk + 4 * i + 1][lr] = ra[i].y;
-            As[lk + 4 * i + 2][lr] = ra[i].z;
-            As[lk + 4 * i + 3][lr] = ra[i].w;
+            const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                uint32_t h0, m0_, l0, h1, m1, l1;
+                split3(v[j], h0, m0_, l0);
+                split3(v[j + 1], h1, m1, l1);
+                hp[2 * i + j / 2] = h0 | (h1 << 16);
+                mp[2 * i + j / 2] = m0_ | (m1 << 16);
+                lp[2 * i + j / 2] = l0 | (l1 << 16);
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t w4[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                Bs[lk + 8 * i + 2 * j][lr] = bf16_lo(w4[j]);
-                Bs[lk + 8 * i + 2 * j + 1][lr] = bf16_hi(w4[j]);
-            }
+        for (int q = 0; q < 2; ++q) {
+            *reinterpret_cast<uint4*>(&Xs[0][lr][lk + 8 * q]) = make_uint4(hp[4 * q], hp[4 * q + 1], hp[4 * q + 2], hp[4 * q + 3]);
+            *reinterpret_cast<uint4*>(&Xs[1][lr][lk + 8 * q]) = make_uint4(mp[4 * q], mp[4 * q + 1], mp[4 * q + 2], mp[4 * q + 3]);
+            *reinterpret_cast<uint4*>(&Xs[2][lr][lk + 8 * q]) = make_uint4(lp[4 * q], lp[4 * q + 1], lp[4 * q + 2], lp[4 * q + 3]);
+            *reinterpret_cast<uint4*>(&Ws[lr][lk + 8 * q]) = rb[q];
         }
     };
 
@@ -76,7 +101,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int am = wm * 64 + (lane & 31), bn = wn * 64 + (lane & 31), kg = (lane >> 5) * 16;
+    const int ar = wm * 64 + (lane & 31), br = wn * 64 + (lane & 31), kh = (lane >> 5) * 8;
     load_stage(0);
     for (int k0 = 0; k0 < a.K; k0 += kBK) {
         __syncthreads();
@@ -84,13 +109,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         __syncthreads();
         if (k0 + kBK < a.K) load_stage(k0 + kBK);
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const float a0 = As[kg + s][am], a1 = As[kg + s][am + 32];
-            const float b0 = Bs[kg + s][bn], b1 = Bs[kg + s][bn + 32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        for (int s = 0; s < kBK / 16; ++s) {
+            const int kk = s * 16 + kh;
+            bf16x8 bop[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bop[j] = *reinterpret_cast<const bf16x8*>(&Ws[br + 32 * j][kk]);
+#pragma unroll
+            for (int p = 2; p >= 0; --p) {  // lo, mid, hi
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const bf16x8 aop = *reinterpret_cast<const bf16x8*>(&Xs[p][ar + 32 * i][kk]);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[j], acc[i][j], 0, 0, 0);
+                }
+            }
         }
     }
 #pragma unroll
