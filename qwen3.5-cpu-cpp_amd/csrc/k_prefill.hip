@@ -13,11 +13,12 @@
 //              A[i][j] = beta_i k_i.k_j e^(gamma_i - gamma_j)  (j < i)
 //              [U | W] = (I + A)^-1 [beta v | beta e^gamma k]  (forward substitution, one
 //                                                               column per thread, in registers)
-//   scan     per (v-head, 16-column slice of the state), sequential over the chunks:
-//              v_new = U - W S;  o = e^gamma (Q S) + P v_new;
+//   state    per (v-head, 16-column slice of the state), sequential over the chunks, on the
+//            fp32 matrix cores: store the chunk-start state S_c, v_new = U - W S,
 //              S <- e^(gamma_last) S + K^T (e^(gamma_last - gamma) v_new)
 //            The delta rule is column-separable, so the 8 slices of a head are independent.
-//   norm     rmsnorm_gated per (token, v-head) (src/forward_pass.cpp:86-93).
+//   output   per (v-head, chunk), in parallel: o = e^gamma (Q S_c) + P v_new on the matrix
+//            cores, then rmsnorm_gated per (token, v-head) (src/forward_pass.cpp:86-93).
 // Causal attention, flash form on the matrix cores (v_mfma_f32_16x16x4_f32):
 //   prep     q_norm + RoPE of every query row (head-major), k_norm + RoPE of every key and
 //            the values appended to the KV cache at pos0 + t (angles in double).
@@ -34,7 +35,6 @@ namespace {
 
 constexpr int kD = 128;   // GDN head dim
 constexpr int kC = 64;    // chunk length
-constexpr int kCW = 16;   // state columns per scan workgroup
 constexpr int kHD = 256;  // attention head dim
 
 // ------------------------------------------------------------------ GDN prep
@@ -194,100 +194,186 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
     for (int i = 0; i < kC; ++i) dst[static_cast<int64_t>(i) * kD] = col[i];
 }
 
-// ------------------------------------------------------------------ GDN scan
-// grid (VH, 128 / kCW), 256 threads; sequential over the chunks.
-__global__ __launch_bounds__(256) void gdn_scan_kernel(GdnPrefillArgs a) {
-    const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
-    const int kh = vh / (a.VH / a.KH);
-    const int col0 = cs * kCW;
-    __shared__ float Ws[kC][kD + 1];
-    __shared__ float Qs[kC][kD + 1];
-    __shared__ float Ks[kC][kD + 1];
-    __shared__ float Ss[kD][kCW];
-    __shared__ float Vn[kC][kCW];
-    __shared__ float Ps[kC][kC + 1];
-    __shared__ float gam[kC];
-    float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
-    for (int i = tid; i < kD * kCW; i += 256) Ss[i / kCW][i % kCW] = S[(i / kCW) * kD + col0 + i % kCW];
-    const int nchunk = a.Tp / kC;
-    const int cc = tid % kCW, grp = tid / kCW;  // column, row group (16 groups)
-    for (int c = 0; c < nchunk; ++c) {
-        const int64_t row0 = static_cast<int64_t>(c) * kC;
-        __syncthreads();  // previous chunk done with the tiles
-        const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
-        const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-        const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-        for (int i = tid; i < kC * kD; i += 256) {
-            Ws[i / kD][i % kD] = W[i];
-            Qs[i / kD][i % kD] = Q[i];
-            Ks[i / kD][i % kD] = K[i];
-        }
-        const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
-        for (int i = tid; i < kC * kC; i += 256) Ps[i / kC][i % kC] = P[i];
-        if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
-        __syncthreads();
-        // v_new = U - W S and the inter-chunk readout e^gamma (Q S), rows grp*4 .. +3
-        float vn[4], oi[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vn[r] = oi[r] = 0.0f;
-        for (int k = 0; k < kD; ++k) {
-            const float s = Ss[k][cc];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                vn[r] = fmaf(Ws[grp * 4 + r][k], s, vn[r]);
-                oi[r] = fmaf(Qs[grp * 4 + r][k], s, oi[r]);
-            }
-        }
-        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0 + cc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = grp * 4 + r;
-            vn[r] = U[static_cast<int64_t>(i) * kD] - vn[r];
-            Vn[i][cc] = vn[r];
-            oi[r] *= expf(gam[i]);
-        }
-        __syncthreads();
-        // intra-chunk: o_i += sum_{j <= i} P[i][j] v_new_j
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = grp * 4 + r;
-            float o = oi[r];
-            for (int j = 0; j <= i; ++j) o = fmaf(Ps[i][j], Vn[j][cc], o);
-            const int64_t t = row0 + i;
-            if (t < a.T) a.O[t * (a.VH * kD) + vh * kD + col0 + cc] = o;
-        }
-        // state: S <- e^(gamma_last) S + K^T (e^(gamma_last - gamma) v_new); rows grp*8 .. +7
-        const float glast = gam[kC - 1];
-        float sn[8];
-        const float dlast = expf(glast);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) sn[r] = Ss[grp * 8 + r][cc] * dlast;
-        for (int i = 0; i < kC; ++i) {
-            const float w = expf(glast - gam[i]) * Vn[i][cc];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) sn[r] = fmaf(Ks[i][grp * 8 + r], w, sn[r]);
-        }
-        __syncthreads();  // every thread has read Ss for this chunk
-#pragma unroll
-        for (int r = 0; r < 8; ++r) Ss[grp * 8 + r][cc] = sn[r];
-    }
-    __syncthreads();
-    for (int i = tid; i < kD * kCW; i += 256) S[(i / kCW) * kD + col0 + i % kCW] = Ss[i / kCW][i % kCW];
+// ------------------------------------------------------------------ GDN state scan
+// v_mfma_f32_16x16x4_f32, one block: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// result register v of lane l is D[4 (l / 16) + v][l % 16].
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// ------------------------------------------------------------------ GDN gated norm
-// grid (T, VH), 128 threads: out = w * (o * rsqrt(mean(o^2) + eps)) * silu(z)
-__global__ __launch_bounds__(128) void gdn_gated_norm_kernel(GdnPrefillArgs a) {
-    const int t = blockIdx.x, vh = blockIdx.y, i = threadIdx.x;
-    __shared__ double red[2];
-    const int64_t off = static_cast<int64_t>(t) * (a.VH * kD) + vh * kD + i;
-    const float o = a.O[off];
-    double ss = wave_sum(static_cast<double>(o) * o);
-    if ((i & 63) == 0) red[i >> 6] = ss;
+constexpr int kSW = 16;        // state columns per state-scan workgroup
+constexpr int kLdW = kD + 4;   // -W rows in LDS (A operand: 16 rows x 4 k per read, conflict-free)
+constexpr int kLdK = kD + 16;  // decayed K rows in LDS (A operand read transposed)
+
+// grid (VH, 128 / kSW), 256 threads: sequential over the chunks of one state column slice.
+// Per chunk: store the chunk-start state, v_new = U - W S (written over U), then
+// S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Wave w computes v_new rows
+// [16w, 16w + 16) and the new state rows [32w, 32w + 32). The next chunk's W and K are
+// loaded into registers while the current one is computed.
+__global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
+    const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int kh = vh / (a.VH / a.KH);
+    const int col0 = cs * kSW;
+    const int nchunk = a.Tp / kC;
+    __shared__ float Ss[kD][kSW];
+    __shared__ float VN[kC][kSW];
+    __shared__ float Wl[kC][kLdW];
+    __shared__ float Kl[kC][kLdK];
+    float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
+    for (int i = tid; i < kD * kSW; i += 256) Ss[i / kSW][i % kSW] = S[(i / kSW) * kD + col0 + i % kSW];
+
+    // staging map: float4 f = tid + 256 i (i < 8) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32)
+    float4 rw[8], rk[8];
+    auto load_chunk = [&](int c) {
+        const int64_t row0 = static_cast<int64_t>(c) * kC;
+        const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
+        const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = tid + 256 * i;
+            rw[i] = *reinterpret_cast<const float4*>(W + (f >> 5) * kD + (f & 31) * 4);
+            rk[i] = *reinterpret_cast<const float4*>(K + (f >> 5) * kD + (f & 31) * 4);
+        }
+    };
+    auto store_chunk = [&](int c) {
+        const float* gam = a.Gam + static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC;
+        const float glast = gam[kC - 1];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = tid + 256 * i, r = f >> 5, c4 = (f & 31) * 4;
+            const float d = expf(glast - gam[r]);
+            Wl[r][c4 + 0] = -rw[i].x;
+            Wl[r][c4 + 1] = -rw[i].y;
+            Wl[r][c4 + 2] = -rw[i].z;
+            Wl[r][c4 + 3] = -rw[i].w;
+            Kl[r][c4 + 0] = rk[i].x * d;
+            Kl[r][c4 + 1] = rk[i].y * d;
+            Kl[r][c4 + 2] = rk[i].z * d;
+            Kl[r][c4 + 3] = rk[i].w * d;
+        }
+    };
+    load_chunk(0);
+    for (int c = 0; c < nchunk; ++c) {
+        __syncthreads();  // previous chunk done with Wl / Kl / Ss
+        store_chunk(c);
+        // chunk-start state for the output pass
+        float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
+        for (int i = tid; i < kD * kSW; i += 256) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
+        const float glast = a.Gam[static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC + kC - 1];
+        __syncthreads();
+        if (c + 1 < nchunk) load_chunk(c + 1);
+
+        // v_new rows [16w, 16w + 16) = U - W S
+        float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
+        floatx4 vn;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) vn[v] = U[(16 * wave + 4 * lg + v) * kD + lr];
+#pragma unroll 8
+        for (int k = 0; k < kD; k += 4) vn = mfma4(Wl[16 * wave + lr][k + lg], Ss[k + lg][lr], vn);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            U[(16 * wave + 4 * lg + v) * kD + lr] = vn[v];
+            VN[16 * wave + 4 * lg + v][lr] = vn[v];
+        }
+        __syncthreads();  // VN complete, every wave done reading Ss
+
+        // new state rows [32w, 32w + 32), one 16-row block at a time. Each block is written
+        // back right after its product: with both blocks' eight stores in one basic block this
+        // compiler paired two of them into a ds_write2_b32 with a wrong offset (the state of
+        // row 16 landed in row 3).
+        const float dl = expf(glast);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            float* srow = &Ss[32 * wave + 16 * rb + 4 * lg][lr];
+            floatx4 sn;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sn[v] = srow[v * kSW] * dl;
+#pragma unroll 4
+            for (int t = 0; t < kC; t += 4) sn = mfma4(Kl[t + lg][32 * wave + 16 * rb + lr], VN[t + lg][lr], sn);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) srow[v * kSW] = sn[v];
+        }
+    }
     __syncthreads();
-    const float inv = 1.0f / sqrtf(static_cast<float>((red[0] + red[1]) / kD) + a.eps);
-    const float z = a.z[static_cast<int64_t>(t) * a.ld_z + vh * kD + i];
-    a.out[off] = a.norm_w[i] * (o * inv) * silu_f(z);
+    for (int i = tid; i < kD * kSW; i += 256) S[(i / kSW) * kD + col0 + i % kSW] = Ss[i / kSW][i % kSW];
+}
+
+// ------------------------------------------------------------------ GDN chunk output
+constexpr int kLdQ = kD + 4;    // Q rows (A operand)
+constexpr int kLdS = kD + 16;   // state / v_new rows (B operand)
+constexpr int kLdP = kC + 4;    // P rows (A operand)
+
+// grid (VH, Tp / 64), 256 threads: o = e^gamma (Q S_c) + P v_new for one chunk of one v-head,
+// then the gated rmsnorm (src/forward_pass.cpp:86-93, sum of squares in double) or the raw
+// readout. Wave w owns output rows [16w, 16w + 16), all 128 columns (8 blocks of 16).
+__global__ __launch_bounds__(256) void gdn_out_kernel(GdnPrefillArgs a) {
+    const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int kh = vh / (a.VH / a.KH);
+    const int nchunk = a.Tp / kC;
+    const int64_t row0 = static_cast<int64_t>(c) * kC;
+    __shared__ float A_s[kC][kLdQ];   // Q, then P
+    __shared__ float B_s[kD][kLdS];   // S_c, then v_new
+    __shared__ float gam[kC];
+    const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+    const float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD;
+    for (int f = tid; f < kC * kD / 4; f += 256)
+        *reinterpret_cast<float4*>(&A_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
+    for (int f = tid; f < kD * kD / 4; f += 256)
+        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Sc + f * 4);
+    if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
+    __syncthreads();
+    floatx4 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = 0; k < kD; k += 4) {
+        const float av = A_s[16 * wave + lr][k + lg];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const float e = expf(gam[16 * wave + 4 * lg + v]);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b][v] *= e;
+    }
+    __syncthreads();  // done with Q and S_c
+    const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
+    const float* Vn = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
+    for (int f = tid; f < kC * kC / 4; f += 256)
+        *reinterpret_cast<float4*>(&A_s[f >> 4][(f & 15) * 4]) = *reinterpret_cast<const float4*>(P + f * 4);
+    for (int f = tid; f < kC * kD / 4; f += 256)
+        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Vn + f * 4);
+    __syncthreads();
+    // P is lower triangular: the row block of wave w needs columns j < 16 (w + 1)
+    for (int k = 0; k < 16 * (wave + 1); k += 4) {
+        const float av = A_s[16 * wave + lr][k + lg];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
+    }
+    // epilogue: rows 16w + 4 lg + v, columns 16 b + lr
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int64_t t = row0 + 16 * wave + 4 * lg + v;
+        double ss = 0.0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) ss += static_cast<double>(acc[b][v]) * acc[b][v];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);  // the 16 lanes of the row
+        const float inv = 1.0f / sqrtf(static_cast<float>(ss / kD) + a.eps);
+        if (t >= a.T) continue;
+        float* out = a.out + t * (a.VH * kD) + vh * kD;
+        const float* z = a.z ? a.z + t * a.ld_z + vh * kD : nullptr;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int col = 16 * b + lr;
+            out[col] = a.norm_w ? a.norm_w[col] * (acc[b][v] * inv) * silu_f(z[col]) : acc[b][v];
+        }
+    }
 }
 
 // ------------------------------------------------------------------ attention prep
@@ -337,7 +423,6 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 }
 
 // ------------------------------------------------------------------ flash attention
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kQT = 64;   // query rows per workgroup (16 per wave)
 constexpr int kKT = 32;   // key / value positions per tile
 constexpr int kLd = kHD + 4;
@@ -498,7 +583,7 @@ int64_t gdn_prefill_workspace_floats(int KH, int VH, int T) {
     return (2 * KH + 3 * static_cast<int64_t>(VH)) * Tp * kD  // Qg Kg Vg U W
            + 3 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Gam
            + static_cast<int64_t>(VH) * Tp * kC                // P
-           + static_cast<int64_t>(T) * VH * kD                 // O (raw readout)
+           + static_cast<int64_t>(VH) * (Tp / kC) * kD * kD    // Sc (chunk-start states)
            + 64 * 8;                                           // alignment slack
 }
 
@@ -518,7 +603,7 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
     a.Gg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Gam = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.P = take(static_cast<int64_t>(a.VH) * a.Tp * kC);
-    a.O = take(static_cast<int64_t>(a.T) * a.VH * kD);
+    a.Sc = take(static_cast<int64_t>(a.VH) * (a.Tp / kC) * kD * kD);
 }
 
 hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
@@ -526,13 +611,8 @@ hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
     if (a.Tp > a.T) gdn_pad_kernel<<<blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s>>>(a);
     gdn_ring_kernel<<<blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s>>>(a);
     gdn_chunk_kernel<<<dim3(a.VH, a.Tp / kC), 256, 0, s>>>(a);
-    gdn_scan_kernel<<<dim3(a.VH, kD / kCW), 256, 0, s>>>(a);
-    if (a.norm_w) {
-        gdn_gated_norm_kernel<<<dim3(a.T, a.VH), 128, 0, s>>>(a);
-    } else {
-        hipError_t e = hipMemcpyAsync(a.out, a.O, static_cast<size_t>(a.T) * a.VH * kD * 4, hipMemcpyDeviceToDevice, s);
-        if (e != hipSuccess) return e;
-    }
+    gdn_state_kernel<<<dim3(a.VH, kD / kSW), 256, 0, s>>>(a);
+    gdn_out_kernel<<<dim3(a.VH, a.Tp / kC), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

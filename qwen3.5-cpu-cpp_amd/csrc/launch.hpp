@@ -131,7 +131,8 @@ struct GdnPrefillArgs {
     float *conv_ring, *state;
     float* out;        // [T][VH * 128]
     // workspace (head-major, padded to Tp rows)
-    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Gam, *P, *O;
+    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Gam, *P;
+    float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
 };
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);
 void gdn_prefill_carve(GdnPrefillArgs& a, float* ws);
