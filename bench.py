@@ -107,6 +107,29 @@ def cpu_baseline(model_dir: str, dims, ctx: int, n_steps: int) -> dict:
                       f"{ctx + 1}..{ctx + n_steps} (synthetic cache), {dt:.1f} s, OpenMP threads={threads}"}
 
 
+def cpu_greedy_baseline(model_dir: str, dims, prompt_len: int, n_steps: int) -> dict:
+    """The reference (oracle/_ref when built, else the oracle port): the prompt, then n_steps
+    greedy steps of the same checkpoint, timed over the greedy steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_py as op
+    import pyq35
+
+    kind = "reference" if op.ref_available() else "port"
+    prompt = pyq35.synth_token_ids(1, dims.vocab_size, prompt_len)
+    eng = op.Ref(model_dir, prompt_len + n_steps + 2) if kind == "reference" else op.Oracle(model_dir, prompt_len + n_steps + 2)
+    lg = None
+    for t in prompt:
+        lg = eng.step(int(t))
+    tok = int(np.argmax(lg))
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        tok = int(np.argmax(eng.step(tok)))
+    dt = time.perf_counter() - t0
+    eng.close()
+    return {"value": n_steps / dt, "unit": "tok/s", "cores": op.threads(), "kind": kind,
+            "sample": f"{n_steps} greedy steps after the {prompt_len}-token prompt, {dt:.1f} s"}
+
+
 def bench_gdn(a) -> dict:
     """Isolated GDN decode: 18 layers of 16 x 128 x 128 fp32 state in one launch per token,
     `steps` sequential tokens (q/k/v/z/a/b drawn N(0,1), A_log and dt_bias N(0,1), state
@@ -272,6 +295,7 @@ def bench_prefill(a) -> dict:
     import pyq35
 
     d = pyq35.dims_for("2b")
+    a.model_dir = a.model_dir or "/tmp/q35_synth_2b_seed0"
     ensure_model(a.model_dir, d, pyq35)
     T = a.prompt
     ids = pyq35.synth_token_ids(2, d.vocab_size, T)
@@ -374,7 +398,10 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=8192)
-    ap.add_argument("--model-dir", default="/tmp/q35_synth_2b_seed0")
+    ap.add_argument("--model", choices=["2b", "0.8b"], default="2b",
+                    help="decode: 2B shape at --ctx (synthetic cache) or the 0.8B shape after a prompt")
+    ap.add_argument("--model-dir", default="", help="checkpoint directory (written when absent)")
+    ap.add_argument("--prompt-len", type=int, default=32, help="0.8b decode: prompt tokens")
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["decode", "gdn", "attn", "prefill"], default="decode",
@@ -402,17 +429,26 @@ def main() -> None:
 
     import pyq35
 
-    d = pyq35.dims_for("2b")
-    ensure_model(a.model_dir, d, pyq35)
-    max_ctx = a.ctx + a.warmup + 2 * a.steps + 4
+    small = a.model == "0.8b"
+    d = pyq35.dims_for(a.model)
+    model_dir = a.model_dir or ("/tmp/q35_synth_08b_seed0" if small else "/tmp/q35_synth_2b_seed0")
+    ensure_model(model_dir, d, pyq35)
+    ctx = a.prompt_len if small else a.ctx
+    max_ctx = ctx + a.warmup + 2 * a.steps + 4
     t = time.time()
-    m = pyq35.Model(a.model_dir, max_ctx)
+    m = pyq35.Model(model_dir, max_ctx)
     log(f"model uploaded in {time.time() - t:.1f} s; budget {m.budget()}")
-    m.fill_synthetic(a.ctx, seed=0, state_std=0.1)
     hip = pyq35.Hip()
+    if small:
+        # the 0.8B-shaped greedy run: a prompt of uniform ids (seed 1) prefilled, then decode
+        prompt = pyq35.synth_token_ids(1, d.vocab_size, ctx)
+        lg = m.prefill(prompt)
+        tok = int(np.argmax(lg[-1]))
+    else:
+        m.fill_synthetic(ctx, seed=0, state_std=0.1)
+        tok = 1
 
     # warm-up (builds and replays the step graph)
-    tok = 1
     ids = m.decode_greedy(tok, a.warmup)
     tok = int(ids[-1])
     # timed: K greedy steps back to back on the device (graph replays), bracketed by syncs
@@ -464,16 +500,25 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic: random-init bf16 weights N(0,0.02) seed 0, KV cache N(0,1), GDN state N(0,0.1)",
-        "config": {"workload": f"2B-shaped Qwen3.5 greedy decode at {a.ctx} context",
+        "data": ("synthetic: random-init bf16 weights N(0,0.02) seed 0, "
+                 + (f"{ctx}-token prompt of uniform ids (seed 1) prefilled" if small
+                    else "KV cache N(0,1), GDN state N(0,0.1)")),
+        "config": {"workload": (f"{'0.8B' if small else '2B'}-shaped Qwen3.5 greedy decode at "
+                                f"{'a ' + str(ctx) + '-token prompt' if small else str(ctx) + ' context'}"),
                    "hidden": d.hidden_size, "layers": "24 = 18 GDN + 6 gated attention",
                    "gdn_heads": d.gdn_v_heads, "attn_heads": f"{NQ}q/{NKV}kv x {HD}",
-                   "ffn": d.ffn_intermediate, "vocab": d.vocab_size, "context": a.ctx,
+                   "ffn": d.ffn_intermediate, "vocab": d.vocab_size, "context": ctx,
                    "batch": 1},
-        "roofline": {"bound": "hbm", "kernel": "attention decode split-K partial (per layer)",
-                     "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": attn_gbs / HBM_PEAK_GBS, "traffic": None,
-                     "bytes_per_launch": attn_bytes, "avg_launch_us": attn_avg_s * 1e6},
+        # the dominant kernel of the step by time: the bf16 matvec (every projection, the FFN
+        # and the tied output head; 97 launches per step), bytes = the weights it streams
+        "roofline": {"bound": "hbm", "kernel": "bf16 matvec (all projections + output head, per step)",
+                     "achieved": gemv_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gemv_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": wb / (gemv_n / a.steps), "avg_launch_us": 1e3 * gemv_ms / gemv_n},
+        "roofline_attention": {"bound": "hbm", "kernel": "attention decode split-K partial (per layer)",
+                               "achieved": attn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": attn_gbs / HBM_PEAK_GBS, "traffic": None,
+                               "bytes_per_launch": attn_bytes, "avg_launch_us": attn_avg_s * 1e6},
         "mixers": {
             "attention_mixer_GBs": mixer_gbs, "attention_mixer_frac": mixer_gbs / HBM_PEAK_GBS,
             "gdn_decode_GBs": gdn_gbs, "gdn_decode_frac": gdn_gbs / HBM_PEAK_GBS,
@@ -485,14 +530,17 @@ def main() -> None:
     m.close()
     if a.calibration_copy:
         calibration_copy()
-    traffic_file = os.path.join(ROOT, "profiles", "attn_decode_traffic.json")
-    if os.path.exists(traffic_file) and a.ctx == 8192:
-        # HBM bytes per launch of the split-K kernel from the committed counter runs
+    traffic_file = os.path.join(ROOT, "profiles", "decode_2b_8k_traffic.json")
+    if os.path.exists(traffic_file) and not small and ctx == 8192:
+        # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter runs
         with open(traffic_file) as f:
-            result["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
+            tr = json.load(f)
+        result["roofline"]["traffic"] = tr.get("gemv_bytes_per_launch")
+        result["roofline_attention"]["traffic"] = tr.get("attn_bytes_per_launch")
     if not a.no_cpu_baseline:
         with stdout_to_stderr():
-            result["cpu_baseline"] = cpu_baseline(a.model_dir, d, a.ctx, a.cpu_steps)
+            result["cpu_baseline"] = (cpu_greedy_baseline(model_dir, d, ctx, a.cpu_steps) if small
+                                      else cpu_baseline(model_dir, d, ctx, a.cpu_steps))
     print(json.dumps(result), flush=True)
 
 
