@@ -201,28 +201,36 @@ def bench_gdn(a) -> dict:
 def bench_attn(a) -> dict:
     """Isolated gated-attention decode at the 2B shape: 6 layers with their own fp32 KV
     caches (N(0,1)) at each context of --ctx-list, one new token per step across the 6 layers
-    (q/k norm + RoPE + append + split-K softmax + gate)."""
+    (q/k norm + RoPE + append + split-K softmax + gate). --kv bf16: bf16 caches."""
     import pyq35
 
     hip = pyq35.Hip()
     NQ, NKV, HD, L = 16, 2, 256, 6
+    E = 2 if a.kv == "bf16" else 4
+
+    def cache(n, stream):
+        x = pyq35.synth_normal(n, 11, stream)
+        if E == 2:  # nearest-even bf16 bit patterns
+            u = x.view(np.uint32).astype(np.uint64)
+            x = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        return hip.upload(x)
     res = {}
     for ctx in a.ctx_list:
         maxc = ctx + 2 * (a.warmup + a.steps) + 1
         n = NKV * maxc * HD  # one layer's K (or V) cache
-        K = hip.upload(pyq35.synth_normal(L * n, 11, 0))
-        V = hip.upload(pyq35.synth_normal(L * n, 11, 1))
+        K = cache(L * n, 0)
+        V = cache(L * n, 1)
         qg = hip.upload(pyq35.synth_normal(L * 2 * NQ * HD, 12, 0))
         kn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 1))
         vn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 2))
         w = hip.upload(np.zeros(L * HD, np.float32))
         out = hip.malloc(L * NQ * HD * 4)
-        row = {"kv_working_set_MiB": 2 * L * n * 4 / 2**20}
+        row = {"kv_working_set_MiB": 2 * L * n * E / 2**20}
         p = ctx
         for mode in ("batched", "per_layer"):
             args = pyq35.AttnDecodeArgs(q_heads=NQ, kv_heads=NKV, head_dim=HD, rotary_dim=64, pos=ctx,
                                         n_splits=a.attn_splits, n_layers=L if mode == "batched" else 1,
-                                        max_context=maxc, rope_theta=1e7, eps=1e-6)
+                                        max_context=maxc, rope_theta=1e7, eps=1e-6, kv_dtype=int(E == 2))
             ws = pyq35.lib.q35_attn_decode_workspace_bytes(args)
             wsp = hip.malloc(ws)
             args.out, args.workspace, args.workspace_bytes = out, wsp, ws
@@ -237,7 +245,7 @@ def bench_attn(a) -> dict:
                     for l in range(L):
                         args.qg, args.k_new = qg + l * 2 * NQ * HD * 4, kn + l * NKV * HD * 4
                         args.v_new, args.q_norm, args.k_norm = vn + l * NKV * HD * 4, w, w
-                        args.k_cache, args.v_cache = K + l * n * 4, V + l * n * 4
+                        args.k_cache, args.v_cache = K + l * n * E, V + l * n * E
                         pyq35.check(pyq35.lib.q35_attn_decode(args, None))
             for _ in range(a.warmup):
                 step(p)
@@ -252,7 +260,7 @@ def bench_attn(a) -> dict:
             hip.record(e1)
             per = hip.elapsed_ms(e0, e1) / a.steps
             T = p_first + (a.steps + 1) / 2.0
-            nbytes = L * (4096 * T + 59_392)
+            nbytes = L * (2 * NKV * HD * E * T + 59_392)
             row[mode] = {"ms_per_token": per, "GBs": nbytes / (per / 1e3) / 1e9,
                          "frac": nbytes / (per / 1e3) / 1e9 / HBM_PEAK_GBS}
             hip.free(wsp)
@@ -266,7 +274,7 @@ def bench_attn(a) -> dict:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
             "data": "synthetic N(0,1) KV cache and inputs",
             "config": {"workload": "isolated attention decode", "context": int(key), "layers": L,
-                       "heads": f"{NQ}q/{NKV}kv x {HD}"},
+                       "heads": f"{NQ}q/{NKV}kv x {HD}", "kv_cache": a.kv},
             "roofline": {"bound": "hbm", "kernel": "attention decode (split-K + combine), 6 layers",
                          "achieved": r["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
                          "traffic": None},
@@ -413,6 +421,8 @@ def main() -> None:
     ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets, round-robin")
     ap.add_argument("--ctx-list", type=lambda s: [int(x) for x in s.split(",")], default=[2048, 8192, 32768])
     ap.add_argument("--attn-splits", type=int, default=0)
+    ap.add_argument("--kv", choices=["fp32", "bf16"], default="fp32",
+                    help="KV cache element type (decode, attn): fp32 is the reference's cache")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()
@@ -436,7 +446,8 @@ def main() -> None:
     ctx = a.prompt_len if small else a.ctx
     max_ctx = ctx + a.warmup + 2 * a.steps + 4
     t = time.time()
-    m = pyq35.Model(model_dir, max_ctx)
+    kv_elem = 2 if a.kv == "bf16" else 4
+    m = pyq35.Model(model_dir, max_ctx, kv_bytes_per_elem=kv_elem)
     log(f"model uploaded in {time.time() - t:.1f} s; budget {m.budget()}")
     hip = pyq35.Hip()
     if small:
@@ -476,10 +487,10 @@ def main() -> None:
     NKV, HD, NQ = d.attn_kv_heads, d.attn_head_dim, d.attn_q_heads
     attn_ms, attn_n = kt["attn_decode"]
     attn_avg_s = attn_ms / 1e3 / attn_n
-    attn_bytes = 2 * NKV * HD * 4 * mean_n + NQ * HD * 4  # K and V rows + the queries
+    attn_bytes = 2 * NKV * HD * kv_elem * mean_n + NQ * HD * 4  # K and V rows + the queries
     attn_gbs = attn_bytes / attn_avg_s / 1e9
     mixer_ms = sum(kt[k][0] for k in ("attn_decode", "attn_combine"))
-    mixer_bytes = 4096 * mean_n + 59_392  # per layer incl. projection outputs, append, output
+    mixer_bytes = 2 * NKV * HD * kv_elem * mean_n + 59_392  # per layer incl. projection outputs, append, output
     mixer_gbs = mixer_bytes * attn_n / (mixer_ms / 1e3) / 1e9
     gdn_ms, gdn_n = kt["gdn_decode"]
     gdn_gbs = GDN_LAYER_BYTES * gdn_n / (gdn_ms / 1e3) / 1e9
@@ -508,7 +519,7 @@ def main() -> None:
                    "hidden": d.hidden_size, "layers": "24 = 18 GDN + 6 gated attention",
                    "gdn_heads": d.gdn_v_heads, "attn_heads": f"{NQ}q/{NKV}kv x {HD}",
                    "ffn": d.ffn_intermediate, "vocab": d.vocab_size, "context": ctx,
-                   "batch": 1},
+                   "batch": 1, "kv_cache": a.kv},
         # the dominant kernel of the step by time: the bf16 matvec (every projection, the FFN
         # and the tied output head; 97 launches per step), bytes = the weights it streams
         "roofline": {"bound": "hbm", "kernel": "bf16 matvec (all projections + output head, per step)",
@@ -531,7 +542,7 @@ def main() -> None:
     if a.calibration_copy:
         calibration_copy()
     traffic_file = os.path.join(ROOT, "profiles", "decode_2b_8k_traffic.json")
-    if os.path.exists(traffic_file) and not small and ctx == 8192:
+    if os.path.exists(traffic_file) and not small and ctx == 8192 and a.kv == "fp32":
         # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counter runs
         with open(traffic_file) as f:
             tr = json.load(f)

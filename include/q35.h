@@ -135,6 +135,17 @@ typedef struct q35_tensor {
  * the KV capacity in positions. */
 q35_status q35_model_create(const q35_dims *d, const q35_tensor *tensors, int32_t n_tensors,
                             int64_t max_context, q35_model **out);
+/* Creation options. kv_bytes_per_elem is memory_budget's KV element width
+ * (include/memory_budget.h:37-42): 4 = fp32 cache (the reference's; the default), 2 = bf16
+ * cache (rows rounded to nearest even when appended; half the KV bytes and bandwidth). */
+typedef struct q35_model_options {
+    int32_t kv_bytes_per_elem;
+    int32_t reserved[7];
+} q35_model_options;
+q35_status q35_model_create_opts(const q35_dims *d, const q35_tensor *tensors, int32_t n_tensors,
+                                 int64_t max_context, const q35_model_options *opt, q35_model **out);
+q35_status q35_model_open_opts(const char *model_dir, int64_t max_context,
+                               const q35_model_options *opt, q35_model **out);
 /* Same, reading <dir>/config.json and every <dir>/ *.safetensors shard. */
 q35_status q35_model_open(const char *model_dir, int64_t max_context, q35_model **out);
 void q35_model_destroy(q35_model *m);
@@ -279,7 +290,7 @@ typedef struct q35_attn_decode_args {
     int32_t pos;
     int32_t n_splits;      /* KV splits per kv head; 0 = automatic */
     int32_t n_layers;      /* independent layers in one launch (0 or 1 = one) */
-    int32_t reserved;
+    int32_t kv_dtype;      /* cache elements: 0 = fp32, 1 = bf16 (appended rows rounded to nearest even) */
     int64_t max_context;
     double rope_theta;
     float eps;
@@ -322,6 +333,8 @@ q35_status q35_gdn_prefill(const q35_gdn_prefill_args *args, q35_stream s);
  * workspace: q35_attn_prefill_workspace_bytes() bytes. Requires HD == 256. */
 typedef struct q35_attn_prefill_args {
     int32_t n_tokens, pos0, q_heads, kv_heads, head_dim, rotary_dim;
+    int32_t kv_dtype;      /* cache elements: 0 = fp32, 1 = bf16 (as q35_attn_decode_args) */
+    int32_t reserved;
     int64_t max_context;
     double rope_theta;
     float eps;

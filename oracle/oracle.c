@@ -655,10 +655,38 @@ void orc_gdn_core(const orc_dims *d, const float *qkv, const float *z, const flo
     free(o);
 }
 
-/* src/qwen_model.cpp:119-150 */
+/* fp32 -> nearest bf16 value (ties to even), returned widened. The reference keeps an fp32
+ * cache (src/qwen_model.cpp:29-30); this is the rounding a bf16 cache applies to the rows it
+ * stores, memory_budget's kv_bytes_per_elem = 2 (include/memory_budget.h:37-42). NaN stays
+ * NaN; values that round past the largest bf16 become infinity. */
+float orc_round_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+        u |= 0x00400000u; /* quiet NaN */
+    } else {
+        u += 0x7fffu + ((u >> 16) & 1u);
+    }
+    u &= 0xffff0000u;
+    float y;
+    memcpy(&y, &u, 4);
+    return y;
+}
+
+void orc_round_bf16_array(float *x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_round_bf16(x[i]);
+}
+
 void orc_attn_core(const orc_dims *d, int pos, const float *qg, const float *k_new,
                    const float *v_new, const float *q_norm, const float *k_norm,
                    float *kcache, float *vcache, float *out) {
+    orc_attn_core_ex(d, pos, qg, k_new, v_new, q_norm, k_norm, kcache, vcache, out, 0, 1);
+}
+
+/* src/qwen_model.cpp:119-150 */
+void orc_attn_core_ex(const orc_dims *d, int pos, const float *qg, const float *k_new,
+                      const float *v_new, const float *q_norm, const float *k_norm,
+                      float *kcache, float *vcache, float *out, int kv_bf16, int append) {
     const int NQ = d->attn_q_heads, NKV = d->attn_kv_heads, HD = d->attn_head_dim,
               GRP = NQ / NKV;
     const int ROT = (int)(HD * d->partial_rotary_factor);
@@ -675,12 +703,18 @@ void orc_attn_core(const orc_dims *d, int pos, const float *qg, const float *k_n
     }
     float *kslot = kcache + (size_t)pos * NKV * HD;
     float *vslot = vcache + (size_t)pos * NKV * HD;
-    for (int kh = 0; kh < NKV; ++kh) {
-        float *kd = kslot + (size_t)kh * HD;
-        orc_rmsnorm(k_new + (size_t)kh * HD, k_norm, kd, HD, eps);
-        orc_apply_rope(kd, ROT, pos, d->rope_theta);
+    if (append) {
+        for (int kh = 0; kh < NKV; ++kh) {
+            float *kd = kslot + (size_t)kh * HD;
+            orc_rmsnorm(k_new + (size_t)kh * HD, k_norm, kd, HD, eps);
+            orc_apply_rope(kd, ROT, pos, d->rope_theta);
+        }
+        memcpy(vslot, v_new, sizeof(float) * (size_t)NKV * HD);
+        if (kv_bf16) {
+            orc_round_bf16_array(kslot, (int64_t)NKV * HD);
+            orc_round_bf16_array(vslot, (int64_t)NKV * HD);
+        }
     }
-    memcpy(vslot, v_new, sizeof(float) * (size_t)NKV * HD);
     for (int h = 0; h < NQ; ++h) {
         const int kh = h / GRP;
         const float *q = Q + (size_t)h * HD;
@@ -744,7 +778,10 @@ struct orc_model {
     float *hidden, *normed, *mix, *ff, *logits;
     float *trace;
     int ok;
+    int kv_bf16; /* 1: cache rows stored rounded to bf16 */
 };
+
+void orc_set_kv_bf16(orc_model *m, int on) { m->kv_bf16 = on ? 1 : 0; }
 
 static const uint16_t *need_bf16(orc_model *m, const char *name) {
     const st_entry *e = st_find(&m->st, name);
@@ -952,7 +989,8 @@ static void attn_step(orc_model *m, const orc_layer *L, float *out) {
     orc_matmul_bf16(L->q, m->normed, qg, NQ * HD * 2, H);
     orc_matmul_bf16(L->k, m->normed, kn, NKV * HD, H);
     orc_matmul_bf16(L->v, m->normed, vn, NKV * HD, H);
-    orc_attn_core(d, m->pos, qg, kn, vn, L->q_norm, L->k_norm, m->kc[L->idx], m->vc[L->idx], ac);
+    orc_attn_core_ex(d, m->pos, qg, kn, vn, L->q_norm, L->k_norm, m->kc[L->idx], m->vc[L->idx], ac,
+                     m->kv_bf16, 1);
     orc_matmul_bf16(L->o, ac, out, H, NQ * HD);
     free(qg);
     free(kn);

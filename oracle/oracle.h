@@ -66,11 +66,20 @@ void orc_gdn_core(const orc_dims *d, const float *qkv, const float *z, const flo
 void orc_attn_core(const orc_dims *d, int pos, const float *qg, const float *k_new,
                    const float *v_new, const float *q_norm, const float *k_norm,
                    float *kcache, float *vcache, float *out);
+/* Same with a bf16 cache (kv_bf16 = 1: the appended rows are stored rounded to the nearest
+ * bf16, ties to even, before the attention reads them). append = 0 leaves row pos as the
+ * caller put it (k_new / v_new / k_norm unused): the attention over given cache contents. */
+void orc_attn_core_ex(const orc_dims *d, int pos, const float *qg, const float *k_new,
+                      const float *v_new, const float *q_norm, const float *k_norm,
+                      float *kcache, float *vcache, float *out, int kv_bf16, int append);
+float orc_round_bf16(float x);
+void orc_round_bf16_array(float *x, int64_t n);
 
 /* whole model: src/qwen_model.cpp:12-255, src/qwen_forward.cpp:154-206 */
 typedef struct orc_model orc_model;
 orc_model *orc_open(const char *dir, int max_context);  /* NULL on failure */
 void orc_close(orc_model *m);
+void orc_set_kv_bf16(orc_model *m, int on); /* store cache rows rounded to bf16 from now on */
 const char *orc_error(void);
 void orc_get_dims(const orc_model *m, orc_dims *d);
 void orc_reset(orc_model *m);

@@ -47,6 +47,10 @@ def _load_oracle():
         "orc_load_config": (I, [C.c_char_p, C.POINTER(OrcDims)]),
         "orc_gdn_core": (None, [C.POINTER(OrcDims)] + [P] * 12),
         "orc_attn_core": (None, [C.POINTER(OrcDims), I] + [P] * 8),
+        "orc_attn_core_ex": (None, [C.POINTER(OrcDims), I] + [P] * 8 + [I, I]),
+        "orc_round_bf16": (F, [F]),
+        "orc_round_bf16_array": (None, [P, C.c_int64]),
+        "orc_set_kv_bf16": (None, [P, I]),
         "orc_open": (P, [C.c_char_p, I]),
         "orc_close": (None, [P]),
         "orc_error": (C.c_char_p, []),
@@ -93,10 +97,11 @@ def view(ptr, shape):
 class Oracle:
     """The CPU restatement of QwenModel / QwenForward on a checkpoint directory."""
 
-    def __init__(self, model_dir: str, max_context: int):
+    def __init__(self, model_dir: str, max_context: int, kv_bf16: bool = False):
         self.h = olib.orc_open(model_dir.encode(), max_context)
         if not self.h:
             raise RuntimeError(f"oracle open failed: {olib.orc_error().decode()}")
+        olib.orc_set_kv_bf16(self.h, int(kv_bf16))
         d = OrcDims()
         olib.orc_get_dims(self.h, C.byref(d))
         self.dims = d
@@ -202,6 +207,26 @@ def attn_core(dims, pos, qg, k_new, v_new, q_norm, k_norm, kcache, vcache):
     assert kcache.dtype == np.float32 and kcache.flags.c_contiguous
     olib.orc_attn_core(C.byref(d), int(pos), *[_p(x) for x in args], _p(kcache), _p(vcache), _p(out))
     return out
+
+
+def attn_core_ex(dims, pos, qg, k_new, v_new, q_norm, k_norm, kcache, vcache, kv_bf16, append):
+    """orc_attn_core_ex: kv_bf16 rounds the appended rows to bf16; append=False attends over
+    the caches as given (row pos included)."""
+    d = dims_from(dims)
+    out = np.zeros(d.attn_q_heads * d.attn_head_dim, np.float32)
+    args = [np.ascontiguousarray(x, np.float32) for x in (qg, k_new, v_new, q_norm, k_norm)]
+    assert kcache.dtype == np.float32 and kcache.flags.c_contiguous
+    assert vcache.dtype == np.float32 and vcache.flags.c_contiguous
+    olib.orc_attn_core_ex(C.byref(d), int(pos), *[_p(x) for x in args], _p(kcache), _p(vcache), _p(out),
+                          int(kv_bf16), int(append))
+    return out
+
+
+def round_bf16(x):
+    """orc_round_bf16_array on a copy: nearest bf16 value (ties to even), as fp32."""
+    y = np.array(x, np.float32, copy=True)
+    olib.orc_round_bf16_array(_p(y), y.size)
+    return y
 
 
 def rmsnorm(x, w, eps):

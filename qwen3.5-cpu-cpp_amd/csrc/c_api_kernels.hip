@@ -129,6 +129,7 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
         !g.workspace)
         return q35::fail(Q35_ERR_ARG, "q35_attn_decode: null pointer");
     if (g.n_splits < 0 || g.n_splits > 4096) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: n_splits %d", g.n_splits);
+    if (g.kv_dtype != 0 && g.kv_dtype != 1) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: kv_dtype %d", g.kv_dtype);
     if (g.workspace_bytes < q35_attn_decode_workspace_bytes(args))
         return q35::fail(Q35_ERR_ARG, "q35_attn_decode: workspace of %llu bytes, needs %llu",
                          static_cast<unsigned long long>(g.workspace_bytes),
@@ -151,6 +152,7 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
     a.k_norm = g.k_norm;
     a.k_cache = g.k_cache;
     a.v_cache = g.v_cache;
+    a.kv_bf16 = g.kv_dtype == 1;
     a.out = g.out;
     a.n_layers = g.n_layers > 0 ? g.n_layers : 1;
     a.part_o = static_cast<float*>(g.workspace);
@@ -226,6 +228,7 @@ q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
                          static_cast<long long>(g.pos0) + g.n_tokens, static_cast<long long>(g.max_context));
     if (!g.qkv || !g.q_norm || !g.k_norm || !g.k_cache || !g.v_cache || !g.out || !g.workspace)
         return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: null pointer");
+    if (g.kv_dtype != 0 && g.kv_dtype != 1) return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: kv_dtype %d", g.kv_dtype);
     if (g.ld_qkv < 2LL * g.q_heads * 256 + 2LL * g.kv_heads * 256)
         return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: leading dimension too small");
     if (g.workspace_bytes < q35_attn_prefill_workspace_bytes(args))
@@ -247,6 +250,7 @@ q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
     a.k_norm = g.k_norm;
     a.k_cache = g.k_cache;
     a.v_cache = g.v_cache;
+    a.kv_bf16 = g.kv_dtype == 1;
     a.Qa = static_cast<float*>(g.workspace);
     a.out = g.out;
     return launched(q35k::launch_attn_prefill(a, as_stream(s)), "q35_attn_prefill");

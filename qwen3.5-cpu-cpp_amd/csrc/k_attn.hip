@@ -16,6 +16,8 @@
 //            (4 dims per lane) takes each softmax weight as a scalar operand read from its
 //            lane. The waves are merged once at the end (max-rescaled, fixed order).
 //            Output: unnormalised partial output and (max, sum) per query head and split.
+//            The cache holds fp32 or bf16 elements (bf16: rows rounded to nearest even when
+//            appended, widened exactly when read).
 //   combine  grid (NQ, HD/64): merges the splits with max-rescaled sums (the splits are
 //            shared over the 4 waves, one dim per lane), divides, multiplies by
 //            sigmoid(gate).
@@ -101,11 +103,18 @@ __device__ __forceinline__ float4 load_stream(const float* p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// 4 consecutive bf16 cache elements (8 bytes), widened exactly
+__device__ __forceinline__ float4 load_stream_bf16(const uint16_t* p) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 v = __builtin_nontemporal_load(reinterpret_cast<const u2*>(p));
+    return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+}
+
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-template <int GRP, int LPP, int kBatch, bool DBUF>
+template <int GRP, int LPP, int kBatch, bool DBUF, bool KVB>
 __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     attn_select_layer(a, blockIdx.z);
     constexpr int NF4 = 64 / LPP;   // float4 of one K row per lane in the score layout
@@ -126,8 +135,11 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     const int wpe = (j1 - j0 + kWaves - 1) / kWaves;
     const int w0 = j0 + wave * wpe, w1 = min(j1, w0 + wpe);
 
-    const float* K = a.k_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
-    const float* V = a.v_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    const float* K = a.k_cache + hoff;
+    const float* V = a.v_cache + hoff;
+    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(a.k_cache) + hoff;
+    const uint16_t* Vb = reinterpret_cast<const uint16_t*>(a.v_cache) + hoff;
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
     __shared__ float rows_s[NROW][kHD];  // normed + rotated q rows, then the new key
@@ -142,15 +154,15 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     auto load = [&](float4 (&kr)[QIT][NF4], float4 (&vr)[kBatch], int b0) {
 #pragma unroll
         for (int it = 0; it < QIT; ++it) {
-            const int row = min(b0 + it * PPW + sub, w1 - 1);
-            const float* src = K + static_cast<int64_t>(row) * kHD + pl * 4;
+            const int64_t off = static_cast<int64_t>(min(b0 + it * PPW + sub, w1 - 1)) * kHD + pl * 4;
 #pragma unroll
-            for (int m = 0; m < NF4; ++m) kr[it][m] = load_stream(src + m * LPP * 4);
+            for (int m = 0; m < NF4; ++m)
+                kr[it][m] = KVB ? load_stream_bf16(Kb + off + m * LPP * 4) : load_stream(K + off + m * LPP * 4);
         }
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-            const int row = min(b0 + j, w1 - 1);
-            vr[j] = load_stream(V + static_cast<int64_t>(row) * kHD + lane * 4);
+            const int64_t off = static_cast<int64_t>(min(b0 + j, w1 - 1)) * kHD + lane * 4;
+            vr[j] = KVB ? load_stream_bf16(Vb + off) : load_stream(V + off);
         }
     };
     // ---- prologue loads, then the first two K / V batches, all unconditional (rows clamped
@@ -218,9 +230,20 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     }
     __syncthreads();
     if (owns_new && tid < kHD) {  // append the new K / V rows
-        a.k_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + tid] = rows_s[GRP][tid];
-        a.v_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + tid] = vnew_s[tid];
+        const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + tid;
+        if constexpr (KVB) {
+            // the cache holds the rounded row, and so does the score of position pos here
+            const uint16_t kb = f32_to_bf16(rows_s[GRP][tid]), vb = f32_to_bf16(vnew_s[tid]);
+            reinterpret_cast<uint16_t*>(a.k_cache)[off] = kb;
+            reinterpret_cast<uint16_t*>(a.v_cache)[off] = vb;
+            rows_s[GRP][tid] = bf16_to_f32(kb);
+            vnew_s[tid] = bf16_to_f32(vb);
+        } else {
+            a.k_cache[off] = rows_s[GRP][tid];
+            a.v_cache[off] = vnew_s[tid];
+        }
     }
+    if constexpr (KVB) __syncthreads();
 
     float4 qr[GRP][NF4];
 #pragma unroll
@@ -439,7 +462,8 @@ hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
     constexpr int LPP = GRP <= 4 ? 16 : 32;
     dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
     constexpr int BATCH = GRP <= 4 ? 8 : GRP == 8 ? 4 : 2;
-    attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8)><<<grid, kWaves * 64, 0, s>>>(a);
+    if (a.kv_bf16) attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), true><<<grid, kWaves * 64, 0, s>>>(a);
+    else attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), false><<<grid, kWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -157,6 +157,12 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float* dst, int64_t n,
         dst[i] = static_cast<float>(std * normal_at(key, static_cast<uint64_t>(i)));
 }
 
+__global__ __launch_bounds__(256) void fill_normal_bf16_kernel(uint16_t* dst, int64_t n, uint64_t key, float std) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        dst[i] = f32_to_bf16(static_cast<float>(std * normal_at(key, static_cast<uint64_t>(i))));
+}
+
 __global__ __launch_bounds__(256) void rope_table_kernel(float* t, int64_t n_pos, int rot, double theta) {
     const int half = rot / 2;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_pos * half;
@@ -229,8 +235,9 @@ hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s) {
-    fill_normal_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, key, std);
+hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s, bool bf16) {
+    if (bf16) fill_normal_bf16_kernel<<<grid_for(n), 256, 0, s>>>(reinterpret_cast<uint16_t*>(dst), n, key, std);
+    else fill_normal_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, key, std);
     return hipGetLastError();
 }
 

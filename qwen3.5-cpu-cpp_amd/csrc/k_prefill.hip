@@ -21,7 +21,8 @@
 //            cores, then rmsnorm_gated per (token, v-head) (src/forward_pass.cpp:86-93).
 // Causal attention, flash form on the matrix cores (v_mfma_f32_16x16x4_f32):
 //   prep     q_norm + RoPE of every query row (head-major), k_norm + RoPE of every key and
-//            the values appended to the KV cache at pos0 + t (angles in double).
+//            the values appended to the KV cache at pos0 + t (angles in double; a bf16 cache
+//            stores them rounded to nearest even and the flash kernel widens them back).
 //   flash    grid (query tiles of 64, NQ): 4 waves of 16 query rows with their q in
 //            registers; 32-position K / V tiles in LDS; S = Q K^T and O += P V on MFMA;
 //            running max / sum per row; epilogue O / l * sigmoid(gate).
@@ -387,18 +388,18 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
     const float* row = a.qkv + static_cast<int64_t>(t) * a.ld_qkv;
     const float* src;
     const float* w;
-    float* dst;
-    if (r < a.NQ) {
+    const bool is_q = r < a.NQ;
+    const int kh = r - a.NQ;
+    const int64_t coff = (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD;  // cache row (keys)
+    if (is_q) {
         src = row + static_cast<int64_t>(r) * 2 * kHD;
         w = a.q_norm;
-        dst = a.Qa + (static_cast<int64_t>(r) * a.T + t) * kHD;
     } else {
-        const int kh = r - a.NQ;
         src = row + static_cast<int64_t>(a.NQ) * 2 * kHD + kh * kHD;
         w = a.k_norm;
-        dst = a.k_cache + (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD;
-        a.v_cache[(static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + d] =
-            row[static_cast<int64_t>(a.NQ) * 2 * kHD + static_cast<int64_t>(a.NKV) * kHD + kh * kHD + d];
+        const float v = row[static_cast<int64_t>(a.NQ) * 2 * kHD + static_cast<int64_t>(a.NKV) * kHD + kh * kHD + d];
+        if (a.kv_bf16) reinterpret_cast<uint16_t*>(a.v_cache)[coff + d] = f32_to_bf16(v);
+        else a.v_cache[coff + d] = v;
     }
     const int half = a.ROT / 2;
     if (d < half) {
@@ -419,7 +420,9 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
         const float x1 = buf[i], x2 = buf[i + half];
         y = d < half ? x1 * c - x2 * s : x2 * c + x1 * s;
     }
-    dst[d] = y;
+    if (is_q) a.Qa[(static_cast<int64_t>(r) * a.T + t) * kHD + d] = y;
+    else if (a.kv_bf16) reinterpret_cast<uint16_t*>(a.k_cache)[coff + d] = f32_to_bf16(y);
+    else a.k_cache[coff + d] = y;
 }
 
 // ------------------------------------------------------------------ flash attention
@@ -472,8 +475,11 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnPrefillArgs a) {
     // this lane's query rows (C layout): 4 g4 + i, block-relative positions
     const int qrow0 = t0 + wave * 16 + 4 * g4;
     const int kv_end = a.pos0 + min(a.T, t0 + kQT);  // exclusive, causal for the tile
-    const float* K = a.k_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
-    const float* V = a.v_cache + static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    const float* K = a.k_cache + hoff;
+    const float* V = a.v_cache + hoff;
+    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(a.k_cache) + hoff;
+    const uint16_t* Vb = reinterpret_cast<const uint16_t*>(a.v_cache) + hoff;
     for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
         __syncthreads();
         for (int i = tid; i < kKT * (kHD / 4); i += 256) {
@@ -481,8 +487,16 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnPrefillArgs a) {
             const int p = kv0 + rr;
             float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
             if (p < kv_end) {
-                kv = *reinterpret_cast<const float4*>(K + static_cast<int64_t>(p) * kHD + c4);
-                vv = *reinterpret_cast<const float4*>(V + static_cast<int64_t>(p) * kHD + c4);
+                const int64_t off = static_cast<int64_t>(p) * kHD + c4;
+                if (a.kv_bf16) {
+                    const uint2 kb = *reinterpret_cast<const uint2*>(Kb + off);
+                    const uint2 vb = *reinterpret_cast<const uint2*>(Vb + off);
+                    kv = make_float4(bf16_lo(kb.x), bf16_hi(kb.x), bf16_lo(kb.y), bf16_hi(kb.y));
+                    vv = make_float4(bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y));
+                } else {
+                    kv = *reinterpret_cast<const float4*>(K + off);
+                    vv = *reinterpret_cast<const float4*>(V + off);
+                }
             }
             *reinterpret_cast<float4*>(&KV[0][rr][c4]) = kv;
             *reinterpret_cast<float4*>(&KV[1][rr][c4]) = vv;

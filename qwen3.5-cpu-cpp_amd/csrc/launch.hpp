@@ -71,7 +71,8 @@ struct AttnDecodeArgs {
     float eps;
     const float *qg, *k_new, *v_new, *q_norm, *k_norm;
     const float* rope_cs;       // optional [max_ctx][ROT]: cos (ROT/2) then sin (ROT/2) per position
-    float *k_cache, *v_cache;   // [NKV][max_ctx][HD]
+    float *k_cache, *v_cache;   // [NKV][max_ctx][HD], fp32 or (kv_bf16) bf16 elements
+    int kv_bf16;                // cache element: 0 = fp32, 1 = bf16 (round to nearest even)
     float* part_o;              // [NKV][n_splits][GRP][HD]
     float* part_ml;             // [NKV][n_splits][GRP][2]
     float* out;                 // [NQ][HD]
@@ -90,8 +91,9 @@ __device__ __forceinline__ void attn_select_layer(AttnDecodeArgs& a, int l) {
     a.v_new += static_cast<int64_t>(l) * a.NKV * a.HD;
     a.q_norm += static_cast<int64_t>(l) * a.HD;
     a.k_norm += static_cast<int64_t>(l) * a.HD;
-    a.k_cache += l * lc;
-    a.v_cache += l * lc;
+    const int64_t lce = a.kv_bf16 ? lc / 2 : lc;  // in floats: a bf16 cache is half as long
+    a.k_cache += l * lce;
+    a.v_cache += l * lce;
     a.part_o += static_cast<int64_t>(l) * a.NKV * a.n_splits * grp * a.HD;
     a.part_ml += static_cast<int64_t>(l) * a.NKV * a.n_splits * grp * 2;
     a.out += static_cast<int64_t>(l) * a.NQ * a.HD;
@@ -148,7 +150,8 @@ struct AttnPrefillArgs {
     const float* qkv;  // [T][ld_qkv]: NQ x [q | gate] (2 HD each), NKV x k, NKV x v
     int64_t ld_qkv;
     const float *q_norm, *k_norm;
-    float *k_cache, *v_cache;  // [NKV][max_ctx][HD]
+    float *k_cache, *v_cache;  // [NKV][max_ctx][HD], fp32 or (kv_bf16) bf16 elements
+    int kv_bf16;
     float* Qa;                 // workspace [NQ][T][HD]
     float* out;                // [T][NQ * HD]
 };
@@ -178,8 +181,8 @@ hipError_t launch_add_int(int* p, int v, hipStream_t s);
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t s);
 hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s);
-// dst[i] = std * N(0,1)(key, i)
-hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s);
+// dst[i] = std * N(0,1)(key, i); with bf16, dst holds bf16 elements rounded to nearest even
+hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s, bool bf16 = false);
 // t[p][i] = cos(p * theta^(-2i/rot)), t[p][rot/2 + i] = sin(...) for i < rot/2, in double
 // rounded to float (the apply_rope formula, src/forward_pass.cpp:102-112)
 hipError_t launch_rope_table(float* t, int64_t n_pos, int rot, double theta, hipStream_t s);

@@ -80,6 +80,7 @@ struct q35_model {
     size_t state_bytes = 0;
     float* kv_arena = nullptr;
     size_t kv_bytes = 0;
+    int kv_elem = 4;  // bytes per KV cache element: 4 (fp32) or 2 (bf16)
     uint8_t* scratch = nullptr;
     size_t scratch_bytes = 0;
 
@@ -271,6 +272,14 @@ private:
     std::vector<Piece> pieces_;
 };
 
+// Start of the cache rows of (attention layer, K = 0 / V = 1, kv head), whatever the element
+// width (the kernels take the arena as float* and index it by elements of the cache type).
+float* kv_ptr(const q35_model* m, int layer, int which, int kh) {
+    const int64_t elems = ((static_cast<int64_t>(layer) * 2 + which) * m->d.attn_kv_heads + kh) * m->max_ctx *
+                          m->d.attn_head_dim;
+    return reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(m->kv_arena) + elems * m->kv_elem);
+}
+
 // ------------------------------------------------------------------ step enqueue
 struct Launcher {
     q35_model* m;
@@ -376,8 +385,9 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
             aa.q_norm = ly.q_norm;
             aa.k_norm = ly.k_norm;
             aa.rope_cs = m->rope_cs;
-            aa.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
-            aa.v_cache = aa.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
+            aa.k_cache = kv_ptr(m, ly.idx, 0, 0);
+            aa.v_cache = kv_ptr(m, ly.idx, 1, 0);
+            aa.kv_bf16 = m->kv_elem == 2;
             aa.part_o = m->part_o;
             aa.part_ml = m->part_ml;
             aa.out = m->mix;
@@ -502,12 +512,14 @@ void destroy(q35_model* m) {
     delete m;
 }
 
-q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int64_t max_ctx,
+q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int64_t max_ctx, int kv_elem,
                         q35_model** out) {
     if (!dims || !ts || !out || nt <= 0) return q35::fail(Q35_ERR_ARG, "q35_model_create: null argument");
     *out = nullptr;
     if (max_ctx <= 0 || max_ctx > (int64_t{1} << 30))
         return q35::fail(Q35_ERR_RANGE, "max_context %lld out of range", static_cast<long long>(max_ctx));
+    if (kv_elem != 4 && kv_elem != 2)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "KV cache element of %d bytes (4 = fp32 or 2 = bf16)", kv_elem);
     q35_dims d = *dims;
     d.n_layers_attn = d.n_layers_total / d.attn_interval;
     d.n_layers_gdn = d.n_layers_total - d.n_layers_attn;
@@ -607,7 +619,8 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     const size_t gdn_bytes = static_cast<size_t>(d.n_layers_gdn) * VH * 128 * 128 * 4;
     const size_t ring_bytes = static_cast<size_t>(d.n_layers_gdn) * 4 * CONV * 4;
     m->state_bytes = align256(gdn_bytes) + align256(ring_bytes);
-    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * static_cast<size_t>(max_ctx) * HD * 4;
+    m->kv_elem = kv_elem;
+    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * static_cast<size_t>(max_ctx) * HD * kv_elem;
     m->n_cu = q35k::device_cu_count();
     m->n_splits = q35k::attn_default_splits(max_ctx, NKV, m->n_cu);
     const int64_t proj_n = std::max<int64_t>(static_cast<int64_t>(CONV) + VD + 2 * VH, 2LL * NQ * HD + 2LL * NKV * HD);
@@ -869,8 +882,9 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.ld_qkv = ly.in_rows;
             a.q_norm = ly.q_norm;
             a.k_norm = ly.k_norm;
-            a.k_cache = m->kv_arena + static_cast<int64_t>(ly.idx) * 2 * NKV * m->max_ctx * HD;
-            a.v_cache = a.k_cache + static_cast<int64_t>(NKV) * m->max_ctx * HD;
+            a.k_cache = kv_ptr(m, ly.idx, 0, 0);
+            a.v_cache = kv_ptr(m, ly.idx, 1, 0);
+            a.kv_bf16 = m->kv_elem == 2;
             a.Qa = ws;
             a.out = mix;
             Lr.run(Q35_KT_ATTN_PREFILL, [&] { return q35k::launch_attn_prefill(a, s); });
@@ -966,10 +980,20 @@ int64_t q35_device_alloc_count(void) { return g_dev_allocs.load(); }
 
 q35_status q35_model_create(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
                             int64_t max_context, q35_model** out) {
-    return create_model(d, tensors, n_tensors, max_context, out);
+    return create_model(d, tensors, n_tensors, max_context, 4, out);
+}
+
+q35_status q35_model_create_opts(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
+                                 int64_t max_context, const q35_model_options* opt, q35_model** out) {
+    return create_model(d, tensors, n_tensors, max_context, opt ? opt->kv_bytes_per_elem : 4, out);
 }
 
 q35_status q35_model_open(const char* model_dir, int64_t max_context, q35_model** out) {
+    return q35_model_open_opts(model_dir, max_context, nullptr, out);
+}
+
+q35_status q35_model_open_opts(const char* model_dir, int64_t max_context, const q35_model_options* opt,
+                               q35_model** out) {
     if (!model_dir || !out) return q35::fail(Q35_ERR_ARG, "q35_model_open: null argument");
     ModelConfig cfg;
     load_model_config(std::string(model_dir) + "/config.json", cfg);
@@ -992,7 +1016,8 @@ q35_status q35_model_open(const char* model_dir, int64_t max_context, q35_model*
     }
     q35_dims d;
     q35::dims_from_config(cfg, &d);
-    return create_model(&d, table.data(), static_cast<int32_t>(table.size()), max_context, out);
+    return create_model(&d, table.data(), static_cast<int32_t>(table.size()), max_context,
+                        opt ? opt->kv_bytes_per_elem : 4, out);
 }
 
 void q35_model_destroy(q35_model* m) { destroy(m); }
@@ -1216,39 +1241,48 @@ q35_status q35_model_read_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t 
                              float* v_host) {
     if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
         return q35::fail(Q35_ERR_ARG, "bad argument");
-    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
-    const float* base = m->kv_arena + static_cast<int64_t>(layer) * 2 * NKV * m->max_ctx * HD;
+    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim, E = m->kv_elem;
+    std::vector<uint16_t> tmp(m->kv_elem == 2 ? static_cast<size_t>(n) * NKV * HD : 0);
     for (int which = 0; which < 2; ++which) {
         float* dst = which == 0 ? k_host : v_host;
         if (!dst) continue;
+        void* hdst = E == 2 ? static_cast<void*>(tmp.data()) : static_cast<void*>(dst);
         for (int kh = 0; kh < NKV; ++kh) {
-            const float* src = base + (static_cast<int64_t>(which) * NKV + kh) * m->max_ctx * HD + pos0 * HD;
-            HIPCHK(hipMemcpy2DAsync(dst + kh * HD, static_cast<size_t>(NKV) * HD * 4, src,
-                                    static_cast<size_t>(HD) * 4, static_cast<size_t>(HD) * 4,
-                                    static_cast<size_t>(n), hipMemcpyDeviceToHost, m->stream));
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(kv_ptr(m, layer, which, kh)) + pos0 * HD * E;
+            HIPCHK(hipMemcpy2DAsync(static_cast<uint8_t*>(hdst) + static_cast<size_t>(kh) * HD * E,
+                                    static_cast<size_t>(NKV) * HD * E, src, static_cast<size_t>(HD) * E,
+                                    static_cast<size_t>(HD) * E, static_cast<size_t>(n), hipMemcpyDeviceToHost,
+                                    m->stream));
         }
+        HIPCHK(hipStreamSynchronize(m->stream));
+        if (E == 2)
+            for (size_t i = 0; i < tmp.size(); ++i) dst[i] = bf16_to_f32(tmp[i]);
     }
-    HIPCHK(hipStreamSynchronize(m->stream));
     return Q35_OK;
 }
 
+// Host rows into the cache; a bf16 cache stores them rounded to nearest even.
 q35_status q35_model_write_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t n, const float* k_host,
                               const float* v_host) {
     if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
         return q35::fail(Q35_ERR_ARG, "bad argument");
-    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
-    float* base = m->kv_arena + static_cast<int64_t>(layer) * 2 * NKV * m->max_ctx * HD;
+    const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim, E = m->kv_elem;
+    std::vector<uint16_t> tmp(m->kv_elem == 2 ? static_cast<size_t>(n) * NKV * HD : 0);
     for (int which = 0; which < 2; ++which) {
         const float* src = which == 0 ? k_host : v_host;
         if (!src) continue;
+        if (E == 2)
+            for (size_t i = 0; i < tmp.size(); ++i) tmp[i] = q35synth::f32_to_bf16(src[i]);
+        const void* hsrc = E == 2 ? static_cast<const void*>(tmp.data()) : static_cast<const void*>(src);
         for (int kh = 0; kh < NKV; ++kh) {
-            float* dst = base + (static_cast<int64_t>(which) * NKV + kh) * m->max_ctx * HD + pos0 * HD;
-            HIPCHK(hipMemcpy2DAsync(dst, static_cast<size_t>(HD) * 4, src + kh * HD, static_cast<size_t>(NKV) * HD * 4,
-                                    static_cast<size_t>(HD) * 4, static_cast<size_t>(n), hipMemcpyHostToDevice,
-                                    m->stream));
+            uint8_t* dst = reinterpret_cast<uint8_t*>(kv_ptr(m, layer, which, kh)) + pos0 * HD * E;
+            HIPCHK(hipMemcpy2DAsync(dst, static_cast<size_t>(HD) * E,
+                                    static_cast<const uint8_t*>(hsrc) + static_cast<size_t>(kh) * HD * E,
+                                    static_cast<size_t>(NKV) * HD * E, static_cast<size_t>(HD) * E,
+                                    static_cast<size_t>(n), hipMemcpyHostToDevice, m->stream));
         }
+        HIPCHK(hipStreamSynchronize(m->stream));
     }
-    HIPCHK(hipStreamSynchronize(m->stream));
     return Q35_OK;
 }
 
@@ -1266,9 +1300,10 @@ q35_status q35_model_fill_synthetic(q35_model* m, int64_t pos, uint64_t seed, fl
     for (int l = 0; l < m->d.n_layers_attn; ++l)
         for (int which = 0; which < 2; ++which)
             for (int kh = 0; kh < NKV; ++kh) {
-                float* dst = m->kv_arena + ((static_cast<int64_t>(l) * 2 + which) * NKV + kh) * m->max_ctx * HD;
+                float* dst = kv_ptr(m, l, which, kh);
                 const uint64_t stream = 0x4b560000ULL + (static_cast<uint64_t>(l) << 8) + (which << 4) + kh;
-                HIPCHK(q35k::launch_fill_normal(dst, pos * HD, q35synth::stream_key(seed, stream), 1.0f, m->stream));
+                HIPCHK(q35k::launch_fill_normal(dst, pos * HD, q35synth::stream_key(seed, stream), 1.0f,
+                                                m->stream, m->kv_elem == 2));
             }
     const int64_t ns = static_cast<int64_t>(m->d.n_layers_gdn) * m->d.gdn_v_heads * 128 * 128;
     HIPCHK(q35k::launch_fill_normal(m->gdn_state, ns, q35synth::stream_key(seed, 0x47444eULL), state_std, m->stream));

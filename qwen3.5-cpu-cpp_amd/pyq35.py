@@ -66,10 +66,15 @@ class GdnDecodeArgs(C.Structure):
 class AttnDecodeArgs(C.Structure):
     _fields_ = [("q_heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("rotary_dim", C.c_int32), ("pos", C.c_int32), ("n_splits", C.c_int32),
-                ("n_layers", C.c_int32), ("reserved", C.c_int32), ("max_context", C.c_int64), ("rope_theta", C.c_double), ("eps", C.c_float)] + [
+                ("n_layers", C.c_int32), ("kv_dtype", C.c_int32), ("max_context", C.c_int64),
+                ("rope_theta", C.c_double), ("eps", C.c_float)] + [
         (n, C.c_void_p) for n in ("qg", "k_new", "v_new", "q_norm", "k_norm", "k_cache",
                                   "v_cache", "out", "workspace")] + [
         ("workspace_bytes", C.c_uint64)]
+
+
+class ModelOptions(C.Structure):
+    _fields_ = [("kv_bytes_per_elem", C.c_int32), ("reserved", C.c_int32 * 7)]
 
 
 class GdnPrefillArgs(C.Structure):
@@ -83,7 +88,7 @@ class GdnPrefillArgs(C.Structure):
 
 class AttnPrefillArgs(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_tokens", "pos0", "q_heads", "kv_heads", "head_dim",
-                                         "rotary_dim")] + [
+                                         "rotary_dim", "kv_dtype", "reserved")] + [
         ("max_context", C.c_int64), ("rope_theta", C.c_double), ("eps", C.c_float),
         ("qkv", C.c_void_p), ("ld_qkv", C.c_int64)] + [
         (n, C.c_void_p) for n in ("q_norm", "k_norm", "k_cache", "v_cache", "out", "workspace")] + [
@@ -112,6 +117,9 @@ def _load():
         "q35_synth_normal": (S, [P, I64, U64, U64, F, I32]),
         "q35_model_create": (S, [C.POINTER(Dims), C.POINTER(Tensor), I32, I64, C.POINTER(P)]),
         "q35_model_open": (S, [C.c_char_p, I64, C.POINTER(P)]),
+        "q35_model_open_opts": (S, [C.c_char_p, I64, C.POINTER(ModelOptions), C.POINTER(P)]),
+        "q35_model_create_opts": (S, [C.POINTER(Dims), C.POINTER(Tensor), I32, I64, C.POINTER(ModelOptions),
+                                      C.POINTER(P)]),
         "q35_model_destroy": (None, [P]),
         "q35_model_dims": (S, [P, C.POINTER(Dims)]),
         "q35_model_budget": (S, [P, C.POINTER(Budget)]),
@@ -212,9 +220,10 @@ def synth_normal(n: int, seed: int, stream: int, std: float = 1.0) -> np.ndarray
 class Model:
     """The device-resident decoder (QwenModel on the GPU)."""
 
-    def __init__(self, model_dir: str, max_context: int):
+    def __init__(self, model_dir: str, max_context: int, kv_bytes_per_elem: int = 4):
         h = C.c_void_p()
-        check(lib.q35_model_open(model_dir.encode(), max_context, C.byref(h)))
+        opt = ModelOptions(kv_bytes_per_elem=kv_bytes_per_elem)
+        check(lib.q35_model_open_opts(model_dir.encode(), max_context, C.byref(opt), C.byref(h)))
         self.h = h
         d = Dims()
         check(lib.q35_model_dims(h, C.byref(d)))

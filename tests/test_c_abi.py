@@ -196,6 +196,9 @@ def test_model_create_rejects_unsupported_shapes(model_dirs):
     assert pyq35.lib.q35_model_create(C.byref(d), tab, len(tab), 64, C.byref(h)) == -7
     d = pyq35.dims_for("tiny")
     assert pyq35.lib.q35_model_create(C.byref(d), tab, len(tab), 0, C.byref(h)) == -6
+    opt = pyq35.ModelOptions(kv_bytes_per_elem=1)
+    assert pyq35.lib.q35_model_create_opts(C.byref(d), tab, len(tab), 64, C.byref(opt), C.byref(h)) == -7
+    assert b"KV cache element" in pyq35.lib.q35_last_error()
 
 
 def test_model_open_reports_bad_files(tmp_path, model_dirs):
@@ -222,5 +225,18 @@ def test_kernel_entry_points_validate_before_launch():
     at = pyq35.AttnDecodeArgs(q_heads=8, kv_heads=2, head_dim=256, rotary_dim=64, pos=5,
                               max_context=4)
     assert pyq35.lib.q35_attn_decode(C.byref(at), None) == -6
+    # cache element type: only 0 (fp32) and 1 (bf16); pointers are never dereferenced
+    fake = dict(qg=1 << 20, k_new=1 << 20, v_new=1 << 20, q_norm=1 << 20, k_norm=1 << 20,
+                k_cache=1 << 20, v_cache=1 << 20, out=1 << 20, workspace=1 << 20)
+    at = pyq35.AttnDecodeArgs(q_heads=8, kv_heads=2, head_dim=256, rotary_dim=64, pos=1, max_context=4,
+                              kv_dtype=2, workspace_bytes=1 << 30, **fake)
+    assert pyq35.lib.q35_attn_decode(C.byref(at), None) == -1
+    assert b"kv_dtype" in pyq35.lib.q35_last_error()
+    ap = pyq35.AttnPrefillArgs(n_tokens=1, q_heads=8, kv_heads=2, head_dim=256, rotary_dim=64, kv_dtype=-1,
+                               max_context=4, ld_qkv=5120, workspace_bytes=1 << 30,
+                               **{k: v for k, v in fake.items() if k not in ("qg", "k_new", "v_new")},
+                               qkv=1 << 20)
+    assert pyq35.lib.q35_attn_prefill(C.byref(ap), None) == -1
+    assert b"kv_dtype" in pyq35.lib.q35_last_error()
     assert pyq35.lib.q35_matmul_bf16(None, None, None, 4, 8, None) == -1
     assert pyq35.lib.q35_matmul_bf16(1 << 20, 1 << 20, 1 << 20, 4, 12, None) == -7

@@ -291,3 +291,51 @@ def test_scalar_activations(x):
     assert op.olib.orc_softplus(x) == pytest.approx(x if x > 20 else math.log1p(math.exp(x)), rel=1e-6)
     assert op.olib.orc_sigmoid(x) == pytest.approx(1 / (1 + math.exp(-x)), rel=1e-6, abs=1e-30)
     assert op.olib.orc_silu(x) == pytest.approx(x / (1 + math.exp(-x)), rel=1e-6, abs=1e-30)
+
+
+def test_round_bf16_matches_torch_cast():
+    """The bf16 cache rounding against torch's fp32 -> bfloat16 cast (nearest, ties to even):
+    random values, exact ties both ways, subnormals, the overflow edge, infinities, NaN."""
+    torch = pytest.importorskip("torch")
+    base = rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 20000)
+    hi = (rng.integers(0, 1 << 16, 4000, dtype=np.uint32) << 16)
+    ties = np.concatenate([hi | 0x8000, (hi | 0x18000) & 0xffffffff, hi | 0x7fff, hi | 0x8001]).view(np.float32)
+    special = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-40, 3.389e38, 3.4e38, -3.4e38, np.inf, -np.inf,
+                        3.4028235e38, 1.1754944e-38], np.float32)
+    x = np.concatenate([base, ties[np.isfinite(ties)], special]).astype(np.float32)
+    got = op.round_bf16(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(op.olib.orc_round_bf16(float("nan")))
+    # every result is a bf16 value and the nearest one
+    assert not np.any(got[np.isfinite(got)].view(np.uint32) & 0xffff)
+    assert op.round_bf16(np.float32(1.00390625)) == 1.0        # tie (1 + 2^-8) -> even 1.0
+    assert op.round_bf16(np.float32(1.01171875)) == 1.015625   # tie (1 + 3 * 2^-8) -> even
+
+
+def test_attention_bf16_cache_rounds_appended_rows():
+    """kv_bf16: the appended rows are the fp32 rows rounded to bf16 and the output equals the
+    attention over the rounded caches (append off on the same contents); with bf16-exact
+    history the fp32 and bf16 paths differ only through the rounded row."""
+    pos = 33
+    qg, kn, vn, K, V = _attn_case(pos)
+    K[:pos] = op.round_bf16(K[:pos])
+    V[:pos] = op.round_bf16(V[:pos])
+    qn = rng.standard_normal(256).astype(np.float32) * 0.1
+    knw = rng.standard_normal(256).astype(np.float32) * 0.1
+    K32, V32 = K.copy(), V.copy()
+    out32 = op.attn_core_ex(D, pos, qg, kn, vn, qn, knw, K32, V32, False, True)
+    np.testing.assert_array_equal(out32, op.attn_core(D, pos, qg, kn, vn, qn, knw, K.copy(), V.copy()))
+    Kb, Vb = K.copy(), V.copy()
+    outb = op.attn_core_ex(D, pos, qg, kn, vn, qn, knw, Kb, Vb, True, True)
+    torch = pytest.importorskip("torch")
+    as_bf16 = lambda a: torch.from_numpy(a).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(Kb[pos], as_bf16(K32[pos]))
+    np.testing.assert_array_equal(Vb[pos], as_bf16(V32[pos]))
+    np.testing.assert_array_equal(Kb[:pos], K[:pos])
+    # the same caches with append off give the same output bit for bit
+    zero = np.zeros_like(kn)
+    again = op.attn_core_ex(D, pos, qg, zero, zero, qn, knw, Kb.copy(), Vb.copy(), True, False)
+    np.testing.assert_array_equal(again, outb)
+    # and the output moved by no more than bf16 rounding of one row can move it
+    assert 0 < np.linalg.norm(outb - out32) / np.linalg.norm(out32) < 4e-3
