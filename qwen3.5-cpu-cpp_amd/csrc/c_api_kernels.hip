@@ -105,9 +105,10 @@ q35_status q35_gdn_decode(const q35_gdn_decode_args* args, q35_stream s) {
 
 uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args* args) {
     if (!args || args->kv_heads <= 0 || args->q_heads <= 0) return 0;
-    const int splits = args->n_splits > 0 ? args->n_splits
-                                          : q35k::attn_default_splits(args->max_context, args->kv_heads, q35k::device_cu_count());
     const uint64_t layers = args->n_layers > 0 ? static_cast<uint64_t>(args->n_layers) : 1;
+    const int splits = args->n_splits > 0 ? args->n_splits
+                                          : q35k::attn_default_splits(args->max_context, args->kv_heads * static_cast<int>(layers),
+                                                                      q35k::device_cu_count());
     return layers * static_cast<uint64_t>(q35k::attn_partial_floats(args->q_heads, args->kv_heads, args->head_dim, splits)) * 4;
 }
 
@@ -134,7 +135,9 @@ q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
         return q35::fail(Q35_ERR_ARG, "q35_attn_decode: workspace of %llu bytes, needs %llu",
                          static_cast<unsigned long long>(g.workspace_bytes),
                          static_cast<unsigned long long>(q35_attn_decode_workspace_bytes(args)));
-    const int splits = g.n_splits > 0 ? g.n_splits : q35k::attn_default_splits(g.max_context, g.kv_heads, q35k::device_cu_count());
+    const int splits = g.n_splits > 0 ? g.n_splits
+                                      : q35k::attn_default_splits(g.max_context, g.kv_heads * std::max(1, g.n_layers),
+                                                                  q35k::device_cu_count());
     q35k::AttnDecodeArgs a{};
     a.NQ = g.q_heads;
     a.NKV = g.kv_heads;

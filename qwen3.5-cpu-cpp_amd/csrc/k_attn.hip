@@ -23,6 +23,9 @@
 //            sigmoid(gate).
 #include <math.h>
 
+#include <cstdlib>
+#include <type_traits>
+
 #include "dev_common.hpp"
 #include "launch.hpp"
 
@@ -408,6 +411,382 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- matrix-core partial kernel
+// GQA group of 8 (the 2B shape), rotary dims a multiple of 32. Same split-K partials as
+// attn_partial_kernel, with the dot products on v_mfma_f32_16x16x4f32 (fp32 operands, fp32
+// accumulation): for a tile of 16 cache positions, S[16 pos][16 cols] = K_tile . Q^T with
+// the 8 query heads in columns 0-7 (8-15 are zero), then O[16 rows][16 dims] += P . V_tile
+// with the heads in rows 0-7. A lane l (column / row l % 16, group g = l / 16) holds
+//   K operand   K[p0 + l%16][16c + 4g + i]              (float4 per c: 64 B per row / instr)
+//   Q operand   Q[head l%16][16c + 4g + i]              (from LDS, same dim order)
+//   scores      S[p0 + 4g + r][head l%16], r = 0..3     (the MFMA output registers)
+//   P operand   P[head l%16][p0 + 4g + v] = score reg v  (no data movement)
+//   V operand   V[p0 + 4g + v][64t + 4(l%16) + i]       (float4 per (v, t): 256 B per row)
+//   O           O[head 4g + r][64t + 4(l%16) + i]        (16 accumulator tiles)
+// so no lane exchange is needed between the two products; the softmax of a tile reduces
+// over the 4 registers and the 4 lane groups (two exchanges). Four waves per workgroup
+// walk whole tiles; their (m, l, O) are merged through LDS at the end.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int kMW = 4;  // waves per workgroup of the matrix-core kernel
+
+template <bool KVB>
+struct KvRaw;
+template <>
+struct KvRaw<false> {
+    using T = float4;
+    static __device__ __forceinline__ T load(const float* base, int64_t off) { return load_stream(base + off); }
+    static __device__ __forceinline__ float4 f4(const T& v) { return v; }
+};
+template <>
+struct KvRaw<true> {
+    using T = uint2;
+    static __device__ __forceinline__ T load(const float* base, int64_t off) {
+        typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+        const u2 v = __builtin_nontemporal_load(reinterpret_cast<const u2*>(reinterpret_cast<const uint16_t*>(base) + off));
+        return make_uint2(v.x, v.y);
+    }
+    static __device__ __forceinline__ float4 f4(const T& v) {
+        return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+    }
+};
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// rmsnorm (1 + w) + RoPE of one 256-vector held as 4 dims per lane (dims 4 lane .. + 3),
+// sum of squares in double; cos / sin of dims (d mod ROT/2) for d < ROT from the table or
+// from the double-precision angle (src/forward_pass.cpp:77-84,102-112).
+__device__ __forceinline__ float4 norm_rope_row(float4 x, float4 w, float4 c, float4 sn, int lane, int ROT, float eps) {
+    double ss = static_cast<double>(x.x) * x.x + static_cast<double>(x.y) * x.y + static_cast<double>(x.z) * x.z +
+                static_cast<double>(x.w) * x.w;
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + eps);
+    float4 y;
+    y.x = x.x * inv * (1.0f + w.x);
+    y.y = x.y * inv * (1.0f + w.y);
+    y.z = x.z * inv * (1.0f + w.z);
+    y.w = x.w * inv * (1.0f + w.w);
+    const int hq = ROT / 8;  // lanes holding the first half of the rotated dims
+    const int src = lane < hq ? lane + hq : lane - hq;
+    float4 o;  // the partner dims d +- ROT/2
+    o.x = __shfl(y.x, src);
+    o.y = __shfl(y.y, src);
+    o.z = __shfl(y.z, src);
+    o.w = __shfl(y.w, src);
+    if (lane < hq) {
+        y.x = y.x * c.x - o.x * sn.x;
+        y.y = y.y * c.y - o.y * sn.y;
+        y.z = y.z * c.z - o.z * sn.z;
+        y.w = y.w * c.w - o.w * sn.w;
+    } else if (lane < 2 * hq) {
+        y.x = y.x * c.x + o.x * sn.x;
+        y.y = y.y * c.y + o.y * sn.y;
+        y.z = y.z * c.z + o.z * sn.z;
+        y.w = y.w * c.w + o.w * sn.w;
+    }
+    return y;
+}
+
+// weight of a wave's partial with maximum mw in a merge with maximum M (0 for an empty wave)
+__device__ __forceinline__ float m_run_of(float mw, float M) { return mw == -INFINITY ? 0.0f : expf(mw - M); }
+
+template <bool KVB>
+__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a) {
+    attn_select_layer(a, blockIdx.z);
+    using KV = KvRaw<KVB>;
+    using KT = typename KV::T;
+    constexpr int GRP = 8, TP = 16;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop bounds
+    const int n16 = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, kh = blockIdx.y;
+    const int pos = read_pos(a);
+    const int n = pos + 1;
+    const int per = split_len(n, a.n_splits);
+    const int j0 = split * per;
+    if (j0 >= n) return;
+    const int j1 = min(n, j0 + per);
+    const bool owns_new = j1 == n;
+    const int tpw = ((j1 - j0 + TP - 1) / TP + kMW - 1) / kMW;  // tiles per wave
+    const int w0 = min(j1, j0 + wave * tpw * TP), w1 = min(j1, w0 + tpw * TP);
+    // the wave ending at pos walks the cached positions only; the appended row is added at
+    // the end from LDS (so nothing in the tile loop depends on where pos falls)
+    const bool has_new = owns_new && w0 < w1 && w1 == n;  // empty waves also end at n
+    const int wl = has_new ? w1 - 1 : w1;
+
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    const float* Kc_ = KVB ? reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff)
+                           : a.k_cache + hoff;
+    const float* Vc_ = KVB ? reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff)
+                           : a.v_cache + hoff;
+    const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
+
+    __shared__ float4 qs[16][64];             // Q operand: [c][lane]
+    __shared__ float4 ks[kHD / 4], vs[kHD / 4];  // the appended rows (as the cache holds them)
+    __shared__ float os[kMW][GRP][kHD];
+    __shared__ float ml_s[kMW][GRP][2];
+
+    // ---- prologue loads first (rows of this wave: q heads wave, wave + 4; the key on wave
+    // 0 and the value on wave 1 of the workgroup holding pos), then the first K / V tiles
+    const int ROT = a.ROT, half = ROT / 2;
+    float4 px[3], pw[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
+        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
+                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
+        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
+        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
+    }
+    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    const int ci = (lane * 4) % max(half, 4);  // table column of this lane's first dim
+    float4 cs4 = make_float4(1.f, 1.f, 1.f, 1.f), sn4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.rope_cs) {
+        const float* t = a.rope_cs + static_cast<int64_t>(pos) * ROT;
+        cs4 = *reinterpret_cast<const float4*>(t + min(ci, max(half - 4, 0)));
+        sn4 = *reinterpret_cast<const float4*>(t + half + min(ci, max(half - 4, 0)));
+    }
+    KT kA[16], vr[4][4];
+    // Loads are issued unconditionally (a load under a branch makes the wait-count pass wait
+    // for all outstanding loads at the join); past the end of the range every lane reads the
+    // same 16 bytes of row w1 - 1, which costs the memory pipeline almost nothing.
+    const int last = max(wl - 1, 0);  // a valid row to clamp to
+    auto loadK = [&](KT (&kr)[16], int p0) {
+        const int mask = -static_cast<int>(p0 < wl);  // all ones while live (no branch)
+        const int64_t row = min(p0 + n16, last);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) kr[c] = KV::load(Kc_, row * kHD + ((16 * c + 4 * g) & mask));
+    };
+    auto loadV = [&](int p0) {
+        const int mask = -static_cast<int>(p0 < wl);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t row = min((p0 + 4 * g + v) & mask, last) | (last & ~mask);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) vr[v][t] = KV::load(Vc_, row * kHD + ((64 * t + 4 * n16) & mask));
+        }
+    };
+    loadK(kA, w0);
+    loadV(w0);
+
+    // ---- Q operand and the appended rows
+    if (!a.rope_cs) {  // double-precision angles, as the reference: one per lane, then shared
+        float cv = 1.0f, sv = 0.0f;
+        if (lane < half) {
+            const double inv_freq = pow(a.theta, -static_cast<double>(2 * lane) / ROT);
+            const double ang = static_cast<double>(pos) * inv_freq;
+            cv = static_cast<float>(cos(ang));
+            sv = static_cast<float>(sin(ang));
+        }
+        const int c0 = min(ci, 60);
+        cs4 = make_float4(__shfl(cv, c0), __shfl(cv, c0 + 1), __shfl(cv, c0 + 2), __shfl(cv, c0 + 3));
+        sn4 = make_float4(__shfl(sv, c0), __shfl(sv, c0 + 1), __shfl(sv, c0 + 2), __shfl(sv, c0 + 3));
+    }
+    for (int e = tid; e < 16 * 32; e += kMW * 64)  // columns 8-15: zero heads
+        qs[e >> 5][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = wave + i * kMW;
+        if (r > GRP || (r == GRP && !owns_new)) continue;  // uniform per wave
+        float4 y = norm_rope_row(px[i], pw[i], cs4, sn4, lane, ROT, a.eps);
+        if (r < GRP) {
+            qs[lane >> 2][16 * (lane & 3) + r] = y;  // dims 4 lane .. + 3 of head r
+        } else {
+            const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + lane * 4;
+            if constexpr (KVB) {
+                const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.k_cache) + off) =
+                    make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
+                y = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
+            } else {
+                *reinterpret_cast<float4*>(a.k_cache + off) = y;
+            }
+            ks[lane] = y;
+        }
+    }
+    if (owns_new && wave == 1) {
+        const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + lane * 4;
+        float4 y = vn4;
+        if constexpr (KVB) {
+            const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.v_cache) + off) =
+                make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
+            y = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
+        } else {
+            *reinterpret_cast<float4*>(a.v_cache + off) = y;
+        }
+        vs[lane] = y;
+    }
+    __syncthreads();
+
+    floatx4 O[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) O[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;  // of head n16 (same in the 4 lane groups)
+
+    // one tile of positions p0 .. p0 + 15 from K registers kr and the V registers; the next
+    // tile's rows are requested as soon as these registers are consumed
+    auto tile = [&](KT (&kr)[16], int p0) {
+        // four independent accumulation chains (dims 16c + 4g + i, one chain per i)
+        floatx4 S4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const float4 q = qs[c][lane];
+            const float4 k = KV::f4(kr[c]);
+            S4[0] = mfma16(k.x, q.x, S4[0]);
+            S4[1] = mfma16(k.y, q.y, S4[1]);
+            S4[2] = mfma16(k.z, q.z, S4[2]);
+            S4[3] = mfma16(k.w, q.w, S4[3]);
+            // keep the Q operand reads close to their use (a few in flight, not all 16)
+            if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+        const floatx4 S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
+        loadK(kr, p0 + TP);
+        float s[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = p0 + 4 * g + r < wl ? S[r] * sc : -INFINITY;
+        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        tm = fmaxf(tm, xchg(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        // the reference max moves only when a score exceeds it by more than 8 (the weights
+        // exp(s - m) stay below e^8, far from overflow), so the accumulators are rarely rescaled
+        const float m_new = tm > m_run + 8.0f ? tm : m_run;
+        const float f = expf(m_run - m_new);
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = n16 < GRP ? expf(s[r] - m_new) : 0.0f;
+            ps += p[r];
+        }
+        ps += xchg(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l_run = l_run * f + ps;
+        m_run = m_new;
+        if (__any(f != 1.0f)) {  // rescale the accumulators of heads 4g + r
+            float fh[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) fh[r] = __shfl(f, 4 * g + r);
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                O[t][0] *= fh[0];
+                O[t][1] *= fh[1];
+                O[t][2] *= fh[2];
+                O[t][3] *= fh[3];
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float4 vv = KV::f4(vr[v][t]);
+                O[4 * t + 0] = mfma16(p[v], vv.x, O[4 * t + 0]);
+                O[4 * t + 1] = mfma16(p[v], vv.y, O[4 * t + 1]);
+                O[4 * t + 2] = mfma16(p[v], vv.z, O[4 * t + 2]);
+                O[4 * t + 3] = mfma16(p[v], vv.w, O[4 * t + 3]);
+            }
+        loadV(p0 + TP);
+    };
+    for (int p0 = w0; p0 < wl; p0 += TP) tile(kA, p0);
+
+    if (has_new) {  // position pos: score of head h = lane & 7 over the 32 dims of chunk lane >> 3
+        const int h = lane & 7, j = lane >> 3;
+        float d = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                const float4 q = qs[2 * j + cc][16 * gg + h], kk = ks[4 * (2 * j + cc) + gg];
+                d = fmaf(q.x, kk.x, d);
+                d = fmaf(q.y, kk.y, d);
+                d = fmaf(q.z, kk.z, d);
+                d = fmaf(q.w, kk.w, d);
+            }
+        d += __shfl_xor(d, 8);
+        d += __shfl_xor(d, 16);
+        d += __shfl_xor(d, 32);
+        const float sn = __shfl(d, n16 & 7) * sc;  // the score of head n16
+        const float m_new = sn > m_run + 8.0f ? sn : m_run;
+        const float f = expf(m_run - m_new);
+        const float pn = n16 < GRP ? expf(sn - m_new) : 0.0f;
+        l_run = l_run * f + pn;
+        m_run = m_new;
+        float fh[4], ph[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            fh[r] = __shfl(f, 4 * g + r);
+            ph[r] = __shfl(pn, 4 * g + r);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float4 v = vs[16 * t + n16];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                O[4 * t + 0][r] = fmaf(ph[r], v.x, O[4 * t + 0][r] * fh[r]);
+                O[4 * t + 1][r] = fmaf(ph[r], v.y, O[4 * t + 1][r] * fh[r]);
+                O[4 * t + 2][r] = fmaf(ph[r], v.z, O[4 * t + 2][r] * fh[r]);
+                O[4 * t + 3][r] = fmaf(ph[r], v.w, O[4 * t + 3][r] * fh[r]);
+            }
+        }
+    }
+
+    // ---- merge the waves: maxima first, then each wave rescales its own accumulators to the
+    // workgroup maximum and the four are summed in a fixed order
+    if (g == 0 && n16 < GRP) {
+        ml_s[wave][n16][0] = m_run;
+        ml_s[wave][n16][1] = l_run;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (g < 2) {
+        float sc4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * g + r;
+            float M = ml_s[0][h][0];
+#pragma unroll
+            for (int w = 1; w < kMW; ++w) M = fmaxf(M, ml_s[w][h][0]);
+            sc4[r] = m_run_of(ml_s[wave][h][0], M);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4*>(&os[wave][4 * g + r][64 * t + 4 * n16]) =
+                    make_float4(O[4 * t][r] * sc4[r], O[4 * t + 1][r] * sc4[r], O[4 * t + 2][r] * sc4[r],
+                                O[4 * t + 3][r] * sc4[r]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
+#pragma unroll
+    for (int it = 0; it < GRP * kHD / (4 * kMW * 64); ++it) {
+        const int e = (it * kMW * 64 + tid) * 4, h = e / kHD, dd = e - h * kHD;
+        float4 o = *reinterpret_cast<const float4*>(&os[0][h][dd]);
+#pragma unroll
+        for (int w = 1; w < kMW; ++w) {
+            const float4 x = *reinterpret_cast<const float4*>(&os[w][h][dd]);
+            o.x += x.x;
+            o.y += x.y;
+            o.z += x.z;
+            o.w += x.w;
+        }
+        *reinterpret_cast<float4*>(a.part_o + base * kHD + e) = o;
+    }
+    if (tid < GRP) {
+        float M = ml_s[0][tid][0];
+        for (int w = 1; w < kMW; ++w) M = fmaxf(M, ml_s[w][tid][0]);
+        float L = 0.0f;
+        for (int w = 0; w < kMW; ++w) L += ml_s[w][tid][1] * m_run_of(ml_s[w][tid][0], M);
+        a.part_ml[(base + tid) * 2] = M;
+        a.part_ml[(base + tid) * 2 + 1] = L;
+    }
+}
+
 // grid (NQ, HD / 64), 256 threads: wave w merges splits w, w+4, ... for 64 dims (one per lane)
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
     attn_select_layer(a, blockIdx.z);
@@ -459,15 +838,30 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
 
 template <int GRP>
 hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
+    if (GRP == 8 && a.ROT % 32 == 0 && a.ROT > 0 && !attn_force_valu()) {
+        dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
+        if (a.kv_bf16) klaunch(attn_mfma_kernel<true>, grid, kMW * 64, 0, s, a);
+        else klaunch(attn_mfma_kernel<false>, grid, kMW * 64, 0, s, a);
+        return hipGetLastError();
+    }
     constexpr int LPP = GRP <= 4 ? 16 : 32;
     dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
     constexpr int BATCH = GRP <= 4 ? 8 : GRP == 8 ? 4 : 2;
-    if (a.kv_bf16) attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), true><<<grid, kWaves * 64, 0, s>>>(a);
-    else attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), false><<<grid, kWaves * 64, 0, s>>>(a);
+    if (a.kv_bf16) klaunch(attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), true>, grid, kWaves * 64, 0, s, a);
+    else klaunch(attn_partial_kernel<GRP, LPP, BATCH, (GRP <= 8), false>, grid, kWaves * 64, 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
+
+// Q35_ATTN_VALU=1 keeps the vector-ALU kernel for every group size (for comparisons).
+bool attn_force_valu() {
+    static const bool v = [] {
+        const char* e = std::getenv("Q35_ATTN_VALU");
+        return e && e[0] == '1';
+    }();
+    return v;
+}
 
 hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s) {
     switch (a.NQ / a.NKV) {
@@ -490,7 +884,7 @@ int device_cu_count() {
 
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s) {
     dim3 grid(a.NQ, kHD / 64, a.n_layers > 0 ? a.n_layers : 1);
-    attn_combine_kernel<<<grid, 256, 0, s>>>(a);
+    klaunch(attn_combine_kernel, grid, 256, 0, s, a);
     return hipGetLastError();
 }
 

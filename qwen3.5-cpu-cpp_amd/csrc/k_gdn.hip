@@ -179,10 +179,10 @@ hipError_t launch_gdn_decode(const GdnDecodeArgs& in, bool fuse_norm, hipStream_
     if (!a.ls_out) a.ls_out = VD;
     if (fuse_norm) {
         dim3 grid(a.VH, a.n_layers);
-        gdn_decode_kernel<128, true><<<grid, 256, 0, s>>>(a);
+        klaunch(gdn_decode_kernel<128, true>, grid, 256, 0, s, a);
     } else {
         dim3 grid(a.VH * (kD / 32), a.n_layers);
-        gdn_decode_kernel<32, false><<<grid, 256, 0, s>>>(a);
+        klaunch(gdn_decode_kernel<32, false>, grid, 256, 0, s, a);
     }
     return hipGetLastError();
 }

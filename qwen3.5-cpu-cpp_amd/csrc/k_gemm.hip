@@ -147,8 +147,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
-    if (a.R) gemm_kernel<true><<<grid, 256, 0, s>>>(a);
-    else gemm_kernel<false><<<grid, 256, 0, s>>>(a);
+    if (a.R) klaunch(gemm_kernel<true>, grid, 256, 0, s, a);
+    else klaunch(gemm_kernel<false>, grid, 256, 0, s, a);
     return hipGetLastError();
 }
 

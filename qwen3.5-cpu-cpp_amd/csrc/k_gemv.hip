@@ -328,10 +328,10 @@ hipError_t launch_kc(const GemvArgs& a, hipStream_t s) {
     const int max_blocks = gemv_max_blocks();
     if (EPI == kEpiSwiGluPair || a.rows >= 8192) {
         const int blocks = min(max_blocks, (a.rows + 7) / 8);
-        gemv_kernel<PRO, EPI, 2, NX, KC><<<blocks, 256, lds, s>>>(a);
+        klaunch(gemv_kernel<PRO, EPI, 2, NX, KC>, blocks, 256, lds, s, a);
     } else {
         const int blocks = min(max_blocks, (a.rows + 3) / 4);
-        gemv_kernel<PRO, EPI, 1, NX, KC><<<blocks, 256, lds, s>>>(a);
+        klaunch(gemv_kernel<PRO, EPI, 1, NX, KC>, blocks, 256, lds, s, a);
     }
     return hipGetLastError();
 }

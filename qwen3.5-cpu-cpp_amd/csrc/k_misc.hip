@@ -185,24 +185,24 @@ int grid_for(int64_t n) {
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
                                float eps, int gated, const float* gate, hipStream_t s) {
-    rmsnorm_rows_kernel<<<rows, 256, 0, s>>>(x, w, y, n, eps, gated, gate);
+    klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate);
     return hipGetLastError();
 }
 
 hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s) {
-    l2norm_rows_kernel<<<rows, 256, 0, s>>>(x, n, eps);
+    klaunch(l2norm_rows_kernel, rows, 256, 0, s, x, n, eps);
     return hipGetLastError();
 }
 
 hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
                             double theta, hipStream_t s) {
-    rope_rows_kernel<<<rows, 64, 0, s>>>(x, hd, rot, pos, pos0, theta);
+    klaunch(rope_rows_kernel, rows, 64, 0, s, x, hd, rot, pos, pos0, theta);
     return hipGetLastError();
 }
 
 hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* hidden, int H,
                         hipStream_t s) {
-    embed_kernel<<<(H + 255) / 256, 256, 0, s>>>(embed, token_dev, hidden, H);
+    klaunch(embed_kernel, (H + 255) / 256, 256, 0, s, embed, token_dev, hidden, H);
     return hipGetLastError();
 }
 
@@ -210,40 +210,45 @@ hipError_t launch_argmax(const float* logits, int n, void* part, int* token_out,
                          int* pos, hipStream_t s) {
     float* pv = static_cast<float*>(part);
     int* pi = reinterpret_cast<int*>(pv + kArgmaxBlocks);
-    argmax_pass1<<<kArgmaxBlocks, 256, 0, s>>>(logits, n, pv, pi);
-    argmax_pass2<<<1, 256, 0, s>>>(pv, pi, token_out, ids, pos);
+    klaunch(argmax_pass1, kArgmaxBlocks, 256, 0, s, logits, n, pv, pi);
+    klaunch(argmax_pass2, 1, 256, 0, s, pv, pi, token_out, ids, pos);
     return hipGetLastError();
 }
 
 hipError_t launch_add_int(int* p, int v, hipStream_t s) {
-    add_int_kernel<<<1, 1, 0, s>>>(p, v);
+    klaunch(add_int_kernel, 1, 1, 0, s, p, v);
     return hipGetLastError();
 }
 
 hipError_t launch_set_int(int* p, int v, hipStream_t s) {
-    set_int_kernel<<<1, 1, 0, s>>>(p, v);
+    klaunch(set_int_kernel, 1, 1, 0, s, p, v);
     return hipGetLastError();
 }
 
 hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t s) {
-    copy_kernel<<<grid_for(n), 256, 0, s>>>(dst, src, n);
+    klaunch(copy_kernel, grid_for(n), 256, 0, s, dst, src, n);
     return hipGetLastError();
 }
 
 hipError_t launch_fill_f32(float* dst, int64_t n, float v, hipStream_t s) {
-    fill_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, v);
+    klaunch(fill_kernel, grid_for(n), 256, 0, s, dst, n, v);
     return hipGetLastError();
 }
 
 hipError_t launch_fill_normal(float* dst, int64_t n, uint64_t key, float std, hipStream_t s, bool bf16) {
-    if (bf16) fill_normal_bf16_kernel<<<grid_for(n), 256, 0, s>>>(reinterpret_cast<uint16_t*>(dst), n, key, std);
-    else fill_normal_kernel<<<grid_for(n), 256, 0, s>>>(dst, n, key, std);
+    if (bf16) klaunch(fill_normal_bf16_kernel, grid_for(n), 256, 0, s, reinterpret_cast<uint16_t*>(dst), n, key, std);
+    else klaunch(fill_normal_kernel, grid_for(n), 256, 0, s, dst, n, key, std);
     return hipGetLastError();
+}
+
+LaunchTimer*& launch_timer() {
+    static thread_local LaunchTimer* t = nullptr;
+    return t;
 }
 
 hipError_t launch_rope_table(float* t, int64_t n_pos, int rot, double theta, hipStream_t s) {
     if (rot <= 0) return hipSuccess;
-    rope_table_kernel<<<grid_for(n_pos * (rot / 2)), 256, 0, s>>>(t, n_pos, rot, theta);
+    klaunch(rope_table_kernel, grid_for(n_pos * (rot / 2)), 256, 0, s, t, n_pos, rot, theta);
     return hipGetLastError();
 }
 

@@ -305,7 +305,6 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
 // ------------------------------------------------------------------ GDN chunk output
 constexpr int kLdQ = kD + 4;    // Q rows (A operand)
 constexpr int kLdS = kD + 16;   // state / v_new rows (B operand)
-constexpr int kLdP = kC + 4;    // P rows (A operand)
 
 // grid (VH, Tp / 64), 256 threads: o = e^gamma (Q S_c) + P v_new for one chunk of one v-head,
 // then the gated rmsnorm (src/forward_pass.cpp:86-93, sum of squares in double) or the raw
@@ -621,30 +620,30 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
 }
 
 hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
-    gdn_prep_kernel<<<dim3(a.T, a.KH), 256, 0, s>>>(a);
-    if (a.Tp > a.T) gdn_pad_kernel<<<blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s>>>(a);
-    gdn_ring_kernel<<<blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s>>>(a);
-    gdn_chunk_kernel<<<dim3(a.VH, a.Tp / kC), 256, 0, s>>>(a);
-    gdn_state_kernel<<<dim3(a.VH, kD / kSW), 256, 0, s>>>(a);
-    gdn_out_kernel<<<dim3(a.VH, a.Tp / kC), 256, 0, s>>>(a);
+    klaunch(gdn_prep_kernel, dim3(a.T, a.KH), 256, 0, s, a);
+    if (a.Tp > a.T) klaunch(gdn_pad_kernel, blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s, a);
+    klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
+    klaunch(gdn_chunk_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
+    klaunch(gdn_state_kernel, dim3(a.VH, kD / kSW), 256, 0, s, a);
+    klaunch(gdn_out_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
     return hipGetLastError();
 }
 
 int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_t>(NQ) * T * kHD + 64; }
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
-    attn_prefill_prep_kernel<<<dim3(a.T, a.NQ + a.NKV), 256, 0, s>>>(a);
-    flash_attn_kernel<<<dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s>>>(a);
+    klaunch(attn_prefill_prep_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
+    klaunch(flash_attn_kernel, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s) {
-    swiglu_rows_kernel<<<blocks_for(static_cast<int64_t>(T) * I), 256, 0, s>>>(gu, h, T, I);
+    klaunch(swiglu_rows_kernel, blocks_for(static_cast<int64_t>(T) * I), 256, 0, s, gu, h, T, I);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s) {
-    embed_rows_kernel<<<blocks_for(static_cast<int64_t>(T) * H), 256, 0, s>>>(embed, ids, hidden, T, H);
+    klaunch(embed_rows_kernel, blocks_for(static_cast<int64_t>(T) * H), 256, 0, s, embed, ids, hidden, T, H);
     return hipGetLastError();
 }
 

@@ -1,12 +1,34 @@
 #pragma once
 // Host-side launchers of the gfx950 kernels. Each returns the hipError_t of its launch.
 // Shapes are checked by the callers (c_api_kernels.hip, runtime.hip) before launching.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdint>
 
 namespace q35k {
+
+// Per-launch timing of a host thread. While launch_timer() is set, every launch records the
+// kernel's own start (first launch) and end (every launch) in the two events, through
+// hipExtLaunchKernelGGL: the events take the dispatch's begin / end timestamps, so the host
+// and queue overheads between launches are not counted (what a kernel trace reports).
+struct LaunchTimer {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool started = false;
+};
+LaunchTimer*& launch_timer();
+
+template <typename... KArgs, typename... Args>
+inline void klaunch(void (*k)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+    if (LaunchTimer* t = launch_timer()) {
+        hipExtLaunchKernelGGL(k, grid, block, lds, s, t->started ? nullptr : t->start, t->stop, 0u,
+                              static_cast<KArgs>(args)...);
+        t->started = true;
+    } else {
+        k<<<grid, block, lds, s>>>(static_cast<KArgs>(args)...);
+    }
+}
 
 // ---------------------------------------------------------------- bf16 x fp32 matvec
 // y[r] = (resid ? resid[r] : 0) + sum_i W[r][i] * x'[i] for r < rows, where x' is the input
@@ -100,14 +122,15 @@ __device__ __forceinline__ void attn_select_layer(AttnDecodeArgs& a, int l) {
 }
 // split-K partials, with the q/k norm + RoPE + K/V append of position pos folded in
 hipError_t launch_attn_partial(const AttnDecodeArgs& a, hipStream_t s);
+bool attn_force_valu();  // Q35_ATTN_VALU=1: no matrix-core kernel
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s);
 // workspace floats for part_o + part_ml
 inline int64_t attn_partial_floats(int NQ, int NKV, int HD, int n_splits) {
     const int grp = NQ / NKV;
     return static_cast<int64_t>(NKV) * n_splits * grp * (HD + 2);
 }
-// Default splits per kv head: one 8-wave workgroup per CU over all kv heads, and no split
-// shorter than 64 positions at full context.
+// Default splits per kv head: one 8-wave workgroup per CU over all kv heads (of all layers
+// in the launch: NKV counts them), and no split shorter than 64 positions at full context.
 inline int attn_default_splits(int64_t max_ctx, int NKV, int n_cu) {
     const int64_t want = (max_ctx + 63) / 64;
     const int64_t cap = std::max<int64_t>(1, n_cu / std::max(1, NKV));

@@ -302,15 +302,16 @@ struct Launcher {
                 m->ev_class.push_back(cls);
             }
             m->ev_class[m->ev_used / 2] = cls;
-            if (hipEventRecord(m->ev[m->ev_used], s) != hipSuccess) {
-                st = q35::fail(Q35_ERR_HIP, "hipEventRecord failed");
-                return;
-            }
         }
+        // timed: the launches inside f() stamp the pair with their own start / end
+        q35k::LaunchTimer timer{timed ? m->ev[m->ev_used] : nullptr, timed ? m->ev[m->ev_used + 1] : nullptr, false};
+        if (timed) q35k::launch_timer() = &timer;
         const hipError_t e = f();
+        if (timed) q35k::launch_timer() = nullptr;
         if (e != hipSuccess) st = q35::fail(Q35_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
         if (timed) {
-            if (hipEventRecord(m->ev[m->ev_used + 1], s) != hipSuccess && st == Q35_OK)
+            if (!timer.started && st == Q35_OK &&  // nothing launched: an empty interval
+                (hipEventRecord(timer.start, s) != hipSuccess || hipEventRecord(timer.stop, s) != hipSuccess))
                 st = q35::fail(Q35_ERR_HIP, "hipEventRecord failed");
             m->ev_used += 2;
         }
