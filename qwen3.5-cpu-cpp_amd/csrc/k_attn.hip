@@ -618,7 +618,10 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         }
         vs[lane] = y;
     }
-    __syncthreads();
+    // LDS-only barrier: the K / V tiles in flight are not waited for here
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
     floatx4 O[16];
 #pragma unroll
@@ -627,7 +630,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
 
     // one tile of positions p0 .. p0 + 15 from K registers kr and the V registers; the next
     // tile's rows are requested as soon as these registers are consumed
-    auto tile = [&](KT (&kr)[16], int p0) {
+    auto tile = [&](KT (&kr)[16], int p0, auto more) {
         // four independent accumulation chains (dims 16c + 4g + i, one chain per i)
         floatx4 S4[4];
 #pragma unroll
@@ -644,7 +647,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
             if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
         const floatx4 S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
-        loadK(kr, p0 + TP);
+        if constexpr (decltype(more)::value) loadK(kr, p0 + TP);
         float s[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[r] = p0 + 4 * g + r < wl ? S[r] * sc : -INFINITY;
@@ -687,9 +690,11 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
                 O[4 * t + 2] = mfma16(p[v], vv.z, O[4 * t + 2]);
                 O[4 * t + 3] = mfma16(p[v], vv.w, O[4 * t + 3]);
             }
-        loadV(p0 + TP);
+        if constexpr (decltype(more)::value) loadV(p0 + TP);
     };
-    for (int p0 = w0; p0 < wl; p0 += TP) tile(kA, p0);
+    int p0 = w0;
+    for (; p0 + TP < wl; p0 += TP) tile(kA, p0, std::true_type{});
+    if (p0 < wl) tile(kA, p0, std::false_type{});  // the last tile requests nothing more
 
     if (has_new) {  // position pos: score of head h = lane & 7 over the 32 dims of chunk lane >> 3
         const int h = lane & 7, j = lane >> 3;
