@@ -58,6 +58,27 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return t;
 }
 
+// Workgroup barrier that orders LDS only: unlike __syncthreads it does not wait for the
+// wave's outstanding global loads (a weight stream in flight stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// block_sum with LDS-only barriers (for callers that exchange nothing else through memory).
+__device__ __forceinline__ double block_sum_lds(double v, double* red) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    v = wave_sum(v);
+    lds_barrier();
+    if (lane == 0) red[wave] = v;
+    lds_barrier();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
 // Counter-based normal draw (splitmix64 finaliser + Box-Muller in double); the same
 // formula as the host generator of synthetic checkpoints.
 __device__ __forceinline__ uint64_t mix64(uint64_t x) {

@@ -619,9 +619,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         vs[lane] = y;
     }
     // LDS-only barrier: the K / V tiles in flight are not waited for here
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    lds_barrier();
 
     floatx4 O[16];
 #pragma unroll
@@ -743,9 +741,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         ml_s[wave][n16][0] = m_run;
         ml_s[wave][n16][1] = l_run;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    lds_barrier();
     if (g < 2) {
         float sc4[4];
 #pragma unroll
@@ -764,9 +760,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
                     make_float4(O[4 * t][r] * sc4[r], O[4 * t + 1][r] * sc4[r], O[4 * t + 2][r] * sc4[r],
                                 O[4 * t + 3][r] * sc4[r]);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    lds_barrier();
     const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
 #pragma unroll
     for (int it = 0; it < GRP * kHD / (4 * kMW * 64); ++it) {

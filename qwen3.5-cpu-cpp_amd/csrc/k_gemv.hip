@@ -13,7 +13,8 @@
 // weight rows at a time with 16-byte loads (8 bf16 per lane, 1 KiB per wave per row and
 // chunk), issuing up to 4 chunks of loads before consuming them. The first row group's
 // loads are issued before the prologue, which they do not depend on, so the HBM latency
-// overlaps the input staging. bf16 is widened exactly (shift into the upper half of an
+// overlaps the input staging (its barriers order LDS only, so they do not wait for the
+// weights in flight). bf16 is widened exactly (shift into the upper half of an
 // fp32) and accumulated in fp32 FMA; the 64 lane partials are summed with a butterfly.
 #include <cstdlib>
 
@@ -68,9 +69,9 @@ __device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs) {
             const double v = a.x[i];
             ss += v * v;
         }
-        ss = block_sum(ss, red);
+        ss = block_sum_lds(ss, red);
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + a.eps);
-        __syncthreads();
+        lds_barrier();
         for (int i = tid; i < n; i += 256) xs[i] = xs[i] * inv * (1.0f + a.norm_w[i]);
     }
     if (PRO == kProGatedNorm) {
@@ -84,13 +85,13 @@ __device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs) {
             ss = wave_sum(ss);
             if (lane == 0) head_inv[h] = 1.0f / sqrtf(static_cast<float>(ss / hd) + a.eps);
         }
-        __syncthreads();
+        lds_barrier();
         for (int i = tid; i < n; i += 256) {
             const int h = i / hd;
             xs[i] = a.norm_w[i - h * hd] * (xs[i] * head_inv[h]) * silu_f(a.gate[i]);
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Number of 512-element chunks prefetched for the first row group: all KC of them when the
@@ -251,7 +252,7 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
             if ((tid + j * 256) * 4 < n)
                 ss += static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
                       static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
-        ss = block_sum(ss, red);
+        ss = block_sum_lds(ss, red);
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + a.eps);
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
@@ -281,7 +282,7 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
         const int i = (tid + j * 256) * 4;
         if (i < n) *reinterpret_cast<float4*>(xs + i) = xv[j];
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 template <int PRO, int EPI, int RPW, int NX, int KC>
