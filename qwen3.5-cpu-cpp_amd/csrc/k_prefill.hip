@@ -425,142 +425,181 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 }
 
 // ------------------------------------------------------------------ flash attention
+// 64 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
+// the cache. Per tile of 32 keys, two 16-key blocks: S^T = K Q^T on v_mfma_f32_16x16x4_f32
+// with the keys as rows, so a lane's score registers (keys 4g + v of its block, query row
+// l % 16) are directly the A operand of O += P V for k-step v; the head dims are permuted
+// consistently (dims 16c + 4g + i of a k-step, dims 64t + 4(l%16) + i of an output tile) so
+// every LDS operand read is one 16-byte vector. The next tile's K / V rows are loaded into
+// registers while the current one is computed.
 constexpr int kQT = 64;   // query rows per workgroup (16 per wave)
 constexpr int kKT = 32;   // key / value positions per tile
 constexpr int kLd = kHD + 4;
 
-__global__ __launch_bounds__(256) void flash_attn_kernel(AttnPrefillArgs a) {
-    const int qt = blockIdx.x, h = blockIdx.y;
+template <bool KVB>
+__global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
+    // Causal work grows with the query block. Workgroups are dispatched in linear order and
+    // two of them share a CU, ids L and L + half: the first half of the grid takes the
+    // query blocks in reverse (longest first), the second half in order, so the two
+    // workgroups of a CU carry complementary amounts of work.
+    const int nqt = gridDim.x, nlin = gridDim.x * gridDim.y;
+    const int L = blockIdx.x + blockIdx.y * nqt, half = nlin / 2;
+    const int h = L / nqt, xi = L - h * nqt;
+    const int qt = (L < half) ? nqt - 1 - xi : xi;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = a.NQ / a.NKV, kh = h / grp;
     const int t0 = qt * kQT;                  // first query row (block-relative)
-    __shared__ float KV[2][kKT][kLd];         // K tile, V tile (Q staging at the start)
-    __shared__ float Ps[4][16][kKT + 4];
-    const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
     const int r16 = lane & 15, g4 = lane >> 4;
+    __shared__ float Ks[kKT][kLd], Vs[kKT][kLd];
+    const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
-    // stage this wave's 16 query rows through LDS, then keep the A-operand layout in registers:
-    // q[s] = Q[row r16][4 s + g4]
-    float q[64];
+    // this lane's query row (the B operand column): Q[row r16][16c + 4 g4 + i]
+    const int qrow = t0 + wave * 16 + r16;  // block-relative
+    float4 qv[16];
     {
-        float* Qst = &KV[0][0][0];  // 64 rows x 256 would not fit kLd layout: stage per wave
-        const int rows = kQT;
-        for (int w = 0; w < 4; ++w) {
-            __syncthreads();
-            if (wave == w) {
-                for (int i = lane; i < 16 * kHD; i += 64) {
-                    const int rr = i / kHD, dd = i % kHD;
-                    const int t = t0 + w * 16 + rr;
-                    Qst[rr * kLd + dd] = t < a.T ? a.Qa[(static_cast<int64_t>(h) * a.T + t) * kHD + dd] : 0.0f;
-                }
-            }
-            __syncthreads();
-            if (wave == w) {
+        const float* src = a.Qa + (static_cast<int64_t>(h) * a.T + min(qrow, a.T - 1)) * kHD + 4 * g4;
 #pragma unroll
-                for (int s = 0; s < 64; ++s) q[s] = Qst[r16 * kLd + 4 * s + g4];
-            }
-        }
-        (void)rows;
+        for (int c = 0; c < 16; ++c) qv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
     }
+    const int qpos = a.pos0 + qrow;  // absolute position of this lane's query row
     floatx4 o[16];
 #pragma unroll
-    for (int b = 0; b < 16; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run[4], l_run[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m_run[i] = -INFINITY;
-        l_run[i] = 0.0f;
-    }
-    // this lane's query rows (C layout): 4 g4 + i, block-relative positions
-    const int qrow0 = t0 + wave * 16 + 4 * g4;
+    for (int t = 0; t < 16; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;  // of query row r16 (same in the 4 lane groups)
+
     const int kv_end = a.pos0 + min(a.T, t0 + kQT);  // exclusive, causal for the tile
     const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
-    const float* K = a.k_cache + hoff;
-    const float* V = a.v_cache + hoff;
-    const uint16_t* Kb = reinterpret_cast<const uint16_t*>(a.k_cache) + hoff;
-    const uint16_t* Vb = reinterpret_cast<const uint16_t*>(a.v_cache) + hoff;
-    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
-        __syncthreads();
-        for (int i = tid; i < kKT * (kHD / 4); i += 256) {
-            const int rr = i / (kHD / 4), c4 = (i % (kHD / 4)) * 4;
-            const int p = kv0 + rr;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (p < kv_end) {
-                const int64_t off = static_cast<int64_t>(p) * kHD + c4;
-                if (a.kv_bf16) {
-                    const uint2 kb = *reinterpret_cast<const uint2*>(Kb + off);
-                    const uint2 vb = *reinterpret_cast<const uint2*>(Vb + off);
-                    kv = make_float4(bf16_lo(kb.x), bf16_hi(kb.x), bf16_lo(kb.y), bf16_hi(kb.y));
-                    vv = make_float4(bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y));
-                } else {
-                    kv = *reinterpret_cast<const float4*>(K + off);
-                    vv = *reinterpret_cast<const float4*>(V + off);
-                }
+    // staging of one tile: thread tid holds rows tid / 64 + 4 j (j < 8), float4 column lane
+    constexpr int SR = kKT / 4;
+    float4 kst[SR], vst[SR];
+    auto load_tile = [&](int kv0) {
+        const bool live = kv0 < kv_end;
+#pragma unroll
+        for (int j = 0; j < SR; ++j) {
+            const int p = min(kv0 + wave + 4 * j, kv_end - 1);
+            const int64_t off = live ? static_cast<int64_t>(p) * kHD + 4 * lane : 0;  // past the end: one line
+            if constexpr (KVB) {
+                const uint2 kb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff + off);
+                const uint2 vb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff + off);
+                kst[j] = make_float4(bf16_lo(kb.x), bf16_hi(kb.x), bf16_lo(kb.y), bf16_hi(kb.y));
+                vst[j] = make_float4(bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y));
+            } else {
+                kst[j] = *reinterpret_cast<const float4*>(a.k_cache + hoff + off);
+                vst[j] = *reinterpret_cast<const float4*>(a.v_cache + hoff + off);
             }
-            *reinterpret_cast<float4*>(&KV[0][rr][c4]) = kv;
-            *reinterpret_cast<float4*>(&KV[1][rr][c4]) = vv;
         }
-        __syncthreads();
-        // S = Q K^T: two 16 x 16 blocks of key positions
-        floatx4 s[2];
+    };
+    auto store_tile = [&](int kv0) {
+#pragma unroll
+        for (int j = 0; j < SR; ++j) {
+            const int r = wave + 4 * j;
+            const bool ok = kv0 + r < kv_end;  // rows past the end are zero (masked anyway)
+            *reinterpret_cast<float4*>(&Ks[r][4 * lane]) = ok ? kst[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&Vs[r][4 * lane]) = ok ? vst[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load_tile(0);
+    store_tile(0);
+    lds_barrier();
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
+        load_tile(kv0 + kKT);  // in flight during this tile's products
+        float sv[2][4];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            s[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+            floatx4 S4[4];
 #pragma unroll
-            for (int st = 0; st < 64; ++st)
-                s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(q[st], KV[0][b * 16 + r16][4 * st + g4], s[b], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const float4 k = *reinterpret_cast<const float4*>(&Ks[b * 16 + r16][16 * c + 4 * g4]);
+                S4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.x, qv[c].x, S4[0], 0, 0, 0);
+                S4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.y, qv[c].y, S4[1], 0, 0, 0);
+                S4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.z, qv[c].z, S4[2], 0, 0, 0);
+                S4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.w, qv[c].w, S4[3], 0, 0, 0);
+            }
+            const floatx4 S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int key = kv0 + b * 16 + 4 * g4 + v;  // S^T[key][query r16]
+                sv[b][v] = key <= qpos && key < kv_end ? S[v] * sc : -INFINITY;
+            }
         }
-        // mask, scale, running softmax per row (rows 4 g4 + i, key column b * 16 + r16)
-        float f[4];
+        float tm = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qpos = a.pos0 + qrow0 + i;
-            float v0 = s[0][i] * sc, v1 = s[1][i] * sc;
-            if (kv0 + r16 > qpos) v0 = -INFINITY;
-            if (kv0 + 16 + r16 > qpos) v1 = -INFINITY;
-            float mx = fmaxf(v0, v1);
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float m_new = fmaxf(m_run[i], mx);
-            // rows past the prompt end (or fully masked so far) keep m = -inf: no update
-            const bool live = m_new != -INFINITY;
-            const float e0 = live ? expf(v0 - m_new) : 0.0f, e1 = live ? expf(v1 - m_new) : 0.0f;
-            float es = e0 + e1;
+            for (int v = 0; v < 4; ++v) tm = fmaxf(tm, sv[b][v]);
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        // the reference max moves only when a score exceeds it by more than 8; a row with no
+        // key yet keeps -inf and weight 0
+        const float m_new = tm > m_run + 8.0f ? tm : m_run;
+        const bool live = m_new != -INFINITY;
+        const float f = live ? expf(m_run - m_new) : 1.0f;
+        float p[2][4], ps = 0.0f;
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) es += __shfl_xor(es, off);
-            f[i] = live ? expf(m_run[i] - m_new) : 1.0f;
-            l_run[i] = l_run[i] * f[i] + es;
-            m_run[i] = live ? m_new : m_run[i];
-            Ps[wave][4 * g4 + i][r16] = e0;
-            Ps[wave][4 * g4 + i][16 + r16] = e1;
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                p[b][v] = live ? expf(sv[b][v] - m_new) : 0.0f;
+                ps += p[b][v];
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l_run = l_run * f + ps;
+        m_run = m_new;
+        if (__any(f != 1.0f)) {  // rescale output rows 4 g4 + r
+            float fr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) fr[r] = __shfl(f, 4 * g4 + r);
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                o[t][0] *= fr[0];
+                o[t][1] *= fr[1];
+                o[t][2] *= fr[2];
+                o[t][3] *= fr[3];
+            }
         }
+        // O[query row][64 t + 4 r16 + i] += P[query row][key] V[key][.]
 #pragma unroll
-        for (int b = 0; b < 16; ++b)
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[b][i] *= f[i];
-        // O += P V: A = P (row r16, key 4 st + g4), B = V (key 4 st + g4, dim 16 b + r16)
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int st = 0; st < kKT / 4; ++st) {
-            const float pa = Ps[wave][r16][4 * st + g4];
-#pragma unroll
-            for (int b = 0; b < 16; ++b)
-                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, KV[1][4 * st + g4][16 * b + r16], o[b], 0, 0, 0);
+                for (int t = 0; t < 4; ++t) {
+                    const float4 vv = *reinterpret_cast<const float4*>(&Vs[b * 16 + 4 * g4 + v][64 * t + 4 * r16]);
+                    o[4 * t + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.x, o[4 * t + 0], 0, 0, 0);
+                    o[4 * t + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.y, o[4 * t + 1], 0, 0, 0);
+                    o[4 * t + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.z, o[4 * t + 2], 0, 0, 0);
+                    o[4 * t + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.w, o[4 * t + 3], 0, 0, 0);
+                }
+        lds_barrier();  // every wave is done with this tile
+        if (kv0 + kKT < kv_end) {
+            store_tile(kv0 + kKT);
+            lds_barrier();
         }
     }
-    // epilogue: rows 4 g4 + i, dims 16 b + r16
+    // epilogue: lane holds rows 4 g4 + r, dims 64 t + 4 r16 + i
+    float lr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = qrow0 + i;
+    for (int r = 0; r < 4; ++r) lr[r] = __shfl(l_run, 4 * g4 + r);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int t = t0 + wave * 16 + 4 * g4 + r;
         if (t >= a.T) continue;
-        const float inv = 1.0f / l_run[i];
+        const float inv = 1.0f / lr[r];
         const float* gate = a.qkv + static_cast<int64_t>(t) * a.ld_qkv + static_cast<int64_t>(h) * 2 * kHD + kHD;
         float* out = a.out + static_cast<int64_t>(t) * (a.NQ * kHD) + static_cast<int64_t>(h) * kHD;
 #pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            const int dd = 16 * b + r16;
-            out[dd] = (o[b][i] * inv) * sigmoid_f(gate[dd]);
+        for (int tt = 0; tt < 4; ++tt) {
+            const int dd = 64 * tt + 4 * r16;
+            const float4 gv = *reinterpret_cast<const float4*>(gate + dd);
+            float4 y;
+            y.x = (o[4 * tt + 0][r] * inv) * sigmoid_f(gv.x);
+            y.y = (o[4 * tt + 1][r] * inv) * sigmoid_f(gv.y);
+            y.z = (o[4 * tt + 2][r] * inv) * sigmoid_f(gv.z);
+            y.w = (o[4 * tt + 3][r] * inv) * sigmoid_f(gv.w);
+            *reinterpret_cast<float4*>(out + dd) = y;
         }
     }
 }
@@ -633,7 +672,8 @@ int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
     klaunch(attn_prefill_prep_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
-    klaunch(flash_attn_kernel, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
+    if (a.kv_bf16) klaunch(flash_attn_kernel<true>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
+    else klaunch(flash_attn_kernel<false>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     return hipGetLastError();
 }
 
