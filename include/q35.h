@@ -183,7 +183,7 @@ q35_status q35_model_prefill(q35_model *m, const int32_t *ids, int32_t n, float 
  * q35_model_decode_greedy. */
 q35_status q35_model_extend(q35_model *m, const int32_t *ids, int32_t n, float *logits_host,
                             float *trace_host);
-/* Tokens per prefill block (0 = automatic: min(2048, max_context)). Larger blocks make
+/* Tokens per prefill block (0 = automatic: min(4096, max_context)). Larger blocks make
  * larger GEMMs and a larger prompt arena. */
 q35_status q35_model_set_prefill_block(q35_model *m, int32_t tokens);
 

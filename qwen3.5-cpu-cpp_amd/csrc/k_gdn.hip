@@ -56,6 +56,15 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     __shared__ float part[NRG][CS];
     __shared__ double red[4];
 
+    // The state slice and the per-head scalars do not depend on the conv: request them first,
+    // so their latency overlaps the conv loads instead of following the two barriers.
+    const int c = tid % CS, rg = tid / CS, r0 = rg * RPT;
+    float* Sc = S + split * CS + c;
+    float s[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) s[i] = Sc[(r0 + i) * kD];
+    const float A_v = A_log[vh], dt_v = dt_bias[vh], a_v = ain[vh], b_v = bin[vh];
+
     // causal conv (taps oldest first) + SiLU for the 128 q and 128 k channels of head kh
     {
         const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
@@ -102,16 +111,11 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
             k_s[tid - kD] = v * inv;
         }
     }
-    const float g = -expf(A_log[vh]) * softplus_f(ain[vh] + dt_bias[vh]);
-    const float alpha = expf(g), beta = sigmoid_f(bin[vh]);
+    const float g = -expf(A_v) * softplus_f(a_v + dt_v);
+    const float alpha = expf(g), beta = sigmoid_f(b_v);
     __syncthreads();
 
     // decay, S^T k, delta, rank-1 update, S^T q on the register-resident slice
-    const int c = tid % CS, rg = tid / CS, r0 = rg * RPT;
-    float* Sc = S + split * CS + c;
-    float s[RPT];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = Sc[(r0 + i) * kD];
     float km = 0.0f;
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {

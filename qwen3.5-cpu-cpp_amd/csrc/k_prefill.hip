@@ -438,14 +438,16 @@ constexpr int kLd = kHD + 4;
 
 template <bool KVB>
 __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
-    // Causal work grows with the query block. Workgroups are dispatched in linear order and
-    // two of them share a CU, ids L and L + half: the first half of the grid takes the
-    // query blocks in reverse (longest first), the second half in order, so the two
-    // workgroups of a CU carry complementary amounts of work.
+    // Causal work grows with the query block. Workgroups are dispatched in linear order, S
+    // of them resident at once, ids c and c + S/2 of a dispatch round on the same CU. Work
+    // items are ranked longest first; within each full round of S the second half takes
+    // the ranks in reverse, so the two workgroups of a CU carry complementary amounts of
+    // work, and later rounds (more workgroups than slots) bring the shorter items.
     const int nqt = gridDim.x, nlin = gridDim.x * gridDim.y;
-    const int L = blockIdx.x + blockIdx.y * nqt, half = nlin / 2;
-    const int h = L / nqt, xi = L - h * nqt;
-    const int qt = (L < half) ? nqt - 1 - xi : xi;
+    const int L = blockIdx.x + blockIdx.y * nqt, S = max(2, a.wg_slots & ~1);
+    const int round0 = L - L % S, r = L - round0;
+    const int rank = round0 + S <= nlin ? round0 + (r < S / 2 ? r : 3 * S / 2 - 1 - r) : L;
+    const int qt = nqt - 1 - rank / a.NQ, h = rank % a.NQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = a.NQ / a.NKV, kh = h / grp;
     const int t0 = qt * kQT;                  // first query row (block-relative)
@@ -670,7 +672,9 @@ hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
 
 int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_t>(NQ) * T * kHD + 64; }
 
-hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
+hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
+    AttnPrefillArgs a = in;
+    a.wg_slots = 2 * device_cu_count();  // two flash workgroups per CU (LDS and registers)
     klaunch(attn_prefill_prep_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
     if (a.kv_bf16) klaunch(flash_attn_kernel<true>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     else klaunch(flash_attn_kernel<false>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);

@@ -177,6 +177,7 @@ struct AttnPrefillArgs {
     int kv_bf16;
     float* Qa;                 // workspace [NQ][T][HD]
     float* out;                // [T][NQ * HD]
+    int wg_slots;              // flash workgroups resident at once (set by the launcher)
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);

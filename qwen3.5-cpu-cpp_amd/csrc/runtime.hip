@@ -794,7 +794,7 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb) {
 }
 
 int prefill_block_tokens(const q35_model* m) {
-    const int64_t want = m->pf_block > 0 ? m->pf_block : 2048;
+    const int64_t want = m->pf_block > 0 ? m->pf_block : 4096;
     return static_cast<int>(std::min<int64_t>(want, m->max_ctx));
 }
 
