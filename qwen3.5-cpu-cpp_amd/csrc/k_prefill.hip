@@ -226,26 +226,34 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
     float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
     for (int i = tid; i < kD * kSW; i += 256) Ss[i / kSW][i % kSW] = S[(i / kSW) * kD + col0 + i % kSW];
 
-    // staging map: float4 f = tid + 256 i (i < 8) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32)
+    // staging map: float4 f = tid + 256 i (i < 8) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32).
+    // Everything a chunk step reads from global memory (W, K, the cumulative decays and this
+    // lane's U entries) is requested one chunk ahead, so the sequential chain only waits on LDS.
     float4 rw[8], rk[8];
+    float rgam[8], rglast, ru[4];
     auto load_chunk = [&](int c) {
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
         const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
+        const float* gam = a.Gam + static_cast<int64_t>(vh) * a.Tp + row0;
+        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int f = tid + 256 * i;
             rw[i] = *reinterpret_cast<const float4*>(W + (f >> 5) * kD + (f & 31) * 4);
             rk[i] = *reinterpret_cast<const float4*>(K + (f >> 5) * kD + (f & 31) * 4);
+            rgam[i] = gam[f >> 5];
         }
+        rglast = gam[kC - 1];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * wave + 4 * lg + v) * kD + lr];
     };
-    auto store_chunk = [&](int c) {
-        const float* gam = a.Gam + static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC;
-        const float glast = gam[kC - 1];
+    auto store_chunk = [&]() {
+        const float glast = rglast;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int f = tid + 256 * i, r = f >> 5, c4 = (f & 31) * 4;
-            const float d = expf(glast - gam[r]);
+            const float d = expf(glast - rgam[i]);
             Wl[r][c4 + 0] = -rw[i].x;
             Wl[r][c4 + 1] = -rw[i].y;
             Wl[r][c4 + 2] = -rw[i].z;
@@ -259,21 +267,27 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
     load_chunk(0);
     for (int c = 0; c < nchunk; ++c) {
         __syncthreads();  // previous chunk done with Wl / Kl / Ss
-        store_chunk(c);
+        store_chunk();
+        const float glast = rglast;
+        floatx4 vn;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) vn[v] = ru[v];
         // chunk-start state for the output pass
         float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
         for (int i = tid; i < kD * kSW; i += 256) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
-        const float glast = a.Gam[static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC + kC - 1];
         __syncthreads();
         if (c + 1 < nchunk) load_chunk(c + 1);
 
         // v_new rows [16w, 16w + 16) = U - W S
         float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
-        floatx4 vn;
+        {  // four independent accumulation chains (k-steps interleaved), summed in a fixed order
+            floatx4 ch[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) vn[v] = U[(16 * wave + 4 * lg + v) * kD + lr];
-#pragma unroll 8
-        for (int k = 0; k < kD; k += 4) vn = mfma4(Wl[16 * wave + lr][k + lg], Ss[k + lg][lr], vn);
+            for (int q = 0; q < 4; ++q) ch[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < kD; k += 4) ch[(k >> 2) & 3] = mfma4(Wl[16 * wave + lr][k + lg], Ss[k + lg][lr], ch[(k >> 2) & 3]);
+            vn = vn + ((ch[0] + ch[1]) + (ch[2] + ch[3]));
+        }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             U[(16 * wave + 4 * lg + v) * kD + lr] = vn[v];
@@ -292,8 +306,11 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
             floatx4 sn;
 #pragma unroll
             for (int v = 0; v < 4; ++v) sn[v] = srow[v * kSW] * dl;
-#pragma unroll 4
-            for (int t = 0; t < kC; t += 4) sn = mfma4(Kl[t + lg][32 * wave + 16 * rb + lr], VN[t + lg][lr], sn);
+            floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int t = 0; t < kC; t += 4)
+                ch[(t >> 2) & 1] = mfma4(Kl[t + lg][32 * wave + 16 * rb + lr], VN[t + lg][lr], ch[(t >> 2) & 1]);
+            sn = sn + (ch[0] + ch[1]);
 #pragma unroll
             for (int v = 0; v < 4; ++v) srow[v * kSW] = sn[v];
         }
