@@ -58,6 +58,32 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return t;
 }
 
+// cos / sin (from the double-precision angle pos * theta^(-2i/rot), as the reference's
+// apply_rope) of the rotation indices i = (4 lane) mod rot/2 .. + 3 that a lane holding dims
+// 4 lane .. 4 lane + 3 of a head needs. Wave-wide (uses lane shuffles): call from all lanes.
+__device__ __forceinline__ void rope_cs4(double theta, int rot, int pos, int lane, float4& c4, float4& s4) {
+    const int half = rot / 2;
+    const int ci = (lane * 4) % (half > 4 ? half : 4);
+    auto angle = [&](int i, float& c, float& s) {
+        const double inv_freq = pow(theta, -static_cast<double>(2 * i) / rot);
+        const double ang = static_cast<double>(pos) * inv_freq;
+        c = static_cast<float>(cos(ang));
+        s = static_cast<float>(sin(ang));
+    };
+    if (half <= 64) {  // one angle per lane, then shared
+        float cv = 1.0f, sv = 0.0f;
+        if (lane < half) angle(lane, cv, sv);
+        c4 = make_float4(__shfl(cv, ci), __shfl(cv, ci + 1), __shfl(cv, ci + 2), __shfl(cv, ci + 3));
+        s4 = make_float4(__shfl(sv, ci), __shfl(sv, ci + 1), __shfl(sv, ci + 2), __shfl(sv, ci + 3));
+    } else {  // wider than 128 rotated dims: each lane its own four
+        float cv[4], sv[4];
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) angle(ci + i, cv[i], sv[i]);
+        c4 = make_float4(cv[0], cv[1], cv[2], cv[3]);
+        s4 = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    }
+}
+
 // Workgroup barrier that orders LDS only: unlike __syncthreads it does not wait for the
 // wave's outstanding global loads (a weight stream in flight stays in flight).
 __device__ __forceinline__ void lds_barrier() {

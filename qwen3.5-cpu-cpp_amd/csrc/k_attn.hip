@@ -571,18 +571,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     loadV(w0);
 
     // ---- Q operand and the appended rows
-    if (!a.rope_cs) {  // double-precision angles, as the reference: one per lane, then shared
-        float cv = 1.0f, sv = 0.0f;
-        if (lane < half) {
-            const double inv_freq = pow(a.theta, -static_cast<double>(2 * lane) / ROT);
-            const double ang = static_cast<double>(pos) * inv_freq;
-            cv = static_cast<float>(cos(ang));
-            sv = static_cast<float>(sin(ang));
-        }
-        const int c0 = min(ci, 60);
-        cs4 = make_float4(__shfl(cv, c0), __shfl(cv, c0 + 1), __shfl(cv, c0 + 2), __shfl(cv, c0 + 3));
-        sn4 = make_float4(__shfl(sv, c0), __shfl(sv, c0 + 1), __shfl(sv, c0 + 2), __shfl(sv, c0 + 3));
-    }
+    if (!a.rope_cs) rope_cs4(a.theta, ROT, pos, lane, cs4, sn4);  // double-precision angles
     for (int e = tid; e < 16 * 32; e += kMW * 64)  // columns 8-15: zero heads
         qs[e >> 5][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll

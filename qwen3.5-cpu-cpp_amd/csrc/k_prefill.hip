@@ -41,46 +41,72 @@ constexpr int kHD = 256;  // attention head dim
 // ------------------------------------------------------------------ GDN prep
 // grid (T, KH), 256 threads: conv + SiLU for the k-head's q, k and its rep v-heads' v
 // channels, l2norm of q and k, beta / g of the rep v-heads.
+// kPT consecutive tokens per workgroup: each thread owns one channel, reads the kPT + 3 raw
+// inputs of its window once and its four taps once, and serves all kPT tokens.
+constexpr int kPT = 8;
+
 __global__ __launch_bounds__(256) void gdn_prep_kernel(GdnPrefillArgs a) {
-    const int t = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int t0 = blockIdx.x * kPT, kh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int rep = a.VH / a.KH;
     const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
-    const int pos = a.pos0 + t;
-    __shared__ double red[4];
+    const int nt = min(kPT, a.T - t0);
+    __shared__ double red[4][kPT];
     auto xin = [&](int s, int ch) -> float {  // raw input of token s (relative) for channel ch
-        if (s >= 0) return a.qkv[static_cast<int64_t>(s) * a.ld_qkv + ch];
+        if (s >= 0) return a.qkv[static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch];
         return a.conv_ring[static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch];
     };
-    auto conv = [&](int ch) -> float {
-        const float* w4 = a.conv_w + static_cast<int64_t>(ch) * 4;
-        float acc = 0.0f;
-        acc += w4[0] * xin(t - 3, ch);
-        acc += w4[1] * xin(t - 2, ch);
-        acc += w4[2] * xin(t - 1, ch);
-        acc += w4[3] * xin(t, ch);
-        return silu_f(acc);
+    // causal conv + SiLU of channel ch for the kPT tokens (the reference's 4-tap window,
+    // src/qwen_forward.cpp:109-118)
+    auto conv = [&](int ch, float (&y)[kPT]) {
+        const float4 w4 = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(ch) * 4);
+        float x[kPT + 3];
+#pragma unroll
+        for (int j = 0; j < kPT + 3; ++j) x[j] = xin(t0 - 3 + j, ch);
+#pragma unroll
+        for (int j = 0; j < kPT; ++j) {
+            float acc = 0.0f;
+            acc += w4.x * x[j];
+            acc += w4.y * x[j + 1];
+            acc += w4.z * x[j + 2];
+            acc += w4.w * x[j + 3];
+            y[j] = silu_f(acc);
+        }
     };
-    (void)pos;
-    // q (threads 0..127) and k (128..255)
+    // q (threads 0..127) and k (128..255): l2norm per token, sums of squares in double
     const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
-    const float v = conv(ch);
-    double ss = static_cast<double>(v) * v;
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    float y[kPT];
+    conv(ch, y);
+#pragma unroll
+    for (int j = 0; j < kPT; ++j) {
+        double ss = static_cast<double>(y[j]) * y[j];
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave][j] = ss;
+    }
     __syncthreads();
-    const double sq = red[0] + red[1], sk = red[2] + red[3];
-    if (tid < kD) {
-        const float inv = 1.0f / sqrtf(static_cast<float>(sq) + 1e-6f);
-        a.Qg[(static_cast<int64_t>(kh) * a.Tp + t) * kD + tid] = (v * inv) * (1.0f / sqrtf(static_cast<float>(kD)));
-    } else {
-        const float inv = 1.0f / sqrtf(static_cast<float>(sk) + 1e-6f);
-        a.Kg[(static_cast<int64_t>(kh) * a.Tp + t) * kD + (tid - kD)] = v * inv;
+#pragma unroll
+    for (int j = 0; j < kPT; ++j) {
+        if (j >= nt) break;
+        const int64_t row = static_cast<int64_t>(kh) * a.Tp + t0 + j;
+        if (tid < kD) {
+            const float inv = 1.0f / sqrtf(static_cast<float>(red[0][j] + red[1][j]) + 1e-6f);
+            a.Qg[row * kD + tid] = (y[j] * inv) * (1.0f / sqrtf(static_cast<float>(kD)));
+        } else {
+            const float inv = 1.0f / sqrtf(static_cast<float>(red[2][j] + red[3][j]) + 1e-6f);
+            a.Kg[row * kD + (tid - kD)] = y[j] * inv;
+        }
     }
     // v channels and beta / g of the v-heads served by this k-head
     for (int r = 0; r < rep; ++r) {
         const int vh = kh * rep + r;
-        if (tid < kD) a.Vg[(static_cast<int64_t>(vh) * a.Tp + t) * kD + tid] = conv(2 * KD + vh * kD + tid);
-        if (tid == 0) {
+        if (tid < kD) {
+            float yv[kPT];
+            conv(2 * KD + vh * kD + tid, yv);
+#pragma unroll
+            for (int j = 0; j < kPT; ++j)
+                if (j < nt) a.Vg[(static_cast<int64_t>(vh) * a.Tp + t0 + j) * kD + tid] = yv[j];
+        } else if (tid - kD < nt) {
+            const int t = t0 + tid - kD;
             const float bb = a.b[static_cast<int64_t>(t) * a.ld_ba + vh];
             const float aa = a.a[static_cast<int64_t>(t) * a.ld_ba + vh];
             a.Bg[static_cast<int64_t>(vh) * a.Tp + t] = sigmoid_f(bb);
@@ -394,8 +420,8 @@ __global__ __launch_bounds__(256) void gdn_out_kernel(GdnPrefillArgs a) {
 }
 
 // ------------------------------------------------------------------ attention prep
-// grid (T, NQ + NKV), 256 threads (one per dim)
-__global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs a) {
+// Any even rotary width: grid (T, NQ + NKV), one thread per dim.
+__global__ __launch_bounds__(256) void attn_prefill_prep_any_kernel(AttnPrefillArgs a) {
     const int t = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
     const int pos = a.pos0 + t;
     __shared__ float buf[kHD];
@@ -439,6 +465,89 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
     if (is_q) a.Qa[(static_cast<int64_t>(r) * a.T + t) * kHD + d] = y;
     else if (a.kv_bf16) reinterpret_cast<uint16_t*>(a.k_cache)[coff + d] = f32_to_bf16(y);
     else a.k_cache[coff + d] = y;
+}
+
+// One workgroup per token, all of its rows: the NQ query rows (rmsnorm (1 + q_norm) + RoPE
+// -> Qa), the NKV key rows (k_norm + RoPE -> cache) and the NKV value rows (-> cache). A row
+// is 4 dims per lane of one wave (sum of squares in double); the RoPE partner dims d +- ROT/2
+// come from lane +- ROT/8; cos / sin from the table or from the double-precision angle.
+__global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs a) {
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = a.pos0 + t;
+    const int half = a.ROT / 2, hq = a.ROT / 8;
+    const float* row = a.qkv + static_cast<int64_t>(t) * a.ld_qkv;
+    // cos / sin of the 4 dims of this lane (dims d mod half, lanes < ROT / 4)
+    float4 cs4 = make_float4(1.f, 1.f, 1.f, 1.f), sn4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int ci = (lane * 4) % max(half, 4);
+    if (a.rope_cs) {
+        const float* tb = a.rope_cs + static_cast<int64_t>(pos) * a.ROT;
+        const int c0 = min(ci, max(half - 4, 0));
+        cs4 = *reinterpret_cast<const float4*>(tb + c0);
+        sn4 = *reinterpret_cast<const float4*>(tb + half + c0);
+    } else {
+        rope_cs4(a.theta, a.ROT, pos, lane, cs4, sn4);  // double-precision angles
+    }
+    const int nrow = a.NQ + 2 * a.NKV;
+    for (int r = wave; r < nrow; r += 4) {  // uniform per wave
+        if (r >= a.NQ + a.NKV) {  // value row: copied to the cache
+            const int kh = r - a.NQ - a.NKV;
+            const float4 v = *reinterpret_cast<const float4*>(row + static_cast<int64_t>(a.NQ) * 2 * kHD +
+                                                              static_cast<int64_t>(a.NKV + kh) * kHD + lane * 4);
+            const int64_t off = (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + lane * 4;
+            if (a.kv_bf16) {
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.v_cache) + off) =
+                    make_uint2(f32_to_bf16(v.x) | (static_cast<uint32_t>(f32_to_bf16(v.y)) << 16),
+                               f32_to_bf16(v.z) | (static_cast<uint32_t>(f32_to_bf16(v.w)) << 16));
+            } else {
+                *reinterpret_cast<float4*>(a.v_cache + off) = v;
+            }
+            continue;
+        }
+        const bool is_q = r < a.NQ;
+        const int kh = r - a.NQ;
+        const float* src = is_q ? row + static_cast<int64_t>(r) * 2 * kHD
+                                : row + static_cast<int64_t>(a.NQ) * 2 * kHD + static_cast<int64_t>(kh) * kHD;
+        const float4 x = *reinterpret_cast<const float4*>(src + lane * 4);
+        const float4 w = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + lane * 4);
+        double ss = static_cast<double>(x.x) * x.x + static_cast<double>(x.y) * x.y + static_cast<double>(x.z) * x.z +
+                    static_cast<double>(x.w) * x.w;
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(static_cast<float>(ss / kHD) + a.eps);
+        float4 y;
+        y.x = x.x * inv * (1.0f + w.x);
+        y.y = x.y * inv * (1.0f + w.y);
+        y.z = x.z * inv * (1.0f + w.z);
+        y.w = x.w * inv * (1.0f + w.w);
+        const int srcl = lane < hq ? lane + hq : lane - hq;
+        float4 o;
+        o.x = __shfl(y.x, srcl);
+        o.y = __shfl(y.y, srcl);
+        o.z = __shfl(y.z, srcl);
+        o.w = __shfl(y.w, srcl);
+        if (lane < hq) {
+            y.x = y.x * cs4.x - o.x * sn4.x;
+            y.y = y.y * cs4.y - o.y * sn4.y;
+            y.z = y.z * cs4.z - o.z * sn4.z;
+            y.w = y.w * cs4.w - o.w * sn4.w;
+        } else if (lane < 2 * hq) {
+            y.x = y.x * cs4.x + o.x * sn4.x;
+            y.y = y.y * cs4.y + o.y * sn4.y;
+            y.z = y.z * cs4.z + o.z * sn4.z;
+            y.w = y.w * cs4.w + o.w * sn4.w;
+        }
+        if (is_q) {
+            *reinterpret_cast<float4*>(a.Qa + (static_cast<int64_t>(r) * a.T + t) * kHD + lane * 4) = y;
+        } else {
+            const int64_t off = (static_cast<int64_t>(kh) * a.max_ctx + pos) * kHD + lane * 4;
+            if (a.kv_bf16) {
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.k_cache) + off) =
+                    make_uint2(f32_to_bf16(y.x) | (static_cast<uint32_t>(f32_to_bf16(y.y)) << 16),
+                               f32_to_bf16(y.z) | (static_cast<uint32_t>(f32_to_bf16(y.w)) << 16));
+            } else {
+                *reinterpret_cast<float4*>(a.k_cache + off) = y;
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------------ flash attention
@@ -678,7 +787,7 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
 }
 
 hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
-    klaunch(gdn_prep_kernel, dim3(a.T, a.KH), 256, 0, s, a);
+    klaunch(gdn_prep_kernel, dim3((a.T + kPT - 1) / kPT, a.KH), 256, 0, s, a);
     if (a.Tp > a.T) klaunch(gdn_pad_kernel, blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s, a);
     klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
     klaunch(gdn_chunk_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
@@ -692,7 +801,8 @@ int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_
 hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
     AttnPrefillArgs a = in;
     a.wg_slots = 2 * device_cu_count();  // two flash workgroups per CU (LDS and registers)
-    klaunch(attn_prefill_prep_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
+    if (a.ROT % 8 == 0) klaunch(attn_prefill_prep_kernel, a.T, 256, 0, s, a);
+    else klaunch(attn_prefill_prep_any_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
     if (a.kv_bf16) klaunch(flash_attn_kernel<true>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     else klaunch(flash_attn_kernel<false>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     return hipGetLastError();

@@ -886,6 +886,7 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.k_cache = kv_ptr(m, ly.idx, 0, 0);
             a.v_cache = kv_ptr(m, ly.idx, 1, 0);
             a.kv_bf16 = m->kv_elem == 2;
+            a.rope_cs = m->rope_cs;
             a.Qa = ws;
             a.out = mix;
             Lr.run(Q35_KT_ATTN_PREFILL, [&] { return q35k::launch_attn_prefill(a, s); });

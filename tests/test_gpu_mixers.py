@@ -108,9 +108,10 @@ def attn_dims(nq, nkv):
     return pyq35.default_dims(attn_q_heads=nq, attn_kv_heads=nkv)
 
 
-def run_attn(hip, nq, nkv, pos, max_ctx, n_splits, seed):
+def run_attn(hip, nq, nkv, pos, max_ctx, n_splits, seed, rot=64):
     rng = np.random.default_rng(seed)
     d = attn_dims(nq, nkv)
+    d.partial_rotary_factor = rot / 256.0
     HD = 256
     qg = rng.standard_normal(2 * nq * HD).astype(np.float32)
     kn = rng.standard_normal(nkv * HD).astype(np.float32)
@@ -123,7 +124,7 @@ def run_attn(hip, nq, nkv, pos, max_ctx, n_splits, seed):
     Vd[:, :pos] = rng.standard_normal((nkv, pos, HD))
     B = Bufs(hip)
     try:
-        args = pyq35.AttnDecodeArgs(q_heads=nq, kv_heads=nkv, head_dim=HD, rotary_dim=64, pos=pos,
+        args = pyq35.AttnDecodeArgs(q_heads=nq, kv_heads=nkv, head_dim=HD, rotary_dim=rot, pos=pos,
                                     n_splits=n_splits, max_context=max_ctx, rope_theta=d.rope_theta,
                                     eps=d.rms_norm_eps)
         ws = pyq35.lib.q35_attn_decode_workspace_bytes(args)
@@ -159,6 +160,15 @@ def test_attn_decode_small(hip, nq, nkv, pos):
 def test_attn_decode_2b_shape(hip, pos):
     """16 q heads / 2 kv heads (GQA 8:1), head_dim 256, partial RoPE 64, at 2k/8k/32k."""
     out, ref, krow, kref, vrow, vref = run_attn(hip, 16, 2, pos, pos + 1, 0, seed=pos)
+    assert rel_l2(out, ref) < REL_L2
+    np.testing.assert_allclose(krow, kref, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("rot", [0, 18, 32, 96, 256])
+def test_attn_decode_rotary_widths(hip, rot):
+    """GQA 8 with rotary widths that are multiples of 32 takes the matrix-core kernel, others
+    (18) the vector-ALU kernel; 0 and the full head width are the edges."""
+    out, ref, krow, kref, *_ = run_attn(hip, 16, 2, 500, 600, 0, seed=rot + 7, rot=rot)
     assert rel_l2(out, ref) < REL_L2
     np.testing.assert_allclose(krow, kref, rtol=2e-6, atol=2e-6)
 

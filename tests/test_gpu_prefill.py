@@ -144,9 +144,10 @@ def test_gdn_prefill_512_tokens_state(hip):
 
 
 # ----------------------------------------------------------------------------- attention
-def run_attn_prefill(hip, nq, nkv, T, pos0, seed):
+def run_attn_prefill(hip, nq, nkv, T, pos0, seed, rot=64):
     rng = np.random.default_rng(seed)
     d = pyq35.default_dims(attn_q_heads=nq, attn_kv_heads=nkv)
+    d.partial_rotary_factor = rot / 256.0
     HD = 256
     maxc = pos0 + T + 5
     ld = 2 * nq * HD + 2 * nkv * HD
@@ -160,7 +161,7 @@ def run_attn_prefill(hip, nq, nkv, T, pos0, seed):
     B = Bufs(hip)
     try:
         args = pyq35.AttnPrefillArgs(n_tokens=T, pos0=pos0, q_heads=nq, kv_heads=nkv, head_dim=HD,
-                                     rotary_dim=64, max_context=maxc, rope_theta=d.rope_theta,
+                                     rotary_dim=rot, max_context=maxc, rope_theta=d.rope_theta,
                                      eps=d.rms_norm_eps, ld_qkv=ld)
         ws = pyq35.lib.q35_attn_prefill_workspace_bytes(args)
         args.qkv = B.up("rows", rows)
@@ -199,6 +200,17 @@ def test_attn_prefill_vs_oracle(hip, nq, nkv, T, pos0):
     for kh in range(nkv):
         np.testing.assert_allclose(Kdev[kh, :pos0 + T], Ko[:pos0 + T, kh], rtol=2e-6, atol=2e-6)
         np.testing.assert_array_equal(Vdev[kh, :pos0 + T], Vo[:pos0 + T, kh])
+
+
+@pytest.mark.parametrize("rot", [0, 18, 32, 256])
+def test_attn_prefill_rotary_widths(hip, rot):
+    """Rotary widths other than the model's 64: multiples of 8 take the per-token prep
+    kernel, others (18) the per-dim one; 0 and the full head width are the edges."""
+    out, ref, Kdev, Ko, Vdev, Vo = run_attn_prefill(hip, 8, 2, 70, 30, seed=rot + 1, rot=rot)
+    errs = [rel_l2(out[t], ref[t]) for t in range(70)]
+    assert max(errs) < REL_L2, f"rot {rot}: {max(errs)}"
+    for kh in range(2):
+        np.testing.assert_allclose(Kdev[kh, :100], Ko[:100, kh], rtol=2e-6, atol=2e-6)
 
 
 # ----------------------------------------------------------------------------- model level
