@@ -775,51 +775,72 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     }
 }
 
-// grid (NQ, HD / 64), 256 threads: wave w merges splits w, w+4, ... for 64 dims (one per lane)
+// grid (NQ, HD / 64), 256 threads, 64 dims per workgroup (one per lane). Every load is
+// requested up front -- the (m, l) of split t on thread t and the o rows of splits
+// 32 w .. 32 w + 31 on wave w -- so the merge waits for one memory round trip; the maximum
+// and the split weights exp(m_s - M) go through LDS. Past 128 (o rows) or 256 ((m, l)
+// pairs) active splits further passes follow.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
     attn_select_layer(a, blockIdx.z);
-    const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kRW = 32;  // o rows per wave per pass
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int d = blockIdx.y * 64 + lane;
     const int grp = a.NQ / a.NKV, kh = h / grp, g = h - kh * grp;
     const int n = read_pos(a) + 1;
     const int per = split_len(n, a.n_splits);
     const int nact = (n + per - 1) / per;
-    const int64_t base = static_cast<int64_t>(kh) * a.n_splits * grp + g;
-    __shared__ float o_s[4][64], l_s[4];
-    float mx = -INFINITY;
-    for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, a.part_ml[(base + static_cast<int64_t>(s) * grp) * 2]);
-    const float M = wave_max(mx);
+    const int64_t base = static_cast<int64_t>(kh) * a.n_splits * grp + g;  // split s: row base + s grp
+    const float* po = a.part_o + base * kHD + d;
+    const int64_t so = static_cast<int64_t>(grp) * kHD;
+    __shared__ float w_s[256], red[4], o_s[4][64];
+
+    const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + d];
+    float ov[kRW];
+#pragma unroll
+    for (int u = 0; u < kRW; ++u) ov[u] = po[min(wave * kRW + u, nact - 1) * so];
+    const float* ml = a.part_ml + (base + static_cast<int64_t>(min(tid, nact - 1)) * grp) * 2;
+    float m_t = ml[0];
+    const float l_t = ml[1];
+    if (tid >= nact) m_t = -INFINITY;
+    float mx = m_t;
+    for (int s = tid + 256; s < nact; s += 256) mx = fmaxf(mx, a.part_ml[(base + static_cast<int64_t>(s) * grp) * 2]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f, o = 0.0f;
-    int s = wave;
-    for (; s + 12 < nact; s += 16) {
-        float mv[4], lv[4], ov[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t i = base + static_cast<int64_t>(s + 4 * u) * grp;
-            mv[u] = a.part_ml[i * 2];
-            lv[u] = a.part_ml[i * 2 + 1];
-            ov[u] = a.part_o[i * kHD + d];
+    for (int c0 = 0; c0 < nact; c0 += 256) {
+        float w = 0.0f;
+        if (c0 == 0) {
+            if (tid < nact) {
+                w = expf(m_t - M);
+                L = l_t * w;
+            }
+        } else if (c0 + tid < nact) {
+            const int64_t i = base + static_cast<int64_t>(c0 + tid) * grp;
+            w = expf(a.part_ml[i * 2] - M);
+            L = fmaf(a.part_ml[i * 2 + 1], w, L);
         }
+        __syncthreads();  // the previous pass's weights (and the maxima) are consumed
+        w_s[tid] = w;
+        __syncthreads();
+        for (int c1 = 0; c1 < 256 && c0 + c1 < nact; c1 += 4 * kRW) {
+            if (c0 + c1 > 0) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float w = expf(mv[u] - M);
-            L = fmaf(lv[u], w, L);
-            o = fmaf(ov[u], w, o);
+                for (int u = 0; u < kRW; ++u) ov[u] = po[min(c0 + c1 + wave * kRW + u, nact - 1) * so];
+            }
+            // rows past the last active split carry weight 0
+#pragma unroll
+            for (int u = 0; u < kRW; ++u) o = fmaf(ov[u], w_s[c1 + wave * kRW + u], o);
         }
-    }
-    for (; s < nact; s += 4) {
-        const int64_t i = base + static_cast<int64_t>(s) * grp;
-        const float w = expf(a.part_ml[i * 2] - M);
-        L = fmaf(a.part_ml[i * 2 + 1], w, L);
-        o = fmaf(a.part_o[i * kHD + d], w, o);
     }
     o_s[wave][lane] = o;
-    if (lane == 0) l_s[wave] = L;
+    L = wave_sum(L);
+    if (lane == 0) red[wave] = L;
     __syncthreads();
     if (wave == 0) {
-        const float Lt = (l_s[0] + l_s[1]) + (l_s[2] + l_s[3]);
+        const float Lt = (red[0] + red[1]) + (red[2] + red[3]);
         const float ot = (o_s[0][lane] + o_s[1][lane]) + (o_s[2][lane] + o_s[3][lane]);
-        const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + d];
         a.out[static_cast<int64_t>(h) * kHD + d] = (ot / Lt) * sigmoid_f(gate);
     }
 }

@@ -43,7 +43,8 @@ __device__ __forceinline__ void split3(float x, uint32_t& h, uint32_t& m, uint32
     l = __float_as_uint(r2) >> 16;
 }
 
-template <bool RESID>
+// EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs
+template <int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) uint16_t Xs[3][kBM][kLd];
     __shared__ __align__(16) uint16_t Ws[kBN][kLd];
@@ -126,6 +127,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             }
         }
     }
+    if constexpr (EPI == 2) {
+        // the pair (gate, up) of one output sits in adjacent lanes (even, odd column)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float up = __shfl_xor(acc[i][j][v], 1);
+                    const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                    if (!(lane & 1) && col + 1 < a.N && row < a.M)
+                        a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = silu_f(acc[i][j][v]) * up;
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -137,7 +155,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                 const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (row < a.M) {
                     float* y = a.Y + static_cast<int64_t>(row) * a.ldy + col;
-                    *y = RESID ? a.R[static_cast<int64_t>(row) * a.ldr + col] + acc[i][j][v] : acc[i][j][v];
+                    *y = EPI == 1 ? a.R[static_cast<int64_t>(row) * a.ldr + col] + acc[i][j][v] : acc[i][j][v];
                 }
             }
         }
@@ -147,8 +165,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
-    if (a.R) klaunch(gemm_kernel<true>, grid, 256, 0, s, a);
-    else klaunch(gemm_kernel<false>, grid, 256, 0, s, a);
+    if (a.swiglu) klaunch(gemm_kernel<2>, grid, 256, 0, s, a);
+    else if (a.R) klaunch(gemm_kernel<1>, grid, 256, 0, s, a);
+    else klaunch(gemm_kernel<0>, grid, 256, 0, s, a);
     return hipGetLastError();
 }
 

@@ -733,15 +733,6 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
 }
 
 // ------------------------------------------------------------------ small prefill helpers
-__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* gu, float* h, int T, int I) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < static_cast<int64_t>(T) * I;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t t = i / I, c = i % I;  // gate / up columns interleaved
-        const float g = gu[t * 2 * I + 2 * c], u = gu[t * 2 * I + 2 * c + 1];
-        h[i] = silu_f(g) * u;
-    }
-}
-
 __global__ __launch_bounds__(256) void embed_rows_kernel(const uint16_t* embed, const int* ids, float* hidden, int T,
                                                          int H) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < static_cast<int64_t>(T) * H;
@@ -805,11 +796,6 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
     else klaunch(attn_prefill_prep_any_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
     if (a.kv_bf16) klaunch(flash_attn_kernel<true>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
     else klaunch(flash_attn_kernel<false>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s) {
-    klaunch(swiglu_rows_kernel, blocks_for(static_cast<int64_t>(T) * I), 256, 0, s, gu, h, T, I);
     return hipGetLastError();
 }
 

@@ -65,6 +65,9 @@ struct GemmArgs {
     float* Y;
     int M, N, K;
     int64_t ldx, ldr, ldy;
+    // W rows (2i, 2i + 1) are (gate_i, up_i), the interleaved gate/up projection: store
+    // Y[m][i] = silu(gate_i) * up_i instead (Y is M x N/2, row stride ldy); R unused
+    int swiglu = 0;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 
@@ -183,7 +186,6 @@ struct AttnPrefillArgs {
 int64_t attn_prefill_workspace_floats(int NQ, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
 // h[t][i] = silu(gu[t][2i]) * gu[t][2i + 1] (gate / up columns interleaved)
-hipError_t launch_swiglu_rows(const float* gu, float* h, int T, int I, hipStream_t s);
 // hidden[t][:] = bf16 embed[ids[t]][:]
 hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s);
 

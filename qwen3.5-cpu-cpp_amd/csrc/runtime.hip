@@ -758,7 +758,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
 // Layout of the prompt arena for blocks of `tb` tokens (offsets in floats, 256-B aligned).
 struct PrefillPlan {
     int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
-    int64_t hidden = 0, xn = 0, proj = 0, mix = 0, gu = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
+    int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
 };
 
 int64_t proj_width(const q35_dims& d) {
@@ -783,7 +783,6 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb) {
     p.xn = take(T * H);
     p.proj = take(T * proj_width(d));
     p.mix = take(T * std::max(VD, QD));
-    p.gu = take(T * 2 * I);
     p.hb = take(T * I);
     p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
                          q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
@@ -819,8 +818,9 @@ q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
 }
 
 hipError_t gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, int K, const float* R, float* Y,
-                int64_t ldy, hipStream_t s) {
-    const q35k::GemmArgs g{X, W, R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
+                int64_t ldy, hipStream_t s, bool swiglu = false) {
+    q35k::GemmArgs g{X, W, R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
+    g.swiglu = swiglu;
     return q35k::launch_gemm(g, s);
 }
 
@@ -836,7 +836,7 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
     const float eps = d.rms_norm_eps;
     float* F = reinterpret_cast<float*>(m->pf_arena);
     float *hidden = F + p.hidden, *xn = F + p.xn, *proj = F + p.proj, *mix = F + p.mix;
-    float *gu = F + p.gu, *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
+    float *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
     const int* ids = reinterpret_cast<const int*>(F + p.ids);
     Launcher Lr{m, s, m->timing_on};
 
@@ -893,8 +893,8 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             Lr.run(Q35_KT_GEMM, [&] { return gemm(mix, NQ * HD, ly.w_out, T, H, NQ * HD, hidden, hidden, H, s); });
         }
         Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s); });
-        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, gu, 2 * I, s); });
-        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_swiglu_rows(gu, hb, T, I, s); });
+        // gate/up projection with silu(gate) * up in its epilogue: hb = T x I
+        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, hb, I, s, true); });
         Lr.run(Q35_KT_GEMM, [&] { return gemm(hb, I, ly.w_down, T, H, I, hidden, hidden, H, s); });
         if (trace_host)
             Lr.run(Q35_KT_OTHER, [&] {
