@@ -23,20 +23,68 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// Wave-wide reductions. Within each row of 16 lanes the partner values move by DPP (quad
+// xor 1, quad xor 2, half-row mirror, row mirror: after the four steps every lane holds its
+// row's total), the two rows of each half-wave meet through a swizzle (xor 16 within 32
+// lanes), and the totals of lanes 0-31 and 32-63 are read as scalars. Partners combine the
+// same two values in the same order on both sides, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(dpp_i<CTRL>(static_cast<int>(u))),
+                   hi = static_cast<uint32_t>(dpp_i<CTRL>(static_cast<int>(u >> 32)));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ float swz16_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ double swz16_d(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(u), 0x401F)),
+                   hi = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(u >> 32), 0x401F));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double lane_d(double v, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), l)),
+                   hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), l));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp_f<0xB1>(v);   // quad xor 1
+    v += dpp_f<0x4E>(v);   // quad xor 2
+    v += dpp_f<0x141>(v);  // half-row mirror
+    v += dpp_f<0x140>(v);  // row mirror
+    v += swz16_f(v);
+    return lane_f(v, 0) + lane_f(v, 32);
 }
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    v += swz16_d(v);
+    return lane_d(v, 0) + lane_d(v, 32);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, swz16_f(v));
+    return fmaxf(lane_f(v, 0), lane_f(v, 32));
 }
 
 // silu(x) = x / (1 + e^-x), sigmoid, softplus with the > 20 pass-through.

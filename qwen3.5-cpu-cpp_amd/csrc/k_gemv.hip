@@ -245,13 +245,18 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
                                              const float4 (&wv)[NX], float* xs) {
     const int tid = threadIdx.x, n = a.in_dim;
     __shared__ double red[4];
+    // Every use below is unconditional (slots past the input are zeroed by a select and
+    // stored to the spare slot xs[n .. n+3]): a use under a branch lets the compiler sink
+    // the input loads behind the weight loads, and then staging waits for all of them.
+#pragma unroll
+    for (int j = 0; j < NX; ++j)
+        if ((tid + j * 256) * 4 >= n) xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (PRO == kProRmsNorm) {
         double ss = 0.0;
 #pragma unroll
         for (int j = 0; j < NX; ++j)
-            if ((tid + j * 256) * 4 < n)
-                ss += static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
-                      static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
+            ss += static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
+                  static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
         ss = block_sum_lds(ss, red);
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + a.eps);
 #pragma unroll
@@ -280,7 +285,7 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
 #pragma unroll
     for (int j = 0; j < NX; ++j) {
         const int i = (tid + j * 256) * 4;
-        if (i < n) *reinterpret_cast<float4*>(xs + i) = xv[j];
+        *reinterpret_cast<float4*>(xs + min(i, n)) = xv[j];
     }
     lds_barrier();
 }
@@ -325,7 +330,7 @@ int gemv_max_blocks() {
 
 template <int PRO, int EPI, int NX, int KC>
 hipError_t launch_kc(const GemvArgs& a, hipStream_t s) {
-    const size_t lds = static_cast<size_t>(a.in_dim) * sizeof(float);
+    const size_t lds = static_cast<size_t>(a.in_dim + 4) * sizeof(float);  // + the spare slot
     const int max_blocks = gemv_max_blocks();
     if (EPI == kEpiSwiGluPair || a.rows >= 8192) {
         const int blocks = min(max_blocks, (a.rows + 7) / 8);
@@ -345,8 +350,8 @@ hipError_t launch_rpw(const GemvArgs& a, hipStream_t s) {
     const bool gated_ok = PRO != kProGatedNorm || a.head_dim == 128;
     if (PRO != kProSwiGlu) {
         if (a.in_dim == 2048 && gated_ok) return launch_kc<PRO, EPI, 2, 4>(a, s);
-        if (a.in_dim == 4096) return launch_kc<PRO, EPI, 0, 8>(a, s);
-        if (a.in_dim == 6144) return launch_kc<PRO, EPI, 0, 12>(a, s);
+        if (a.in_dim == 4096 && gated_ok) return launch_kc<PRO, EPI, 4, 8>(a, s);
+        if (a.in_dim == 6144 && gated_ok) return launch_kc<PRO, EPI, 6, 12>(a, s);
         if (a.in_dim <= 2048 && gated_ok) return launch_kc<PRO, EPI, 2, 0>(a, s);
     }
     return launch_kc<PRO, EPI, 0, 0>(a, s);
