@@ -70,12 +70,16 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += swz16_f(v);
     return lane_f(v, 0) + lane_f(v, 32);
 }
-__device__ __forceinline__ double wave_sum(double v) {
+// Sum over each half-wave (lanes 0-31, lanes 32-63), held by every lane of the half.
+__device__ __forceinline__ double half_wave_sum(double v) {
     v += dpp_d<0xB1>(v);
     v += dpp_d<0x4E>(v);
     v += dpp_d<0x141>(v);
     v += dpp_d<0x140>(v);
-    v += swz16_d(v);
+    return v + swz16_d(v);
+}
+__device__ __forceinline__ double wave_sum(double v) {
+    v = half_wave_sum(v);
     return lane_d(v, 0) + lane_d(v, 32);
 }
 __device__ __forceinline__ float wave_max(float v) {
@@ -151,6 +155,14 @@ __device__ __forceinline__ double block_sum_lds(double v, double* red) {
     double t = 0.0;
     for (int i = 0; i < nw; ++i) t += red[i];
     return t;
+}
+// Sum over a 256-thread workgroup, for a single use of `red` per kernel (no barrier before
+// the write: nothing read `red` earlier). Every thread gets the total.
+__device__ __forceinline__ double block_sum_once_256(double v, double* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    lds_barrier();
+    return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // Counter-based normal draw (splitmix64 finaliser + Box-Muller in double); the same

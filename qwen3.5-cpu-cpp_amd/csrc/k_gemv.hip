@@ -257,7 +257,7 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
         for (int j = 0; j < NX; ++j)
             ss += static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
                   static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
-        ss = block_sum_lds(ss, red);
+        ss = block_sum_once_256(ss, red);
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + a.eps);
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
@@ -273,8 +273,7 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX]
         for (int j = 0; j < NX; ++j) {
             double ss = static_cast<double>(xv[j].x) * xv[j].x + static_cast<double>(xv[j].y) * xv[j].y +
                         static_cast<double>(xv[j].z) * xv[j].z + static_cast<double>(xv[j].w) * xv[j].w;
-#pragma unroll
-            for (int o = 1; o < 32; o <<= 1) ss += __shfl_xor(ss, o);
+            ss = half_wave_sum(ss);
             const float inv = 1.0f / sqrtf(static_cast<float>(ss / a.head_dim) + a.eps);
             xv[j].x = wv[j].x * (xv[j].x * inv) * silu_f(gv[j].x);
             xv[j].y = wv[j].y * (xv[j].y * inv) * silu_f(gv[j].y);
