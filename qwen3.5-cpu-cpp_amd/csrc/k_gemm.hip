@@ -12,7 +12,8 @@
 // Tiling: 128 x 128 output tile per 256-thread workgroup, 4 waves in a 2 x 2 arrangement of
 // 64 x 64 quadrants, each quadrant 2 x 2 MFMA blocks of 32 x 32 (64 accumulator registers
 // per lane). K advances in stages of 32: the X and W tiles of the next stage are loaded into
-// registers while the current stage runs from LDS. LDS holds the three bf16 parts of the X
+// registers while the current stage runs from LDS (branch-free loads, LDS-only barriers, so
+// the loads stay in flight until the next stage's LDS store needs them). LDS holds the three bf16 parts of the X
 // tile and the W tile k-contiguous ([row][k], rows padded to 40 elements), so each MFMA
 // operand is one 16-byte read of 8 consecutive k.
 //
@@ -55,26 +56,39 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     // global -> register mapping: thread t loads row t / 2, k half (t % 2) * 16 of the stage
     const int lr = tid >> 1, lk = (tid & 1) * 16;
     const bool a_ok = m0 + lr < a.M, b_ok = n0 + lr < a.N;
-    const float* xrow = a.X + static_cast<int64_t>(a_ok ? m0 + lr : 0) * a.ldx + lk;
-    const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + lr : 0) * a.K + lk;
-    float4 ra[4];
-    uint4 rb[2];
+    const float* xrow = a.X + static_cast<int64_t>(a_ok ? m0 + lr : 0) * a.ldx;
+    const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + lr : 0) * a.K;
+    // Two stages of the X / W tiles in registers: while stage k is stored and multiplied,
+    // the loads of stage k + 1 are in flight, and stage k + 2 is requested as soon as
+    // stage k's registers are in LDS. Loads are unconditional (clamped to element K - 8 of
+    // a valid row); chunks past K or past the last row are zeroed by a bit mask when the
+    // stage is stored. A load or a use under a branch would make the wait-count pass wait
+    // for every outstanding load at the join.
     // K % 8 == 0: a 4-float or 8-bf16 chunk is wholly inside K or wholly past it (zeros)
-    auto load_stage = [&](int k0) {
+    uint4 raA[4];  // fp32 bit patterns
+    uint4 rbA[2];
+    auto load_stage = [&](uint4 (&ra)[4], uint4 (&rb)[2], int k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            ra[i] = a_ok && k0 + lk + 4 * i < a.K ? *reinterpret_cast<const float4*>(xrow + k0 + 4 * i)
-                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            ra[i] = *reinterpret_cast<const uint4*>(xrow + min(k0 + lk + 4 * i, a.K - 4));
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            rb[i] = b_ok && k0 + lk + 8 * i < a.K ? *reinterpret_cast<const uint4*>(wrow + k0 + 8 * i)
-                                                  : make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + lk + 8 * i, a.K - 8));
     };
-    auto store_stage = [&]() {
+    auto masked = [](uint4 v, bool live) {
+        const uint32_t m = 0u - static_cast<uint32_t>(live);
+        return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+    };
+    auto store_stage = [&](const uint4 (&rx)[4], const uint4 (&rw)[2], int k0) {
+        uint4 ra[4], rb[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) rb[i] = masked(rw[i], b_ok && k0 + lk + 8 * i < a.K);
         uint32_t hp[8], mp[8], lp[8];  // pairs of bf16 packed in a word
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+            const float v[4] = {__uint_as_float(ra[i].x), __uint_as_float(ra[i].y), __uint_as_float(ra[i].z),
+                                 __uint_as_float(ra[i].w)};
 #pragma unroll
             for (int j = 0; j < 4; j += 2) {
                 uint32_t h0, m0_, l0, h1, m1, l1;
@@ -103,12 +117,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     const int ar = wm * 64 + (lane & 31), br = wn * 64 + (lane & 31), kh = (lane >> 5) * 8;
-    load_stage(0);
-    for (int k0 = 0; k0 < a.K; k0 += kBK) {
-        __syncthreads();
-        store_stage();
-        __syncthreads();
-        if (k0 + kBK < a.K) load_stage(k0 + kBK);
+    auto mma = [&]() {
 #pragma unroll
         for (int s = 0; s < kBK / 16; ++s) {
             const int kk = s * 16 + kh;
@@ -126,6 +135,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
                 }
             }
         }
+    };
+    // LDS-only barriers: the next stages' global loads stay in flight through them
+    load_stage(raA, rbA, 0);
+    for (int k0 = 0; k0 < a.K; k0 += kBK) {
+        lds_barrier();  // the previous stage's operands have been read
+        store_stage(raA, rbA, k0);
+        lds_barrier();
+        load_stage(raA, rbA, k0 + kBK);
+        mma();
     }
     if constexpr (EPI == 2) {
         // the pair (gate, up) of one output sits in adjacent lanes (even, odd column)
