@@ -121,6 +121,7 @@ def run_attn_decode_bf16(hip, nq, nkv, pos, maxc, n_splits, seed, layers=1):
     (2, 1, 0, 3), (16, 2, 1, 4), (16, 2, 33, 40), (8, 2, 100, 103), (16, 1, 64, 70),
     (16, 2, 2047, 2048),   # the 2B head shape (GQA 8:1) at 2k / 8k
     (16, 2, 8191, 8192),
+    (16, 2, 131071, 131072),  # the long-decode context
 ])
 def test_attn_decode_bf16(hip, nq, nkv, pos, maxc):
     run_attn_decode_bf16(hip, nq, nkv, pos, maxc, 0, seed=pos * 7 + nq)

@@ -156,9 +156,10 @@ def test_attn_decode_small(hip, nq, nkv, pos):
     np.testing.assert_array_equal(vrow, vref)
 
 
-@pytest.mark.parametrize("pos", [2047, 8191, 32767])
+@pytest.mark.parametrize("pos", [2047, 8191, 32767, 131071])
 def test_attn_decode_2b_shape(hip, pos):
-    """16 q heads / 2 kv heads (GQA 8:1), head_dim 256, partial RoPE 64, at 2k/8k/32k."""
+    """16 q heads / 2 kv heads (GQA 8:1), head_dim 256, partial RoPE 64, at 2k/8k/32k and the
+    longest context of the long-decode workload (131072 positions, 1 GiB of K/V)."""
     out, ref, krow, kref, vrow, vref = run_attn(hip, 16, 2, pos, pos + 1, 0, seed=pos)
     assert rel_l2(out, ref) < REL_L2
     np.testing.assert_allclose(krow, kref, rtol=2e-6, atol=2e-6)
