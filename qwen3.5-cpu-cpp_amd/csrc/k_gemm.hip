@@ -53,40 +53,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
 
-    // global -> register mapping: thread t loads row t / 2, k half (t % 2) * 16 of the stage
-    const int lr = tid >> 1, lk = (tid & 1) * 16;
+    // global -> register mapping: thread t loads row t / 2, k half (t % 2) of the stage
+    constexpr int NXQ = kBK / 8, NWQ = kBK / 16;  // 16-byte X / W chunks per thread and stage
+    const int lr = tid >> 1, lk = (tid & 1) * (kBK / 2);
     const bool a_ok = m0 + lr < a.M, b_ok = n0 + lr < a.N;
     const float* xrow = a.X + static_cast<int64_t>(a_ok ? m0 + lr : 0) * a.ldx;
     const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + lr : 0) * a.K;
-    // Two stages of the X / W tiles in registers: while stage k is stored and multiplied,
-    // the loads of stage k + 1 are in flight, and stage k + 2 is requested as soon as
-    // stage k's registers are in LDS. Loads are unconditional (clamped to element K - 8 of
-    // a valid row); chunks past K or past the last row are zeroed by a bit mask when the
-    // stage is stored. A load or a use under a branch would make the wait-count pass wait
-    // for every outstanding load at the join.
+    // The next stage's X / W tiles are requested into registers right after the current
+    // stage is in LDS and stay in flight while it is multiplied. Loads are unconditional
+    // (clamped to element K - 8 of a valid row); chunks past K or past the last row are
+    // zeroed by a bit mask when the stage is stored. A load or a use under a branch would
+    // make the wait-count pass wait for every outstanding load at the join.
     // K % 8 == 0: a 4-float or 8-bf16 chunk is wholly inside K or wholly past it (zeros)
-    uint4 raA[4];  // fp32 bit patterns
-    uint4 rbA[2];
-    auto load_stage = [&](uint4 (&ra)[4], uint4 (&rb)[2], int k0) {
+    uint4 raA[NXQ];  // fp32 bit patterns
+    uint4 rbA[NWQ];
+    auto load_stage = [&](uint4 (&ra)[NXQ], uint4 (&rb)[NWQ], int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NXQ; ++i)
             ra[i] = *reinterpret_cast<const uint4*>(xrow + min(k0 + lk + 4 * i, a.K - 4));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + lk + 8 * i, a.K - 8));
+        for (int i = 0; i < NWQ; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + lk + 8 * i, a.K - 8));
     };
     auto masked = [](uint4 v, bool live) {
         const uint32_t m = 0u - static_cast<uint32_t>(live);
         return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
     };
-    auto store_stage = [&](const uint4 (&rx)[4], const uint4 (&rw)[2], int k0) {
-        uint4 ra[4], rb[2];
+    auto store_stage = [&](const uint4 (&rx)[NXQ], const uint4 (&rw)[NWQ], int k0) {
+        uint4 ra[NXQ], rb[NWQ];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
+        for (int i = 0; i < NXQ; ++i) ra[i] = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) rb[i] = masked(rw[i], b_ok && k0 + lk + 8 * i < a.K);
-        uint32_t hp[8], mp[8], lp[8];  // pairs of bf16 packed in a word
+        for (int i = 0; i < NWQ; ++i) rb[i] = masked(rw[i], b_ok && k0 + lk + 8 * i < a.K);
+        uint32_t hp[2 * NXQ], mp[2 * NXQ], lp[2 * NXQ];  // pairs of bf16 packed in a word
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NXQ; ++i) {
             const float v[4] = {__uint_as_float(ra[i].x), __uint_as_float(ra[i].y), __uint_as_float(ra[i].z),
                                  __uint_as_float(ra[i].w)};
 #pragma unroll
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             }
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < NWQ; ++q) {
             *reinterpret_cast<uint4*>(&Xs[0][lr][lk + 8 * q]) = make_uint4(hp[4 * q], hp[4 * q + 1], hp[4 * q + 2], hp[4 * q + 3]);
             *reinterpret_cast<uint4*>(&Xs[1][lr][lk + 8 * q]) = make_uint4(mp[4 * q], mp[4 * q + 1], mp[4 * q + 2], mp[4 * q + 3]);
             *reinterpret_cast<uint4*>(&Xs[2][lr][lk + 8 * q]) = make_uint4(lp[4 * q], lp[4 * q + 1], lp[4 * q + 2], lp[4 * q + 3]);
