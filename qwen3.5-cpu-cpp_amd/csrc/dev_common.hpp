@@ -22,6 +22,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
     return static_cast<uint16_t>(u >> 16);
 }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// x = hi + mid + lo exactly, each a bf16 (returned as its 16-bit pattern): hi = x with its
+// low 16 bits cleared, mid the same of the remainder, lo the rest (at most 8 significant
+// bits). A product of two bf16 values is exact in fp32, so x * w = hi w + mid w + lo w.
+__device__ __forceinline__ void split3(float x, uint32_t& h, uint32_t& m, uint32_t& l) {
+    const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+    const float r1 = x - __uint_as_float(hb);
+    const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+    const float r2 = r1 - __uint_as_float(mb);
+    h = hb >> 16;
+    m = mb >> 16;
+    l = __float_as_uint(r2) >> 16;
+}
 
 // Wave-wide reductions. Within each row of 16 lanes the partner values move by DPP (quad
 // xor 1, quad xor 2, half-row mirror, row mirror: after the four steps every lane holds its

@@ -426,7 +426,15 @@ __global__ __launch_bounds__(512) void attn_partial_kernel(AttnDecodeArgs a) {
 // so no lane exchange is needed between the two products; the softmax of a tile reduces
 // over the 4 registers and the 4 lane groups (two exchanges). Four waves per workgroup
 // walk whole tiles; their (m, l, O) are merged through LDS at the end.
+// With a bf16 cache the products run on the bf16 matrix cores instead, exactly: Q and P are
+// split into three bf16 parts each (hi + mid + lo = the fp32 value) and every bf16 x bf16
+// product is exact in fp32. S = K . Q^T on v_mfma_f32_16x16x32_bf16 (K operand: 8 dims
+// 32c + 8g .. + 7 of row p0 + l%16, one 16-byte load; Q parts from LDS in that order), and
+// O += P . V on v_mfma_f32_16x16x16_bf16 (P operand: the 4 score registers of head l%16 =
+// positions 4g .. 4g + 3; V operand: the same 4 positions of dim 64t + 4(l%16) + i,
+// regrouped from the loaded rows). The scores and O keep the fp32 layouts above.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kMW = 4;  // waves per workgroup of the matrix-core kernel
 
 template <bool KVB>
@@ -523,6 +531,9 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
     __shared__ float4 qs[16][64];             // Q operand: [c][lane]
+    // bf16 caches: the three exact bf16 parts of Q as the B operand of the 16x16x32 products,
+    // [part][c][lane] with lane 16 g + head holding dims 32 c + 8 g .. + 7
+    __shared__ uint4 qsb[KVB ? 3 : 1][KVB ? 8 : 1][64];
     __shared__ float4 ks[kHD / 4], vs[kHD / 4];  // the appended rows (as the cache holds them)
     __shared__ float os[kMW][GRP][kHD];
     __shared__ float ml_s[kMW][GRP][2];
@@ -547,16 +558,31 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         cs4 = *reinterpret_cast<const float4*>(t + min(ci, max(half - 4, 0)));
         sn4 = *reinterpret_cast<const float4*>(t + half + min(ci, max(half - 4, 0)));
     }
-    KT kA[16], vr[4][4];
+    // K rows as the A operand: fp32, 4 dims 16 c + 4 g .. per register (16 per tile); bf16,
+    // 8 dims 32 c + 8 g .. per 16-byte register (8 per tile, the 16x16x32 bf16 operand)
+    using KOp = typename std::conditional<KVB, uint4, KT>::type;
+    constexpr int NK = KVB ? 8 : 16;
+    KOp kA[NK];
+    KT vr[4][4];
     // Loads are issued unconditionally (a load under a branch makes the wait-count pass wait
     // for all outstanding loads at the join); past the end of the range every lane reads the
     // same 16 bytes of row w1 - 1, which costs the memory pipeline almost nothing.
     const int last = max(wl - 1, 0);  // a valid row to clamp to
-    auto loadK = [&](KT (&kr)[16], int p0) {
+    auto loadK = [&](KOp (&kr)[NK], int p0) {
         const int mask = -static_cast<int>(p0 < wl);  // all ones while live (no branch)
         const int64_t row = min(p0 + n16, last);
+        if constexpr (KVB) {
+            typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+            const uint16_t* Kb = reinterpret_cast<const uint16_t*>(Kc_);
 #pragma unroll
-        for (int c = 0; c < 16; ++c) kr[c] = KV::load(Kc_, row * kHD + ((16 * c + 4 * g) & mask));
+            for (int c = 0; c < NK; ++c) {
+                const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(Kb + row * kHD + ((32 * c + 8 * g) & mask)));
+                kr[c] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < NK; ++c) kr[c] = KV::load(Kc_, row * kHD + ((16 * c + 4 * g) & mask));
+        }
     };
     auto loadV = [&](int p0) {
         const int mask = -static_cast<int>(p0 < wl);
@@ -574,6 +600,9 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     if (!a.rope_cs) rope_cs4(a.theta, ROT, pos, lane, cs4, sn4);  // double-precision angles
     for (int e = tid; e < 16 * 32; e += kMW * 64)  // columns 8-15: zero heads
         qs[e >> 5][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (KVB)
+        for (int e = tid; e < 3 * 8 * 32; e += kMW * 64)
+            qsb[e >> 8][(e >> 5) & 7][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int r = wave + i * kMW;
@@ -581,6 +610,18 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         float4 y = norm_rope_row(px[i], pw[i], cs4, sn4, lane, ROT, a.eps);
         if (r < GRP) {
             qs[lane >> 2][16 * (lane & 3) + r] = y;  // dims 4 lane .. + 3 of head r
+            if constexpr (KVB) {  // dims 4 lane .. + 3 = half (lane & 1) of the slot (lane >> 3, (lane >> 1) & 3)
+                const float v4[4] = {y.x, y.y, y.z, y.w};
+                uint32_t hh[4], mm[4], ll[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) split3(v4[e], hh[e], mm[e], ll[e]);
+                uint2* slot0 = reinterpret_cast<uint2*>(&qsb[0][lane >> 3][16 * ((lane >> 1) & 3) + r]) + (lane & 1);
+                uint2* slot1 = reinterpret_cast<uint2*>(&qsb[1][lane >> 3][16 * ((lane >> 1) & 3) + r]) + (lane & 1);
+                uint2* slot2 = reinterpret_cast<uint2*>(&qsb[2][lane >> 3][16 * ((lane >> 1) & 3) + r]) + (lane & 1);
+                *slot0 = make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16));
+                *slot1 = make_uint2(mm[0] | (mm[1] << 16), mm[2] | (mm[3] << 16));
+                *slot2 = make_uint2(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16));
+            }
         } else {
             const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + lane * 4;
             if constexpr (KVB) {
@@ -617,23 +658,42 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
 
     // one tile of positions p0 .. p0 + 15 from K registers kr and the V registers; the next
     // tile's rows are requested as soon as these registers are consumed
-    auto tile = [&](KT (&kr)[16], int p0, auto more) {
-        // four independent accumulation chains (dims 16c + 4g + i, one chain per i)
-        floatx4 S4[4];
+    auto tile = [&](KOp (&kr)[NK], int p0, auto more) {
+        floatx4 S;
+        if constexpr (KVB) {
+            // bf16 K times the three exact bf16 parts of Q on the 16x16x32 bf16 matrix cores
+            // (every product exact in fp32), one accumulation chain per part
+            floatx4 S3[3];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int i = 0; i < 3; ++i) S3[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const float4 q = qs[c][lane];
-            const float4 k = KV::f4(kr[c]);
-            S4[0] = mfma16(k.x, q.x, S4[0]);
-            S4[1] = mfma16(k.y, q.y, S4[1]);
-            S4[2] = mfma16(k.z, q.z, S4[2]);
-            S4[3] = mfma16(k.w, q.w, S4[3]);
-            // keep the Q operand reads close to their use (a few in flight, not all 16)
-            if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            for (int c = 0; c < NK; ++c) {
+                const bf16x8 kop = __builtin_bit_cast(bf16x8, kr[c]);
+#pragma unroll
+                for (int part = 0; part < 3; ++part)
+                    S3[part] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, __builtin_bit_cast(bf16x8, qsb[part][c][lane]),
+                                                                       S3[part], 0, 0, 0);
+                if ((c & 1) == 1) __builtin_amdgcn_sched_barrier(0);
+            }
+            S = (S3[2] + S3[1]) + S3[0];
+        } else {
+            // four independent accumulation chains (dims 16c + 4g + i, one chain per i)
+            floatx4 S4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const float4 q = qs[c][lane];
+                const float4 k = KV::f4(kr[c]);
+                S4[0] = mfma16(k.x, q.x, S4[0]);
+                S4[1] = mfma16(k.y, q.y, S4[1]);
+                S4[2] = mfma16(k.z, q.z, S4[2]);
+                S4[3] = mfma16(k.w, q.w, S4[3]);
+                // keep the Q operand reads close to their use (a few in flight, not all 16)
+                if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            }
+            S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
         }
-        const floatx4 S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
         if constexpr (decltype(more)::value) loadK(kr, p0 + TP);
         float s[4];
 #pragma unroll
@@ -667,16 +727,45 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
                 O[t][3] *= fh[3];
             }
         }
+        if constexpr (KVB) {
+            // the three exact bf16 parts of P (A operand: head n16, positions 4g .. 4g + 3)
+            // times bf16 V (B operand: those positions, dim 64t + 4 n16 + i) on the 16x16x16
+            // bf16 matrix cores; V's 16-bit elements are regrouped from the rows as loaded
+            typedef short short4_ __attribute__((ext_vector_type(4)));
+            uint32_t hh[4], mm[4], ll[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
+            for (int v = 0; v < 4; ++v) split3(p[v], hh[v], mm[v], ll[v]);
+            const short4_ pp[3] = {
+                __builtin_bit_cast(short4_, make_uint2(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16))),
+                __builtin_bit_cast(short4_, make_uint2(mm[0] | (mm[1] << 16), mm[2] | (mm[3] << 16))),
+                __builtin_bit_cast(short4_, make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16)))};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float4 vv = KV::f4(vr[v][t]);
-                O[4 * t + 0] = mfma16(p[v], vv.x, O[4 * t + 0]);
-                O[4 * t + 1] = mfma16(p[v], vv.y, O[4 * t + 1]);
-                O[4 * t + 2] = mfma16(p[v], vv.z, O[4 * t + 2]);
-                O[4 * t + 3] = mfma16(p[v], vv.w, O[4 * t + 3]);
-            }
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint32_t e[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const uint32_t w = i < 2 ? vr[v][t].x : vr[v][t].y;
+                        e[v] = (i & 1) ? w >> 16 : w & 0xffffu;
+                    }
+                    const short4_ vb = __builtin_bit_cast(short4_, make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)));
+#pragma unroll
+                    for (int part = 0; part < 3; ++part)  // lo, mid, hi
+                        O[4 * t + i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pp[part], vb, O[4 * t + i], 0, 0, 0);
+                }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float4 vv = KV::f4(vr[v][t]);
+                    O[4 * t + 0] = mfma16(p[v], vv.x, O[4 * t + 0]);
+                    O[4 * t + 1] = mfma16(p[v], vv.y, O[4 * t + 1]);
+                    O[4 * t + 2] = mfma16(p[v], vv.z, O[4 * t + 2]);
+                    O[4 * t + 3] = mfma16(p[v], vv.w, O[4 * t + 3]);
+                }
+        }
         if constexpr (decltype(more)::value) loadV(p0 + TP);
     };
     int p0 = w0;

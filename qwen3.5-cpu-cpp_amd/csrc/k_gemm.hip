@@ -33,17 +33,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kBM = 128, kBN = 128, kBK = 32;
 constexpr int kLd = kBK + 8;  // padded row (bf16 elements): 80 B, rows start on distinct banks
 
-// x = hi + mid + lo exactly, each a bf16 (returned as its 16-bit pattern)
-__device__ __forceinline__ void split3(float x, uint32_t& h, uint32_t& m, uint32_t& l) {
-    const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
-    const float r1 = x - __uint_as_float(hb);
-    const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
-    const float r2 = r1 - __uint_as_float(mb);
-    h = hb >> 16;
-    m = mb >> 16;
-    l = __float_as_uint(r2) >> 16;
-}
-
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
