@@ -351,7 +351,7 @@ def bench_prefill(a) -> dict:
         "dtype": "fp32", "data": "synthetic: random-init bf16 weights N(0,0.02) seed 0, ids uniform seed 2",
         "config": {"workload": f"2B-shaped Qwen3.5 prefill of {T} tokens", "hidden": d.hidden_size,
                    "layers": "24 = 18 GDN + 6 gated attention", "prompt": T,
-                   "block": a.prefill_block or min(2048, T + 8), "gdn_chunk": 64},
+                   "block": a.prefill_block or min(4096, T + 8), "gdn_chunk": 64},
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": ach, "peak": peak,
                      "unit": "TFLOP/s", "frac": ach / peak, "traffic": None,
                      "note": "fp32 flops of the algorithm; GEMM peak = dense bf16 MFMA peak / 3 (exact "
