@@ -291,8 +291,12 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
         }
     };
     load_chunk(0);
+    // LDS-only barriers inside the loop: the next chunk's loads and this chunk's global
+    // stores stay in flight through them (a full barrier would wait for every outstanding
+    // load, the prefetch included)
+    __syncthreads();  // the state slice is in LDS
     for (int c = 0; c < nchunk; ++c) {
-        __syncthreads();  // previous chunk done with Wl / Kl / Ss
+        lds_barrier();  // previous chunk done with Wl / Kl / Ss
         store_chunk();
         const float glast = rglast;
         floatx4 vn;
@@ -301,8 +305,8 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
         // chunk-start state for the output pass
         float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
         for (int i = tid; i < kD * kSW; i += 256) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
-        __syncthreads();
-        if (c + 1 < nchunk) load_chunk(c + 1);
+        lds_barrier();
+        load_chunk(min(c + 1, nchunk - 1));  // unconditional (the last chunk is requested twice)
 
         // v_new rows [16w, 16w + 16) = U - W S
         float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
@@ -319,7 +323,7 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
             U[(16 * wave + 4 * lg + v) * kD + lr] = vn[v];
             VN[16 * wave + 4 * lg + v][lr] = vn[v];
         }
-        __syncthreads();  // VN complete, every wave done reading Ss
+        lds_barrier();  // VN complete, every wave done reading Ss
 
         // new state rows [32w, 32w + 32), one 16-row block at a time. Each block is written
         // back right after its product: with both blocks' eight stores in one basic block this
