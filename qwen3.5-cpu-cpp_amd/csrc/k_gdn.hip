@@ -56,8 +56,21 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     __shared__ float part[NRG][CS];
     __shared__ double red[4];
 
-    // The state slice and the per-head scalars do not depend on the conv: request them first,
-    // so their latency overlaps the conv loads instead of following the two barriers.
+    // Loads in the order they are needed (they complete in order for the wait counter): the
+    // conv inputs of the 128 q, 128 k and this slice's v channels (every thread loads a v
+    // channel, clamped to the slice, so no load sits under a branch), then the state slice
+    // and the per-head scalars, which are first used after the l2norm. The barriers up to
+    // there order LDS only, so the state loads stay in flight through the conv and the norm.
+    const int chq = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
+    const int chv = 2 * KD + vh * kD + split * CS + (tid % CS);
+    const float4 wq = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chq) * 4);
+    const float xq = qkv[chq];
+    const float rq3 = ring[static_cast<int64_t>(s_m3) * CONV + chq], rq2 = ring[static_cast<int64_t>(s_m2) * CONV + chq],
+                rq1 = ring[static_cast<int64_t>(s_m1) * CONV + chq];
+    const float4 wv = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chv) * 4);
+    const float xv = qkv[chv];
+    const float rv3 = ring[static_cast<int64_t>(s_m3) * CONV + chv], rv2 = ring[static_cast<int64_t>(s_m2) * CONV + chv],
+                rv1 = ring[static_cast<int64_t>(s_m1) * CONV + chv];
     const int c = tid % CS, rg = tid / CS, r0 = rg * RPT;
     float* Sc = S + split * CS + c;
     float s[RPT];
@@ -65,35 +78,31 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     for (int i = 0; i < RPT; ++i) s[i] = Sc[(r0 + i) * kD];
     const float A_v = A_log[vh], dt_v = dt_bias[vh], a_v = ain[vh], b_v = bin[vh];
 
-    // causal conv (taps oldest first) + SiLU for the 128 q and 128 k channels of head kh
+    // causal conv (taps oldest first) + SiLU for the 128 q and 128 k channels of head kh ...
     {
-        const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
-        const float* w4 = convw + static_cast<int64_t>(ch) * 4;
-        const float xn = qkv[ch];
         float acc = 0.0f;
-        acc += w4[0] * ring[static_cast<int64_t>(s_m3) * CONV + ch];
-        acc += w4[1] * ring[static_cast<int64_t>(s_m2) * CONV + ch];
-        acc += w4[2] * ring[static_cast<int64_t>(s_m1) * CONV + ch];
-        acc += w4[3] * xn;
+        acc += wq.x * rq3;
+        acc += wq.y * rq2;
+        acc += wq.z * rq1;
+        acc += wq.w * xq;
         const float y = silu_f(acc);
         if (tid < kD) q_s[tid] = y;
         else k_s[tid - kD] = y;
-        if (vh % rep == 0 && split == 0) ring[static_cast<int64_t>(s_new) * CONV + ch] = xn;
+        if (vh % rep == 0 && split == 0) ring[static_cast<int64_t>(s_new) * CONV + chq] = xq;
     }
     // ... and for this slice's v channels
-    if (tid < CS) {
-        const int ch = 2 * KD + vh * kD + split * CS + tid;
-        const float* w4 = convw + static_cast<int64_t>(ch) * 4;
-        const float xn = qkv[ch];
+    {
         float acc = 0.0f;
-        acc += w4[0] * ring[static_cast<int64_t>(s_m3) * CONV + ch];
-        acc += w4[1] * ring[static_cast<int64_t>(s_m2) * CONV + ch];
-        acc += w4[2] * ring[static_cast<int64_t>(s_m1) * CONV + ch];
-        acc += w4[3] * xn;
-        v_s[tid] = silu_f(acc);
-        ring[static_cast<int64_t>(s_new) * CONV + ch] = xn;
+        acc += wv.x * rv3;
+        acc += wv.y * rv2;
+        acc += wv.z * rv1;
+        acc += wv.w * xv;
+        if (tid < CS) {
+            v_s[tid] = silu_f(acc);
+            ring[static_cast<int64_t>(s_new) * CONV + chv] = xv;
+        }
     }
-    __syncthreads();
+    lds_barrier();
 
     // l2norm (eps 1e-6, sum of squares in double); q also scaled by DK^-1/2
     {
@@ -101,7 +110,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         double ss = static_cast<double>(v) * v;
         ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
-        __syncthreads();
+        lds_barrier();
         const double sq = red[0] + red[1], sk = red[2] + red[3];
         if (tid < kD) {
             const float inv = 1.0f / sqrtf(static_cast<float>(sq) + 1e-6f);
@@ -113,7 +122,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     }
     const float g = -expf(A_v) * softplus_f(a_v + dt_v);
     const float alpha = expf(g), beta = sigmoid_f(b_v);
-    __syncthreads();
+    lds_barrier();
 
     // decay, S^T k, delta, rank-1 update, S^T q on the register-resident slice
     float km = 0.0f;
@@ -123,14 +132,14 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         km += s[i] * k_s[r0 + i];
     }
     part[rg][c] = km;
-    __syncthreads();
+    lds_barrier();
     if (tid < CS) {
         float t = 0.0f;
 #pragma unroll
         for (int r = 0; r < NRG; ++r) t += part[r][tid];
         d_s[tid] = (v_s[tid] - t) * beta;
     }
-    __syncthreads();
+    lds_barrier();
     const float dv = d_s[c];
     float o = 0.0f;
 #pragma unroll
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < RPT; ++i) Sc[(r0 + i) * kD] = s[i];
     part[rg][c] = o;
-    __syncthreads();
+    lds_barrier();
 
     float ov = 0.0f;
     if (tid < CS) {
@@ -152,9 +161,9 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         // CS == 128: threads 0..127 hold the head's readout
         double ss = tid < kD ? static_cast<double>(ov) * ov : 0.0;
         ss = wave_sum(ss);
-        __syncthreads();
+        lds_barrier();
         if (lane == 0) red[wave] = ss;
-        __syncthreads();
+        lds_barrier();
         const double tot = red[0] + red[1];
         if (tid < kD) {
             const float inv = 1.0f / sqrtf(static_cast<float>(tot / kD) + a.eps);
