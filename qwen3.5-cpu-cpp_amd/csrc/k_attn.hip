@@ -883,19 +883,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
     const int64_t so = static_cast<int64_t>(grp) * kHD;
     __shared__ float w_s[256], red[4], o_s[4][64];
 
-    const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + d];
-    float ov[kRW];
-#pragma unroll
-    for (int u = 0; u < kRW; ++u) ov[u] = po[min(wave * kRW + u, nact - 1) * so];
+    // (m, l) first: loads complete in order for the wait counter, so the maximum and the
+    // weights need not wait for the o rows, which stay in flight through the LDS-only
+    // barriers until the weighted sum
     const float* ml = a.part_ml + (base + static_cast<int64_t>(min(tid, nact - 1)) * grp) * 2;
     float m_t = ml[0];
     const float l_t = ml[1];
+    float ov[kRW];
+#pragma unroll
+    for (int u = 0; u < kRW; ++u) ov[u] = po[min(wave * kRW + u, nact - 1) * so];
+    const float gate = a.qg[static_cast<int64_t>(h) * 2 * kHD + kHD + d];
     if (tid >= nact) m_t = -INFINITY;
     float mx = m_t;
     for (int s = tid + 256; s < nact; s += 256) mx = fmaxf(mx, a.part_ml[(base + static_cast<int64_t>(s) * grp) * 2]);
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
-    __syncthreads();
+    lds_barrier();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f, o = 0.0f;
     for (int c0 = 0; c0 < nact; c0 += 256) {
@@ -910,9 +913,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
             w = expf(a.part_ml[i * 2] - M);
             L = fmaf(a.part_ml[i * 2 + 1], w, L);
         }
-        __syncthreads();  // the previous pass's weights (and the maxima) are consumed
+        lds_barrier();  // the previous pass's weights (and the maxima) are consumed
         w_s[tid] = w;
-        __syncthreads();
+        lds_barrier();
         for (int c1 = 0; c1 < 256 && c0 + c1 < nact; c1 += 4 * kRW) {
             if (c0 + c1 > 0) {
 #pragma unroll
@@ -926,7 +929,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
     o_s[wave][lane] = o;
     L = wave_sum(L);
     if (lane == 0) red[wave] = L;
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
         const float Lt = (red[0] + red[1]) + (red[2] + red[3]);
         const float ot = (o_s[0][lane] + o_s[1][lane]) + (o_s[2][lane] + o_s[3][lane]);
