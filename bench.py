@@ -420,7 +420,8 @@ def main() -> None:
     ap.add_argument("--cpu-prompt", type=int, default=32, help="prefill: prompt tokens of the CPU sample")
     ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets, round-robin")
     ap.add_argument("--ctx-list", type=lambda s: [int(x) for x in s.split(",")], default=[2048, 8192, 32768])
-    ap.add_argument("--attn-splits", type=int, default=0)
+    ap.add_argument("--attn-splits", type=int, default=0,
+                    help="attention split-K count (0 = the library default)")
     ap.add_argument("--kv", choices=["fp32", "bf16"], default="fp32",
                     help="KV cache element type (decode, attn): fp32 is the reference's cache")
     ap.add_argument("--calibration-copy", action="store_true",
@@ -449,6 +450,8 @@ def main() -> None:
     kv_elem = 2 if a.kv == "bf16" else 4
     m = pyq35.Model(model_dir, max_ctx, kv_bytes_per_elem=kv_elem)
     log(f"model uploaded in {time.time() - t:.1f} s; budget {m.budget()}")
+    if a.attn_splits:
+        m.set_attn_splits(a.attn_splits)
     hip = pyq35.Hip()
     if small:
         # the 0.8B-shaped greedy run: a prompt of uniform ids (seed 1) prefilled, then decode
