@@ -9,13 +9,17 @@
 // significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul with
 // fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one fp32 MFMA.
 //
-// Tiling: 128 x 128 output tile per 256-thread workgroup, 4 waves in a 2 x 2 arrangement of
-// 64 x 64 quadrants, each quadrant 2 x 2 MFMA blocks of 32 x 32 (64 accumulator registers
-// per lane). K advances in stages of 32: the X and W tiles of the next stage are loaded into
-// registers while the current stage runs from LDS (branch-free loads, LDS-only barriers, so
-// the loads stay in flight until the next stage's LDS store needs them). LDS holds the three bf16 parts of the X
-// tile and the W tile k-contiguous ([row][k], rows padded to 40 elements), so each MFMA
-// operand is one 16-byte read of 8 consecutive k.
+// Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
+// of it: 1 x 4 MFMA blocks of 32 x 32 (64 accumulator registers per lane). K advances in
+// stages of 32: the X and W tiles of the next stage are loaded into registers while the
+// current stage runs from LDS (branch-free loads, LDS-only barriers, so the loads stay in
+// flight until the next stage's LDS store needs them). LDS holds the X tile as fp32
+// ([row][k], rows padded to 36 floats) and the W tile as bf16 ([row][k], rows padded to 40
+// elements); a wave reads its 8 fp32 k values of an X row (two 16-byte reads) and splits them
+// into the three bf16 A operands in registers, and each W operand is one 16-byte read. Per
+// 12 MFMAs a wave reads 32 B of X and 64 B of W per lane from LDS (a quarter less LDS traffic
+// than three pre-split bf16 X tiles), and the split of a value happens once, in the one wave
+// that uses it.
 //
 // MFMA operand layout (32x32x16 bf16, one block): lane l supplies row / column l % 32 and the 8
 // k values 8 (l / 32) .. 8 (l / 32) + 7 of the 16-k step; both operands use the same k
@@ -29,17 +33,29 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
-constexpr int kLd = kBK + 8;  // padded row (bf16 elements): 80 B, rows start on distinct banks
+constexpr int kLdX = kBK + 4;  // padded X row (floats): 144 B, 16-byte reads of 8 rows hit distinct banks
+constexpr int kLd = kBK + 8;   // padded W row (bf16 elements): 80 B
+
+// the three bf16 parts of two floats a, b, each part's pair packed (a low, b high)
+__device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint32_t& m, uint32_t& l) {
+    const uint32_t ha = __float_as_uint(a) & 0xffff0000u, hb = __float_as_uint(b) & 0xffff0000u;
+    const float ra = a - __uint_as_float(ha), rb = b - __uint_as_float(hb);
+    const uint32_t ma = __float_as_uint(ra) & 0xffff0000u, mb = __float_as_uint(rb) & 0xffff0000u;
+    const float la = ra - __uint_as_float(ma), lb = rb - __uint_as_float(mb);
+    h = (ha >> 16) | hb;
+    m = (ma >> 16) | mb;
+    l = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xffff0000u);
+}
 
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-    __shared__ __align__(16) uint16_t Xs[3][kBM][kLd];
+    __shared__ __align__(16) float Xs[kBM][kLdX];
     __shared__ __align__(16) uint16_t Ws[kBN][kLd];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
 
     // global -> register mapping: thread t loads row t / 2, k half (t % 2) of the stage
@@ -68,61 +84,43 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
     };
     auto store_stage = [&](const uint4 (&rx)[NXQ], const uint4 (&rw)[NWQ], int k0) {
-        uint4 ra[NXQ], rb[NWQ];
 #pragma unroll
-        for (int i = 0; i < NXQ; ++i) ra[i] = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
+        for (int i = 0; i < NXQ; ++i)
+            *reinterpret_cast<uint4*>(&Xs[lr][lk + 4 * i]) = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
 #pragma unroll
-        for (int i = 0; i < NWQ; ++i) rb[i] = masked(rw[i], b_ok && k0 + lk + 8 * i < a.K);
-        uint32_t hp[2 * NXQ], mp[2 * NXQ], lp[2 * NXQ];  // pairs of bf16 packed in a word
-#pragma unroll
-        for (int i = 0; i < NXQ; ++i) {
-            const float v[4] = {__uint_as_float(ra[i].x), __uint_as_float(ra[i].y), __uint_as_float(ra[i].z),
-                                 __uint_as_float(ra[i].w)};
-#pragma unroll
-            for (int j = 0; j < 4; j += 2) {
-                uint32_t h0, m0_, l0, h1, m1, l1;
-                split3(v[j], h0, m0_, l0);
-                split3(v[j + 1], h1, m1, l1);
-                hp[2 * i + j / 2] = h0 | (h1 << 16);
-                mp[2 * i + j / 2] = m0_ | (m1 << 16);
-                lp[2 * i + j / 2] = l0 | (l1 << 16);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < NWQ; ++q) {
-            *reinterpret_cast<uint4*>(&Xs[0][lr][lk + 8 * q]) = make_uint4(hp[4 * q], hp[4 * q + 1], hp[4 * q + 2], hp[4 * q + 3]);
-            *reinterpret_cast<uint4*>(&Xs[1][lr][lk + 8 * q]) = make_uint4(mp[4 * q], mp[4 * q + 1], mp[4 * q + 2], mp[4 * q + 3]);
-            *reinterpret_cast<uint4*>(&Xs[2][lr][lk + 8 * q]) = make_uint4(lp[4 * q], lp[4 * q + 1], lp[4 * q + 2], lp[4 * q + 3]);
-            *reinterpret_cast<uint4*>(&Ws[lr][lk + 8 * q]) = rb[q];
-        }
+        for (int q = 0; q < NWQ; ++q)
+            *reinterpret_cast<uint4*>(&Ws[lr][lk + 8 * q]) = masked(rw[q], b_ok && k0 + lk + 8 * q < a.K);
     };
 
-    floatx16 acc[2][2];
+    floatx16 acc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
-    const int ar = wm * 64 + (lane & 31), br = wn * 64 + (lane & 31), kh = (lane >> 5) * 8;
+    const int ar = wave * 32 + (lane & 31), br = lane & 31, kh = (lane >> 5) * 8;
     auto mma = [&]() {
 #pragma unroll
         for (int s = 0; s < kBK / 16; ++s) {
             const int kk = s * 16 + kh;
-            bf16x8 bop[2];
+            const float4 x0 = *reinterpret_cast<const float4*>(&Xs[ar][kk]);
+            const float4 x1 = *reinterpret_cast<const float4*>(&Xs[ar][kk + 4]);
+            bf16x8 bop[4];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bop[j] = *reinterpret_cast<const bf16x8*>(&Ws[br + 32 * j][kk]);
+            for (int j = 0; j < 4; ++j) bop[j] = *reinterpret_cast<const bf16x8*>(&Ws[br + 32 * j][kk]);
+            uint32_t h[4], m[4], l[4];
+            split3_pair(x0.x, x0.y, h[0], m[0], l[0]);
+            split3_pair(x0.z, x0.w, h[1], m[1], l[1]);
+            split3_pair(x1.x, x1.y, h[2], m[2], l[2]);
+            split3_pair(x1.z, x1.w, h[3], m[3], l[3]);
+            const bf16x8 aop[3] = {__builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]}),
+                                   __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]}),
+                                   __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]})};
 #pragma unroll
-            for (int p = 2; p >= 0; --p) {  // lo, mid, hi
+            for (int p = 2; p >= 0; --p)  // lo, mid, hi
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const bf16x8 aop = *reinterpret_cast<const bf16x8*>(&Xs[p][ar + 32 * i][kk]);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[j], acc[i][j], 0, 0, 0);
-                }
-            }
+                for (int j = 0; j < 4; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[p], bop[j], acc[j], 0, 0, 0);
         }
     };
     // LDS-only barriers: the next stages' global loads stay in flight through them
@@ -134,38 +132,35 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         load_stage(raA, rbA, k0 + kBK);
         mma();
     }
+    const int rbase = m0 + wave * 32 + 4 * (lane >> 5);
     if constexpr (EPI == 2) {
         // the pair (gate, up) of one output sits in adjacent lanes (even, odd column)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 4; ++j) {
+            const int col = n0 + j * 32 + (lane & 31);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float up = __shfl_xor(acc[i][j][v], 1);
-                    const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                    if (!(lane & 1) && col + 1 < a.N && row < a.M)
-                        a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = silu_f(acc[i][j][v]) * up;
-                }
+            for (int v = 0; v < 16; ++v) {
+                const float up = __shfl_xor(acc[j][v], 1);
+                const int row = rbase + 8 * (v >> 2) + (v & 3);
+                if (!(lane & 1) && col + 1 < a.N && row < a.M)
+                    a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = silu_f(acc[j][v]) * up;
             }
+        }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 4; ++j) {
+        const int col = n0 + j * 32 + (lane & 31);
+        if (col >= a.N) continue;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (col >= a.N) continue;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                if (row < a.M) {
-                    float* y = a.Y + static_cast<int64_t>(row) * a.ldy + col;
-                    *y = EPI == 1 ? a.R[static_cast<int64_t>(row) * a.ldr + col] + acc[i][j][v] : acc[i][j][v];
-                }
+        for (int v = 0; v < 16; ++v) {
+            const int row = rbase + 8 * (v >> 2) + (v & 3);
+            if (row < a.M) {
+                float* y = a.Y + static_cast<int64_t>(row) * a.ldy + col;
+                *y = EPI == 1 ? a.R[static_cast<int64_t>(row) * a.ldr + col] + acc[j][v] : acc[j][v];
             }
         }
+    }
 }
 
 }  // namespace
