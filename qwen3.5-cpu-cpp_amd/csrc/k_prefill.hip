@@ -356,29 +356,57 @@ constexpr int kLdS = kD + 16;   // state / v_new rows (B operand)
 // grid (VH, Tp / 64), 256 threads: o = e^gamma (Q S_c) + P v_new for one chunk of one v-head,
 // then the gated rmsnorm (src/forward_pass.cpp:86-93, sum of squares in double) or the raw
 // readout. Wave w owns output rows [16w, 16w + 16), all 128 columns (8 blocks of 16).
-__global__ __launch_bounds__(256) void gdn_out_kernel(GdnPrefillArgs a) {
+// S_c goes through LDS in two halves of 64 rows (71 KB of LDS, two workgroups per CU), and
+// each phase's operands are requested into registers while the previous phase multiplies:
+// the second half of S_c during Q S_c[0:64), P and v_new during Q S_c[64:128).
+__global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int kh = vh / (a.VH / a.KH);
     const int nchunk = a.Tp / kC;
     const int64_t row0 = static_cast<int64_t>(c) * kC;
     __shared__ float A_s[kC][kLdQ];   // Q, then P
-    __shared__ float B_s[kD][kLdS];   // S_c, then v_new
+    __shared__ float B_s[kC][kLdS];   // S_c rows [0, 64), then [64, 128), then v_new
     __shared__ float gam[kC];
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD;
-    for (int f = tid; f < kC * kD / 4; f += 256)
+    const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
+    const float* Vn = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
+    constexpr int NQ4 = kC * kD / 4 / 256;  // float4 per thread of a 64 x 128 tile (8)
+    constexpr int NP4 = kC * kC / 4 / 256;  // of the 64 x 64 P tile (4)
+    for (int f = tid; f < kC * kD / 4; f += 256) {
         *reinterpret_cast<float4*>(&A_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
-    for (int f = tid; f < kD * kD / 4; f += 256)
         *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Sc + f * 4);
+    }
     if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
     __syncthreads();
+    float4 rs[NQ4];  // S_c rows [64, 128)
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) rs[i] = *reinterpret_cast<const float4*>(Sc + kC * kD + (tid + 256 * i) * 4);
     floatx4 acc[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-    for (int k = 0; k < kD; k += 4) {
+    for (int k = 0; k < kC; k += 4) {
         const float av = A_s[16 * wave + lr][k + lg];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
+    }
+    lds_barrier();  // done with S_c[0:64)
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = rs[i];
+    }
+    lds_barrier();
+    float4 rp[NP4], rv[NQ4];
+#pragma unroll
+    for (int i = 0; i < NP4; ++i) rp[i] = *reinterpret_cast<const float4*>(P + (tid + 256 * i) * 4);
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) rv[i] = *reinterpret_cast<const float4*>(Vn + (tid + 256 * i) * 4);
+#pragma unroll 4
+    for (int k = 0; k < kC; k += 4) {
+        const float av = A_s[16 * wave + lr][kC + k + lg];
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
     }
@@ -388,14 +416,18 @@ __global__ __launch_bounds__(256) void gdn_out_kernel(GdnPrefillArgs a) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[b][v] *= e;
     }
-    __syncthreads();  // done with Q and S_c
-    const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
-    const float* Vn = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
-    for (int f = tid; f < kC * kC / 4; f += 256)
-        *reinterpret_cast<float4*>(&A_s[f >> 4][(f & 15) * 4]) = *reinterpret_cast<const float4*>(P + f * 4);
-    for (int f = tid; f < kC * kD / 4; f += 256)
-        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Vn + f * 4);
-    __syncthreads();
+    lds_barrier();  // done with Q and S_c
+#pragma unroll
+    for (int i = 0; i < NP4; ++i) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<float4*>(&A_s[f >> 4][(f & 15) * 4]) = rp[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = rv[i];
+    }
+    lds_barrier();
     // P is lower triangular: the row block of wave w needs columns j < 16 (w + 1)
     for (int k = 0; k < 16 * (wave + 1); k += 4) {
         const float av = A_s[16 * wave + lr][k + lg];
