@@ -8,7 +8,7 @@
 //            g = -exp(A_log) softplus(a + dt_bias); head-major outputs padded to whole chunks
 //            (padding rows have q = k = v = 0, beta = g = 0 and change nothing).
 //   ring     the last three raw inputs of the block go to their ring slots.
-//   chunk    per (v-head, chunk): gamma = cumsum(g);
+//   chunk    per (v-head, chunk): gamma = cumsum(g); Q K^T and K K^T on the fp32 matrix cores;
 //              P[i][j] = q_i.k_j e^(gamma_i - gamma_j)      (j <= i)
 //              A[i][j] = beta_i k_i.k_j e^(gamma_i - gamma_j)  (j < i)
 //              [U | W] = (I + A)^-1 [beta v | beta e^gamma k]  (forward substitution, one
@@ -148,21 +148,31 @@ __global__ __launch_bounds__(256) void gdn_ring_kernel(GdnPrefillArgs a) {
     }
 }
 
+// v_mfma_f32_16x16x4_f32, one block: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
+// result register v of lane l is D[4 (l / 16) + v][l % 16].
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 // ------------------------------------------------------------------ GDN chunk
-// grid (VH, Tp / 64), 256 threads.
+// grid (VH, Tp / 64), 256 threads. P and A on the fp32 matrix cores (K and Q rows padded to
+// 132 floats: the 16 rows x 4 dims of an operand read fall in 64 distinct banks).
+constexpr int kLdC = kD + 4;
 __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int kh = vh / (a.VH / a.KH);
     const int64_t row0 = static_cast<int64_t>(c) * kC;
-    __shared__ float Ks[kC][kD + 1];
-    __shared__ float Qs[kC][kD + 1];
+    __shared__ __align__(16) float Ks[kC][kLdC];
+    __shared__ __align__(16) float Qs[kC][kLdC];
     __shared__ float As[kC][kC + 1];
     __shared__ float gam[kC], beta[kC];
     const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-    for (int i = tid; i < kC * kD; i += 256) {
-        Ks[i / kD][i % kD] = K[i];
-        Qs[i / kD][i % kD] = Q[i];
+    for (int f = tid; f < kC * kD / 4; f += 256) {
+        *reinterpret_cast<float4*>(&Ks[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(K + f * 4);
+        *reinterpret_cast<float4*>(&Qs[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
     }
     if (tid < kC) beta[tid] = a.Bg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
     if (tid == 0) {
@@ -174,28 +184,35 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
     }
     __syncthreads();
     if (tid < kC) a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid] = gam[tid];
-    // P (j <= i) and A (j < i); thread: row i = tid / 4, columns j = (tid % 4) * 16 + u
+    // P (j <= i) and A (j < i): S = Q K^T and KK = K K^T over the 128 dims; wave w owns rows
+    // [16 w, 16 w + 16) and the 4 blocks of 16 columns; lane (lr, lg) ends with rows
+    // 16 w + 4 lg + v of column 16 b + lr
     {
-        const int i = tid >> 2, jb = (tid & 3) * 16;
-        float kk[16], qk[16];
+        const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+        floatx4 sq[4], sk[4];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) kk[u] = qk[u] = 0.0f;
-        for (int d = 0; d < kD; ++d) {
-            const float ki = Ks[i][d], qi = Qs[i][d];
+        for (int b = 0; b < 4; ++b) sq[b] = sk[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int k = 0; k < kD; k += 4) {
+            const float aq = Qs[16 * wave + lr][k + lg], ak = Ks[16 * wave + lr][k + lg];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float kj = Ks[jb + u][d];
-                kk[u] = fmaf(ki, kj, kk[u]);
-                qk[u] = fmaf(qi, kj, qk[u]);
+            for (int b = 0; b < 4; ++b) {
+                const float bk = Ks[16 * b + lr][k + lg];
+                sq[b] = mfma4(aq, bk, sq[b]);
+                sk[b] = mfma4(ak, bk, sk[b]);
             }
         }
-        float* P = a.P + ((static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kC + i) * kC;
+        float* P = a.P + (static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kC * kC;
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int j = jb + u;
-            const float dec = j <= i ? expf(gam[i] - gam[j]) : 0.0f;
-            P[j] = j <= i ? qk[u] * dec : 0.0f;
-            As[i][j] = j < i ? beta[i] * kk[u] * dec : 0.0f;
+        for (int v = 0; v < 4; ++v) {
+            const int i = 16 * wave + 4 * lg + v;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = 16 * b + lr;
+                const float dec = j <= i ? expf(gam[i] - gam[j]) : 0.0f;
+                P[i * kC + j] = j <= i ? sq[b][v] * dec : 0.0f;
+                As[i][j] = j < i ? beta[i] * sk[b][v] * dec : 0.0f;
+            }
         }
     }
     __syncthreads();
@@ -222,14 +239,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
 }
 
 // ------------------------------------------------------------------ GDN state scan
-// v_mfma_f32_16x16x4_f32, one block: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16];
-// result register v of lane l is D[4 (l / 16) + v][l % 16].
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 constexpr int kSW = 16;        // state columns per state-scan workgroup
 constexpr int kLdW = kD + 4;   // -W rows in LDS (A operand: 16 rows x 4 k per read, conflict-free)
 constexpr int kLdK = kD + 16;  // decayed K rows in LDS (A operand read transposed)
