@@ -158,15 +158,18 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 
 // ------------------------------------------------------------------ GDN chunk
 // grid (VH, Tp / 64), 256 threads. P and A on the fp32 matrix cores (K and Q rows padded to
-// 132 floats: the 16 rows x 4 dims of an operand read fall in 64 distinct banks).
+// 132 floats: the 16 rows x 4 dims of an operand read fall in 64 distinct banks). A takes
+// the place of Q in LDS once the products are done (68 KB in all: two workgroups per CU).
 constexpr int kLdC = kD + 4;
-__global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
+constexpr int kLdA = kC + 4;  // A rows: 16-byte aligned, read four entries at a time
+__global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int kh = vh / (a.VH / a.KH);
     const int64_t row0 = static_cast<int64_t>(c) * kC;
     __shared__ __align__(16) float Ks[kC][kLdC];
-    __shared__ __align__(16) float Qs[kC][kLdC];
-    __shared__ float As[kC][kC + 1];
+    __shared__ __align__(16) float QA[kC * kLdC];
+    float (*Qs)[kLdC] = reinterpret_cast<float (*)[kLdC]>(QA);
+    float (*As)[kLdA] = reinterpret_cast<float (*)[kLdA]>(QA);
     __shared__ float gam[kC], beta[kC];
     const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
@@ -202,6 +205,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnPrefillArgs a) {
                 sk[b] = mfma4(ak, bk, sk[b]);
             }
         }
+        lds_barrier();  // every wave is done reading Q: A takes its place
         float* P = a.P + (static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kC * kC;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
