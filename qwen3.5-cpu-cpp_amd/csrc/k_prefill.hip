@@ -247,29 +247,34 @@ constexpr int kSW = 16;        // state columns per state-scan workgroup
 constexpr int kLdW = kD + 4;   // -W rows in LDS (A operand: 16 rows x 4 k per read, conflict-free)
 constexpr int kLdK = kD + 16;  // decayed K rows in LDS (A operand read transposed)
 
-// grid (VH, 128 / kSW), 256 threads: sequential over the chunks of one state column slice.
+// grid (VH, 128 / kSW), 512 threads: sequential over the chunks of one state column slice.
 // Per chunk: store the chunk-start state, v_new = U - W S (written over U), then
-// S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Wave w computes v_new rows
-// [16w, 16w + 16) and the new state rows [32w, 32w + 32). The next chunk's W and K are
-// loaded into registers while the current one is computed.
-__global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
+// S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Eight waves: v_new rows
+// [16 (w % 4), + 16) over the dims [64 (w / 4), + 64) (the two halves meet through LDS), and
+// the new state rows [16 w, 16 w + 16). The next chunk's W and K are loaded into registers
+// while the current one is computed.
+constexpr int kSThreads = 512;
+__global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int vb = wave & 3, kq = wave >> 2;  // v_new row block and dim half of this wave
     const int kh = vh / (a.VH / a.KH);
     const int col0 = cs * kSW;
     const int nchunk = a.Tp / kC;
     __shared__ float Ss[kD][kSW];
     __shared__ float VN[kC][kSW];
+    __shared__ float VP[kC][kSW];  // partial v_new of the upper dim half
     __shared__ float Wl[kC][kLdW];
     __shared__ float Kl[kC][kLdK];
     float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
-    for (int i = tid; i < kD * kSW; i += 256) Ss[i / kSW][i % kSW] = S[(i / kSW) * kD + col0 + i % kSW];
+    for (int i = tid; i < kD * kSW; i += kSThreads) Ss[i / kSW][i % kSW] = S[(i / kSW) * kD + col0 + i % kSW];
 
-    // staging map: float4 f = tid + 256 i (i < 8) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32).
+    // staging map: float4 f = tid + 512 i (i < 4) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32).
     // Everything a chunk step reads from global memory (W, K, the cumulative decays and this
     // lane's U entries) is requested one chunk ahead, so the sequential chain only waits on LDS.
-    float4 rw[8], rk[8];
-    float rgam[8], rglast, ru[4];
+    constexpr int NF = kC * kD / 4 / kSThreads;
+    float4 rw[NF], rk[NF];
+    float rgam[NF], rglast, ru[4];
     auto load_chunk = [&](int c) {
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
@@ -277,21 +282,21 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
         const float* gam = a.Gam + static_cast<int64_t>(vh) * a.Tp + row0;
         const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int f = tid + 256 * i;
+        for (int i = 0; i < NF; ++i) {
+            const int f = tid + kSThreads * i;
             rw[i] = *reinterpret_cast<const float4*>(W + (f >> 5) * kD + (f & 31) * 4);
             rk[i] = *reinterpret_cast<const float4*>(K + (f >> 5) * kD + (f & 31) * 4);
             rgam[i] = gam[f >> 5];
         }
         rglast = gam[kC - 1];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * wave + 4 * lg + v) * kD + lr];
+        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * vb + 4 * lg + v) * kD + lr];
     };
     auto store_chunk = [&]() {
         const float glast = rglast;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int f = tid + 256 * i, r = f >> 5, c4 = (f & 31) * 4;
+        for (int i = 0; i < NF; ++i) {
+            const int f = tid + kSThreads * i, r = f >> 5, c4 = (f & 31) * 4;
             const float d = expf(glast - rgam[i]);
             Wl[r][c4 + 0] = -rw[i].x;
             Wl[r][c4 + 1] = -rw[i].y;
@@ -317,49 +322,52 @@ __global__ __launch_bounds__(256) void gdn_state_kernel(GdnPrefillArgs a) {
         for (int v = 0; v < 4; ++v) vn[v] = ru[v];
         // chunk-start state for the output pass
         float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
-        for (int i = tid; i < kD * kSW; i += 256) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
+        for (int i = tid; i < kD * kSW; i += kSThreads) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
         lds_barrier();
         load_chunk(min(c + 1, nchunk - 1));  // unconditional (the last chunk is requested twice)
 
-        // v_new rows [16w, 16w + 16) = U - W S
-        float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
+        // v_new rows [16 vb, 16 vb + 16) = U - W S, dims [64 kq, 64 kq + 64) in this wave
+        floatx4 part;
         {  // four independent accumulation chains (k-steps interleaved), summed in a fixed order
             floatx4 ch[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) ch[q] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int k = 0; k < kD; k += 4) ch[(k >> 2) & 3] = mfma4(Wl[16 * wave + lr][k + lg], Ss[k + lg][lr], ch[(k >> 2) & 3]);
-            vn = vn + ((ch[0] + ch[1]) + (ch[2] + ch[3]));
+            for (int k = 64 * kq; k < 64 * kq + 64; k += 4)
+                ch[(k >> 2) & 3] = mfma4(Wl[16 * vb + lr][k + lg], Ss[k + lg][lr], ch[(k >> 2) & 3]);
+            part = (ch[0] + ch[1]) + (ch[2] + ch[3]);
         }
+        if (kq == 1)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            U[(16 * wave + 4 * lg + v) * kD + lr] = vn[v];
-            VN[16 * wave + 4 * lg + v][lr] = vn[v];
+            for (int v = 0; v < 4; ++v) VP[16 * vb + 4 * lg + v][lr] = part[v];
+        lds_barrier();
+        if (kq == 0) {
+            float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float x = vn[v] + (part[v] + VP[16 * vb + 4 * lg + v][lr]);
+                U[(16 * vb + 4 * lg + v) * kD + lr] = x;
+                VN[16 * vb + 4 * lg + v][lr] = x;
+            }
         }
         lds_barrier();  // VN complete, every wave done reading Ss
 
-        // new state rows [32w, 32w + 32), one 16-row block at a time. Each block is written
-        // back right after its product: with both blocks' eight stores in one basic block this
-        // compiler paired two of them into a ds_write2_b32 with a wrong offset (the state of
-        // row 16 landed in row 3).
+        // new state rows [16 w, 16 w + 16)
         const float dl = expf(glast);
+        float* srow = &Ss[16 * wave + 4 * lg][lr];
+        floatx4 sn;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            float* srow = &Ss[32 * wave + 16 * rb + 4 * lg][lr];
-            floatx4 sn;
+        for (int v = 0; v < 4; ++v) sn[v] = srow[v * kSW] * dl;
+        floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int v = 0; v < 4; ++v) sn[v] = srow[v * kSW] * dl;
-            floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+        for (int t = 0; t < kC; t += 4)
+            ch[(t >> 2) & 1] = mfma4(Kl[t + lg][16 * wave + lr], VN[t + lg][lr], ch[(t >> 2) & 1]);
+        sn = sn + (ch[0] + ch[1]);
 #pragma unroll
-            for (int t = 0; t < kC; t += 4)
-                ch[(t >> 2) & 1] = mfma4(Kl[t + lg][32 * wave + 16 * rb + lr], VN[t + lg][lr], ch[(t >> 2) & 1]);
-            sn = sn + (ch[0] + ch[1]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) srow[v * kSW] = sn[v];
-        }
+        for (int v = 0; v < 4; ++v) srow[v * kSW] = sn[v];
     }
     __syncthreads();
-    for (int i = tid; i < kD * kSW; i += 256) S[(i / kSW) * kD + col0 + i % kSW] = Ss[i / kSW][i % kSW];
+    for (int i = tid; i < kD * kSW; i += kSThreads) S[(i / kSW) * kD + col0 + i % kSW] = Ss[i / kSW][i % kSW];
 }
 
 // ------------------------------------------------------------------ GDN chunk output
@@ -831,7 +839,7 @@ hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
     if (a.Tp > a.T) klaunch(gdn_pad_kernel, blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s, a);
     klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
     klaunch(gdn_chunk_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
-    klaunch(gdn_state_kernel, dim3(a.VH, kD / kSW), 256, 0, s, a);
+    klaunch(gdn_state_kernel, dim3(a.VH, kD / kSW), kSThreads, 0, s, a);
     klaunch(gdn_out_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
     return hipGetLastError();
 }
