@@ -46,7 +46,8 @@ def gdn_dims(kh, vh):
     (16, 16, 2, 512, False),   # the isolated-GDN shape, 512 steps (state bar after 512 steps)
     (16, 16, 3, 24, True),     # gated norm fused in the kernel (one workgroup per head)
     (8, 16, 2, 40, False),     # v-heads = 2 k-heads: q/k shared by two v-heads
-    (16, 16, 18, 24, False),   # 18 layers per launch (1152 workgroups)
+    (16, 16, 18, 24, False),   # 18 layers per launch: 64-column slices (576 workgroups)
+    (8, 16, 16, 16, False),    # 64-column slices with q/k shared by two v-heads
 ])
 def test_gdn_decode_vs_oracle(hip, kh, vh, layers, steps, fused):
     rng = np.random.default_rng(100 + kh + vh + steps)
