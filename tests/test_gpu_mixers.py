@@ -183,10 +183,14 @@ def test_attn_decode_split_invariance(hip, n_splits):
     assert rel_l2(out, ref) < REL_L2
 
 
-def test_attn_decode_layer_batch(hip):
-    """Three independent layers in one launch (grid.z) equal three oracle calls."""
+@pytest.mark.parametrize("L,nq,nkv,pos,maxc", [
+    (3, 8, 2, 700, 800),      # vector-ALU kernel (GQA 4)
+    (6, 16, 2, 8200, 8300),   # matrix-core kernel, 6 layers at 8k: two workgroups per CU (42 splits)
+])
+def test_attn_decode_layer_batch(hip, L, nq, nkv, pos, maxc):
+    """Independent layers in one launch (grid.z) equal one oracle call per layer."""
     rng = np.random.default_rng(5)
-    L, nq, nkv, HD, pos, maxc = 3, 8, 2, 256, 700, 800
+    HD = 256
     d = attn_dims(nq, nkv)
     qg = rng.standard_normal((L, 2 * nq * HD)).astype(np.float32)
     kn = rng.standard_normal((L, nkv * HD)).astype(np.float32)
