@@ -9,8 +9,9 @@
 // significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul with
 // fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one fp32 MFMA.
 //
-// Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
-// of it: 1 x 4 MFMA blocks of 32 x 32 (64 accumulator registers per lane). K advances in
+// Tiling: 128 x BN output tile per 256-thread workgroup (BN = 128, or 256 for the widest
+// projection), each of the 4 waves a 32-row slab of it: 1 x BN / 32 MFMA blocks of 32 x 32
+// (64 or 128 accumulator registers per lane). K advances in
 // stages of 32: the X and W tiles of the next stage are loaded into registers while the
 // current stage runs from LDS (branch-free loads, LDS-only barriers, so the loads stay in
 // flight until the next stage's LDS store needs them). LDS holds the X tile as fp32
@@ -35,7 +36,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kBM = 128, kBK = 32;
 constexpr int kLdX = kBK + 4;  // padded X row (floats): 144 B, 16-byte reads of 8 rows hit distinct banks
 constexpr int kLd = kBK + 8;   // padded W row (bf16 elements): 80 B
 
@@ -50,20 +51,24 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint3
     l = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xffff0000u);
 }
 
-// EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+// EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs.
+// BN: tile width, 128 (4 MFMA blocks per wave) or 256 (8 blocks, two waves per SIMD).
+template <int EPI, int BN>
+__global__ __launch_bounds__(256, BN == 256 ? 2 : 1) void gemm_kernel(GemmArgs a) {
+    constexpr int kBN = BN, kNB = BN / 32;  // 32-column MFMA blocks per wave
     __shared__ __align__(16) float Xs[kBM][kLdX];
     __shared__ __align__(16) uint16_t Ws[kBN][kLd];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
 
-    // global -> register mapping: thread t loads row t / 2, k half (t % 2) of the stage
-    constexpr int NXQ = kBK / 8, NWQ = kBK / 16;  // 16-byte X / W chunks per thread and stage
+    // global -> register mapping: thread t loads X row t / 2, k half (t % 2), and W row
+    // t * BN / 256 .. of the stage: k half (t % 2) for BN = 128, all of it for BN = 256
+    constexpr int NXQ = kBK / 8, NWQ = kBK * BN / (8 * 256);  // 16-byte X / W chunks per thread and stage
     const int lr = tid >> 1, lk = (tid & 1) * (kBK / 2);
-    const bool a_ok = m0 + lr < a.M, b_ok = n0 + lr < a.N;
+    const int wr = BN == 256 ? tid : lr, wk = BN == 256 ? 0 : lk;
+    const bool a_ok = m0 + lr < a.M, b_ok = n0 + wr < a.N;
     const float* xrow = a.X + static_cast<int64_t>(a_ok ? m0 + lr : 0) * a.ldx;
-    const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + lr : 0) * a.K;
+    const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + wr : 0) * a.K;
     // The next stage's X / W tiles are requested into registers right after the current
     // stage is in LDS and stay in flight while it is multiplied. Loads are unconditional
     // (clamped to element K - 8 of a valid row); chunks past K or past the last row are
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         for (int i = 0; i < NXQ; ++i)
             ra[i] = *reinterpret_cast<const uint4*>(xrow + min(k0 + lk + 4 * i, a.K - 4));
 #pragma unroll
-        for (int i = 0; i < NWQ; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + lk + 8 * i, a.K - 8));
+        for (int i = 0; i < NWQ; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + wk + 8 * i, a.K - 8));
     };
     auto masked = [](uint4 v, bool live) {
         const uint32_t m = 0u - static_cast<uint32_t>(live);
@@ -89,12 +94,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             *reinterpret_cast<uint4*>(&Xs[lr][lk + 4 * i]) = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
 #pragma unroll
         for (int q = 0; q < NWQ; ++q)
-            *reinterpret_cast<uint4*>(&Ws[lr][lk + 8 * q]) = masked(rw[q], b_ok && k0 + lk + 8 * q < a.K);
+            *reinterpret_cast<uint4*>(&Ws[wr][wk + 8 * q]) = masked(rw[q], b_ok && k0 + wk + 8 * q < a.K);
     };
 
-    floatx16 acc[4];
+    floatx16 acc[kNB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kNB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
@@ -105,9 +110,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
             const int kk = s * 16 + kh;
             const float4 x0 = *reinterpret_cast<const float4*>(&Xs[ar][kk]);
             const float4 x1 = *reinterpret_cast<const float4*>(&Xs[ar][kk + 4]);
-            bf16x8 bop[4];
+            bf16x8 bop[kNB];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bop[j] = *reinterpret_cast<const bf16x8*>(&Ws[br + 32 * j][kk]);
+            for (int j = 0; j < kNB; ++j) bop[j] = *reinterpret_cast<const bf16x8*>(&Ws[br + 32 * j][kk]);
             uint32_t h[4], m[4], l[4];
             split3_pair(x0.x, x0.y, h[0], m[0], l[0]);
             split3_pair(x0.z, x0.w, h[1], m[1], l[1]);
@@ -119,7 +124,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int p = 2; p >= 0; --p)  // lo, mid, hi
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < kNB; ++j)
                     acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop[p], bop[j], acc[j], 0, 0, 0);
         }
     };
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     if constexpr (EPI == 2) {
         // the pair (gate, up) of one output sits in adjacent lanes (even, odd column)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kNB; ++j) {
             const int col = n0 + j * 32 + (lane & 31);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         return;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kNB; ++j) {
         const int col = n0 + j * 32 + (lane & 31);
         if (col >= a.N) continue;
 #pragma unroll
@@ -163,13 +168,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     }
 }
 
+template <int BN>
+void launch_bn(const GemmArgs& a, hipStream_t s) {
+    dim3 grid((a.N + BN - 1) / BN, (a.M + kBM - 1) / kBM);
+    if (a.swiglu) klaunch(gemm_kernel<2, BN>, grid, 256, 0, s, a);
+    else if (a.R) klaunch(gemm_kernel<1, BN>, grid, 256, 0, s, a);
+    else klaunch(gemm_kernel<0, BN>, grid, 256, 0, s, a);
+}
+
 }  // namespace
 
+// 256-wide tiles for the widest projections (the interleaved gate/up: 7% faster at 4096 x
+// 12288 x 2048), 128-wide for the rest, where 256-wide tiles leave too few workgroups.
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-    dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
-    if (a.swiglu) klaunch(gemm_kernel<2>, grid, 256, 0, s, a);
-    else if (a.R) klaunch(gemm_kernel<1>, grid, 256, 0, s, a);
-    else klaunch(gemm_kernel<0>, grid, 256, 0, s, a);
+    if (a.N >= 12288) launch_bn<256>(a, s);
+    else launch_bn<128>(a, s);
     return hipGetLastError();
 }
 
