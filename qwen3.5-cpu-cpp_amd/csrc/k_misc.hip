@@ -32,6 +32,44 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
     }
 }
 
+// The same for rows of n = 256 NV4 floats, one row per wave: the row stays in registers
+// between the sum of squares (double, reduced across the wave) and the scaling, so it is
+// read once, and no block barrier is needed.
+template <int NV4>
+__global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const float* w, float* y,
+                                                                int rows, float eps, int gated,
+                                                                const float* gate) {
+    constexpr int n = NV4 * 256;
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // whole waves
+    const int64_t off = static_cast<int64_t>(row) * n;
+    float4 v[NV4];
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) v[i] = *reinterpret_cast<const float4*>(x + off + (64 * i + lane) * 4);
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < NV4; ++i)
+        ss += static_cast<double>(v[i].x) * v[i].x + static_cast<double>(v[i].y) * v[i].y +
+              static_cast<double>(v[i].z) * v[i].z + static_cast<double>(v[i].w) * v[i].w;
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + eps);
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {
+        const int c = (64 * i + lane) * 4;
+        const float4 w4 = *reinterpret_cast<const float4*>(w + c);
+        float4 o;
+        if (gated) {
+            const float4 g4 = *reinterpret_cast<const float4*>(gate + off + c);
+            o = make_float4(w4.x * (v[i].x * inv) * silu_f(g4.x), w4.y * (v[i].y * inv) * silu_f(g4.y),
+                            w4.z * (v[i].z * inv) * silu_f(g4.z), w4.w * (v[i].w * inv) * silu_f(g4.w));
+        } else {
+            o = make_float4(v[i].x * inv * (1.0f + w4.x), v[i].y * inv * (1.0f + w4.y), v[i].z * inv * (1.0f + w4.z),
+                            v[i].w * inv * (1.0f + w4.w));
+        }
+        *reinterpret_cast<float4*>(y + off + c) = o;
+    }
+}
+
 // x *= 1 / sqrt(sum(x^2) + eps), in place, one block per row.
 __global__ __launch_bounds__(256) void l2norm_rows_kernel(float* x, int n, float eps) {
     __shared__ double red[4];
@@ -185,7 +223,13 @@ int grid_for(int64_t n) {
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
                                float eps, int gated, const float* gate, hipStream_t s) {
-    klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                         reinterpret_cast<uintptr_t>(y) | (gated ? reinterpret_cast<uintptr_t>(gate) : 0);
+    const int wb = (rows + 3) / 4;
+    if ((al & 15) == 0 && n == 1024) klaunch(rmsnorm_rows_wave_kernel<4>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
+    else if ((al & 15) == 0 && n == 2048) klaunch(rmsnorm_rows_wave_kernel<8>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
+    else if ((al & 15) == 0 && n == 4096) klaunch(rmsnorm_rows_wave_kernel<16>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
+    else klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate);
     return hipGetLastError();
 }
 

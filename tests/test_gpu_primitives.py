@@ -34,7 +34,7 @@ def test_matmul_bf16(hip, rows, cols):
     np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
 
 
-@pytest.mark.parametrize("rows,n", [(1, 256), (8, 1024), (3, 2048), (2, 100)])
+@pytest.mark.parametrize("rows,n", [(1, 256), (8, 1024), (3, 2048), (5, 4096), (2, 100)])
 def test_rmsnorm_and_gated(hip, rows, n):
     eps = 1e-6
     x = rng.standard_normal((rows, n)).astype(np.float32)
