@@ -386,8 +386,12 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const int kh = vh / (a.VH / a.KH);
     const int nchunk = a.Tp / kC;
     const int64_t row0 = static_cast<int64_t>(c) * kC;
-    __shared__ float A_s[kC][kLdQ];   // Q, then P
-    __shared__ float B_s[kC][kLdS];   // S_c rows [0, 64), then [64, 128), then v_new
+    // Operand order: within each 16-deep block of the product, MFMA step j takes from lane
+    // group lg the index 4 lg + j, so a lane's four A values of the block are one 16-byte
+    // read of its row; B rows are stored with their columns permuted (column 16 b + r at
+    // 8 r + b), so a lane's eight column blocks of one B row are two 16-byte reads.
+    __shared__ __align__(16) float A_s[kC][kLdQ];   // Q, then P
+    __shared__ __align__(16) float B_s[kC][kLdS];   // S_c rows [0, 64), then [64, 128), then v_new
     __shared__ float gam[kC];
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD;
@@ -395,42 +399,55 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const float* Vn = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
     constexpr int NQ4 = kC * kD / 4 / 256;  // float4 per thread of a 64 x 128 tile (8)
     constexpr int NP4 = kC * kC / 4 / 256;  // of the 64 x 64 P tile (4)
+    auto put_b = [&](int f, float4 v) {  // float4 f of a row-major 64 x 128 tile -> B_s, permuted
+        const int r = f >> 5, c0 = (f & 31) * 4;
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) B_s[r][((c0 + i) & 15) * 8 + ((c0 + i) >> 4)] = e[i];
+    };
+    floatx4 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // acc += A[rows 16 w ..][acol .. acol + 15] . B[brow .. brow + 15][all 128 columns]
+    auto mma16 = [&](int acol, int brow) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&A_s[16 * wave + lr][acol + 4 * lg]);
+        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4* bp = reinterpret_cast<const float4*>(&B_s[brow + 4 * lg + j][lr * 8]);
+            const float4 b0 = bp[0], b1 = bp[1];
+            acc[0] = mfma4(av[j], b0.x, acc[0]);
+            acc[1] = mfma4(av[j], b0.y, acc[1]);
+            acc[2] = mfma4(av[j], b0.z, acc[2]);
+            acc[3] = mfma4(av[j], b0.w, acc[3]);
+            acc[4] = mfma4(av[j], b1.x, acc[4]);
+            acc[5] = mfma4(av[j], b1.y, acc[5]);
+            acc[6] = mfma4(av[j], b1.z, acc[6]);
+            acc[7] = mfma4(av[j], b1.w, acc[7]);
+        }
+    };
     for (int f = tid; f < kC * kD / 4; f += 256) {
         *reinterpret_cast<float4*>(&A_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
-        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Sc + f * 4);
+        put_b(f, *reinterpret_cast<const float4*>(Sc + f * 4));
     }
     if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
     __syncthreads();
     float4 rs[NQ4];  // S_c rows [64, 128)
 #pragma unroll
     for (int i = 0; i < NQ4; ++i) rs[i] = *reinterpret_cast<const float4*>(Sc + kC * kD + (tid + 256 * i) * 4);
-    floatx4 acc[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int k = 0; k < kC; k += 4) {
-        const float av = A_s[16 * wave + lr][k + lg];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
-    }
+    for (int blk = 0; blk < kC / 16; ++blk) mma16(16 * blk, 16 * blk);
     lds_barrier();  // done with S_c[0:64)
 #pragma unroll
-    for (int i = 0; i < NQ4; ++i) {
-        const int f = tid + 256 * i;
-        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = rs[i];
-    }
+    for (int i = 0; i < NQ4; ++i) put_b(tid + 256 * i, rs[i]);
     lds_barrier();
     float4 rp[NP4], rv[NQ4];
 #pragma unroll
     for (int i = 0; i < NP4; ++i) rp[i] = *reinterpret_cast<const float4*>(P + (tid + 256 * i) * 4);
 #pragma unroll
     for (int i = 0; i < NQ4; ++i) rv[i] = *reinterpret_cast<const float4*>(Vn + (tid + 256 * i) * 4);
-#pragma unroll 4
-    for (int k = 0; k < kC; k += 4) {
-        const float av = A_s[16 * wave + lr][kC + k + lg];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
-    }
+    for (int blk = 0; blk < kC / 16; ++blk) mma16(kC + 16 * blk, 16 * blk);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const float e = expf(gam[16 * wave + 4 * lg + v]);
@@ -444,17 +461,10 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
         *reinterpret_cast<float4*>(&A_s[f >> 4][(f & 15) * 4]) = rp[i];
     }
 #pragma unroll
-    for (int i = 0; i < NQ4; ++i) {
-        const int f = tid + 256 * i;
-        *reinterpret_cast<float4*>(&B_s[f >> 5][(f & 31) * 4]) = rv[i];
-    }
+    for (int i = 0; i < NQ4; ++i) put_b(tid + 256 * i, rv[i]);
     lds_barrier();
     // P is lower triangular: the row block of wave w needs columns j < 16 (w + 1)
-    for (int k = 0; k < 16 * (wave + 1); k += 4) {
-        const float av = A_s[16 * wave + lr][k + lg];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) acc[b] = mfma4(av, B_s[k + lg][16 * b + lr], acc[b]);
-    }
+    for (int blk = 0; blk <= wave; ++blk) mma16(16 * blk, 16 * blk);
     // epilogue: rows 16w + 4 lg + v, columns 16 b + lr
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
