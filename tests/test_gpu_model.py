@@ -236,3 +236,22 @@ def test_cpp_cli_generate(model_dirs):
     assert out.returncode == 0, out.stderr[-2000:]
     got = [int(x) for x in out.stdout.strip().split(",")]
     assert got == g["greedy"].tolist()
+
+
+def test_prefill_wide_ffn_matches_decode(tmp_path):
+    """A gate/up projection 12288 wide takes the 128 x 256 GEMM tiles (with the SwiGLU
+    epilogue) and a 200-token prompt is a ragged row count: the prefill logits equal the
+    token-by-token decode logits (the matvec path, itself checked against the oracle)."""
+    d = pyq35.default_dims(hidden_size=256, n_layers_total=4, gdn_k_heads=2, gdn_v_heads=2,
+                           attn_q_heads=2, attn_kv_heads=1, ffn_intermediate=6144,
+                           vocab_size=1024, native_max_context=4096)
+    path = str(tmp_path / "wide")
+    pyq35.synth_write_model(path, d, seed=3, std=0.02)
+    prompt = pyq35.synth_token_ids(5, d.vocab_size, 200)
+    m = pyq35.Model(path, 256)
+    lg = m.prefill(prompt)
+    m.close()
+    m = pyq35.Model(path, 256)
+    ref = np.stack([m.step(int(t))[0] for t in prompt])
+    m.close()
+    assert rel_l2(lg, ref) < REL_L2

@@ -40,7 +40,8 @@ class Bufs:
 # ----------------------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("M,N,K,ldx,resid", [
     (1, 8, 32, 32, False), (130, 70, 64, 68, True), (257, 300, 520, 520, False),
-    (64, 129, 8, 8, True), (512, 2048, 2048, 2048, True), (1000, 8224, 1024, 1024, False)])
+    (64, 129, 8, 8, True), (512, 2048, 2048, 2048, True), (1000, 8224, 1024, 1024, False),
+    (300, 12290, 136, 136, True), (129, 12288, 64, 72, False)])  # the last two: 128 x 256 tiles
 def test_gemm_bf16(hip, M, N, K, ldx, resid):
     rng = np.random.default_rng(M * 7 + N + K)
     X = rng.standard_normal((M, ldx)).astype(np.float32)
