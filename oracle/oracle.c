@@ -21,6 +21,7 @@
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
+#include <immintrin.h>
 #include <unistd.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -62,26 +63,29 @@ static inline float bf16f(uint16_t h) {
 /* blocks, one eight-lane accumulator over the following 8-wide blocks, the (lo+hi),    */
 /* hadd, hadd horizontal sum, then a scalar tail.                                       */
 /* ---------------------------------------------------------------------------------- */
+/* Eight weights as fp32: bf16 widened exactly (<< 16), or fp32 as stored */
+static inline __m256 w8(const uint16_t *wb, const float *wf, int i) {
+    if (!wb) return _mm256_loadu_ps(wf + i);
+    const __m256i h = _mm256_cvtepu16_epi32(_mm_loadu_si128((const __m128i *)(wb + i)));
+    return _mm256_castsi256_ps(_mm256_slli_epi32(h, 16));
+}
+
 static float dot_w(const uint16_t *wb, const float *wf, const float *x, int n) {
-    float a[4][8];
-    memset(a, 0, sizeof a);
+    __m256 a0 = _mm256_setzero_ps(), a1 = a0, a2 = a0, a3 = a0;
     int i = 0;
-    for (; i + 32 <= n; i += 32)
-        for (int b = 0; b < 4; ++b)
-            for (int l = 0; l < 8; ++l) {
-                int j = i + 8 * b + l;
-                float w = wb ? bf16f(wb[j]) : wf[j];
-                a[b][l] = fmaf(w, x[j], a[b][l]);
-            }
-    float acc[8];
-    for (int l = 0; l < 8; ++l) acc[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
-    for (; i + 8 <= n; i += 8)
-        for (int l = 0; l < 8; ++l) {
-            float w = wb ? bf16f(wb[i + l]) : wf[i + l];
-            acc[l] = fmaf(w, x[i + l], acc[l]);
-        }
-    float s0 = acc[0] + acc[4], s1 = acc[1] + acc[5], s2 = acc[2] + acc[6], s3 = acc[3] + acc[7];
-    float r = (s0 + s1) + (s2 + s3);
+    for (; i + 32 <= n; i += 32) {
+        a0 = _mm256_fmadd_ps(w8(wb, wf, i), _mm256_loadu_ps(x + i), a0);
+        a1 = _mm256_fmadd_ps(w8(wb, wf, i + 8), _mm256_loadu_ps(x + i + 8), a1);
+        a2 = _mm256_fmadd_ps(w8(wb, wf, i + 16), _mm256_loadu_ps(x + i + 16), a2);
+        a3 = _mm256_fmadd_ps(w8(wb, wf, i + 24), _mm256_loadu_ps(x + i + 24), a3);
+    }
+    __m256 acc = _mm256_add_ps(_mm256_add_ps(a0, a1), _mm256_add_ps(a2, a3));
+    for (; i + 8 <= n; i += 8) acc = _mm256_fmadd_ps(w8(wb, wf, i), _mm256_loadu_ps(x + i), acc);
+    /* lane l + lane l + 4, then ((s0 + s1) + (s2 + s3)) */
+    __m128 s = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+    s = _mm_hadd_ps(s, s);
+    s = _mm_hadd_ps(s, s);
+    float r = _mm_cvtss_f32(s);
     for (; i < n; ++i) r += (wb ? bf16f(wb[i]) : wf[i]) * x[i];
     return r;
 }
@@ -89,6 +93,21 @@ static float dot_w(const uint16_t *wb, const float *wf, const float *x, int n) {
 void orc_matmul_bf16(const uint16_t *W, const float *x, float *y, int out_dim, int in_dim) {
 #pragma omp parallel for schedule(static)
     for (int o = 0; o < out_dim; ++o) y[o] = dot_w(W + (size_t)o * in_dim, NULL, x, in_dim);
+}
+
+/* The matvec above for n input rows at once: Y[t][o] = dot(W[o], X[t]), every output with
+ * exactly the arithmetic of orc_matmul_bf16. Blocks of 64 input rows stay in cache while
+ * each weight row is applied to all of them, so a whole prompt streams the weights once
+ * per block instead of once per token. */
+void orc_matmul_bf16_rows(const uint16_t *W, const float *X, int64_t ldx, float *Y, int64_t ldy,
+                          int n, int out_dim, int in_dim) {
+    for (int t0 = 0; t0 < n; t0 += 64) {
+        const int t1 = t0 + 64 < n ? t0 + 64 : n;
+#pragma omp parallel for schedule(static)
+        for (int o = 0; o < out_dim; ++o)
+            for (int t = t0; t < t1; ++t)
+                Y[(size_t)t * ldy + o] = dot_w(W + (size_t)o * in_dim, NULL, X + (size_t)t * ldx, in_dim);
+    }
 }
 
 void orc_matmul_f32(const float *W, const float *x, float *y, int out_dim, int in_dim) {
@@ -779,9 +798,18 @@ struct orc_model {
     float *trace;
     int ok;
     int kv_bf16; /* 1: cache rows stored rounded to bf16 */
+    int handoff; /* 1: orc_prefill leaves its final state in the model (see below) */
 };
 
 void orc_set_kv_bf16(orc_model *m, int on) { m->kv_bf16 = on ? 1 : 0; }
+
+/* The reference's QwenForward::prefill discards the recurrent state it builds (it starts
+ * every call from S = 0, src/qwen_forward.cpp:129-142). With handoff on, orc_prefill keeps
+ * it instead, as n token-serial steps would leave it: each GDN layer's final state and conv
+ * window (the last KER - 1 pre-conv inputs, oldest first), each attention layer's K / V rows
+ * at positions 0 .. n - 1, the residual of the last token, position n. The logits and the
+ * per-layer hidden states are unchanged. */
+void orc_set_prefill_handoff(orc_model *m, int on) { m->handoff = on ? 1 : 0; }
 
 static const uint16_t *need_bf16(orc_model *m, const char *name) {
     const st_entry *e = st_find(&m->st, name);
@@ -1041,6 +1069,19 @@ static void ffn(const orc_model *m, const orc_layer *L, const float *x, float *o
     free(u);
 }
 
+/* The FFN block of n tokens at once (rows of H), each token as ffn() computes it */
+static void ffn_rows(const orc_model *m, const orc_layer *L, const float *x, float *out, int n) {
+    const int H = m->d.hidden_size, I = m->d.ffn_intermediate;
+    float *g = (float *)malloc(sizeof(float) * (size_t)n * I);
+    float *u = (float *)malloc(sizeof(float) * (size_t)n * I);
+    orc_matmul_bf16_rows(L->gate, x, H, g, I, n, I, H);
+    orc_matmul_bf16_rows(L->up, x, H, u, I, n, I, H);
+    for (size_t i = 0; i < (size_t)n * I; ++i) g[i] = orc_silu(g[i]) * u[i];
+    orc_matmul_bf16_rows(L->down, g, I, out, H, n, H, I);
+    free(g);
+    free(u);
+}
+
 /* QwenModel::step, src/qwen_model.cpp:211-239 */
 int orc_step(orc_model *m, int token, float *logits) {
     const orc_dims *d = &m->d;
@@ -1100,11 +1141,14 @@ static void prefill_attention(orc_model *m, const orc_layer *L, const float *in,
     float *Kc = (float *)malloc(sizeof(float) * (size_t)seq * NKV * HD);
     float *Vc = (float *)malloc(sizeof(float) * (size_t)seq * NKV * HD);
     float *gt = (float *)malloc(sizeof(float) * (size_t)seq * NQ * HD);
-    float *qkv = (float *)malloc(sizeof(float) * (size_t)NQ * HD * 2);
-    float *kv = (float *)malloc(sizeof(float) * (size_t)NKV * HD);
+    /* q_proj / k_proj / v_proj of every token (each output a reference matvec) */
+    float *qkv_all = (float *)malloc(sizeof(float) * (size_t)seq * NQ * HD * 2);
+    float *kv_all = (float *)malloc(sizeof(float) * (size_t)seq * NKV * HD);
+    orc_matmul_bf16_rows(L->q, in, H, qkv_all, (int64_t)NQ * HD * 2, seq, NQ * HD * 2, H);
+    orc_matmul_bf16_rows(L->k, in, H, kv_all, (int64_t)NKV * HD, seq, NKV * HD, H);
+    orc_matmul_bf16_rows(L->v, in, H, Vc, (int64_t)NKV * HD, seq, NKV * HD, H);
     for (int t = 0; t < seq; ++t) {
-        const float *x = in + (size_t)t * H;
-        orc_matmul_bf16(L->q, x, qkv, NQ * HD * 2, H);
+        const float *qkv = qkv_all + (size_t)t * NQ * HD * 2, *kv = kv_all + (size_t)t * NKV * HD;
         for (int h = 0; h < NQ; ++h) {
             const float *qgp = qkv + (size_t)h * HD * 2;
             float *qd = Q + ((size_t)t * NQ + h) * HD;
@@ -1112,18 +1156,24 @@ static void prefill_attention(orc_model *m, const orc_layer *L, const float *in,
             orc_apply_rope(qd, ROT, t, d->rope_theta);
             memcpy(gt + ((size_t)t * NQ + h) * HD, qgp + HD, sizeof(float) * (size_t)HD);
         }
-        orc_matmul_bf16(L->k, x, kv, NKV * HD, H);
         for (int kh = 0; kh < NKV; ++kh) {
             float *kd = Kc + ((size_t)t * NKV + kh) * HD;
             orc_rmsnorm(kv + (size_t)kh * HD, L->k_norm, kd, HD, eps);
             orc_apply_rope(kd, ROT, t, d->rope_theta);
         }
-        orc_matmul_bf16(L->v, x, Vc + (size_t)t * NKV * HD, NKV * HD, H);
     }
-    float *ac = (float *)malloc(sizeof(float) * (size_t)NQ * HD);
-    float *sco = (float *)malloc(sizeof(float) * (size_t)seq);
+    /* The (token, query head) pairs are independent: they run in parallel, each with the
+     * reference's serial score / softmax / P.V loops in the reference's order. */
+    float *att = (float *)malloc(sizeof(float) * (size_t)seq * NQ * HD);
+    float *sco_all = (float *)malloc(sizeof(float) * (size_t)seq * orc_threads());
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
     for (int t = 0; t < seq; ++t) {
         for (int h = 0; h < NQ; ++h) {
+#ifdef _OPENMP
+            float *sco = sco_all + (size_t)omp_get_thread_num() * seq;
+#else
+            float *sco = sco_all;
+#endif
             const int kh = h / GRP;
             const float *q = Q + ((size_t)t * NQ + h) * HD;
             float mx = -1e30f;
@@ -1140,7 +1190,7 @@ static void prefill_attention(orc_model *m, const orc_layer *L, const float *in,
                 sco[j] = expf(sco[j] - mx);
                 sm += sco[j];
             }
-            float *oh = ac + (size_t)h * HD;
+            float *oh = att + ((size_t)t * NQ + h) * HD;
             for (int i = 0; i < HD; ++i) oh[i] = 0.0f;
             for (int j = 0; j <= t; ++j) {
                 const float p = sco[j] / sm;
@@ -1148,18 +1198,30 @@ static void prefill_attention(orc_model *m, const orc_layer *L, const float *in,
                 for (int i = 0; i < HD; ++i) oh[i] += p * v[i];
             }
         }
+    }
+    for (int t = 0; t < seq; ++t) {
+        float *ac = att + (size_t)t * NQ * HD;
         const float *g = gt + (size_t)t * NQ * HD;
         for (int i = 0; i < NQ * HD; ++i) ac[i] *= orc_sigmoid(g[i]);
-        orc_matmul_bf16(L->o, ac, out + (size_t)t * H, H, NQ * HD);
+    }
+    orc_matmul_bf16_rows(L->o, att, (int64_t)NQ * HD, out, H, seq, H, NQ * HD);
+    if (m->handoff) {
+        const size_t row = (size_t)NKV * HD;
+        memcpy(m->kc[L->idx], Kc, sizeof(float) * row * (size_t)seq);
+        memcpy(m->vc[L->idx], Vc, sizeof(float) * row * (size_t)seq);
+        if (m->kv_bf16) {
+            orc_round_bf16_array(m->kc[L->idx], (int64_t)(row * (size_t)seq));
+            orc_round_bf16_array(m->vc[L->idx], (int64_t)(row * (size_t)seq));
+        }
     }
     free(Q);
     free(Kc);
     free(Vc);
     free(gt);
-    free(qkv);
-    free(kv);
-    free(ac);
-    free(sco);
+    free(qkv_all);
+    free(kv_all);
+    free(att);
+    free(sco_all);
 }
 
 /* QwenForward::mix_gdn, src/qwen_forward.cpp:83-152 (needs KH == VH, DK == DV) */
@@ -1172,19 +1234,24 @@ static void prefill_gdn(orc_model *m, const orc_layer *L, const float *in, float
     float *zb = (float *)malloc(sizeof(float) * (size_t)seq * VD);
     float *beta = (float *)malloc(sizeof(float) * (size_t)seq * NH);
     float *g = (float *)malloc(sizeof(float) * (size_t)seq * NH);
-    float *bt = (float *)malloc(sizeof(float) * (size_t)NH);
-    float *at = (float *)malloc(sizeof(float) * (size_t)NH);
+    float *bt = (float *)malloc(sizeof(float) * (size_t)seq * NH);
+    float *at = (float *)malloc(sizeof(float) * (size_t)seq * NH);
+    orc_matmul_bf16_rows(L->in_qkv, in, H, qkv, CONV, seq, CONV, H);
+    orc_matmul_bf16_rows(L->in_z, in, H, zb, VD, seq, VD, H);
+    orc_matmul_bf16_rows(L->in_b, in, H, bt, NH, seq, NH, H);
+    orc_matmul_bf16_rows(L->in_a, in, H, at, NH, seq, NH, H);
     for (int t = 0; t < seq; ++t) {
-        const float *x = in + (size_t)t * H;
-        orc_matmul_bf16(L->in_qkv, x, qkv + (size_t)t * CONV, CONV, H);
-        orc_matmul_bf16(L->in_z, x, zb + (size_t)t * VD, VD, H);
-        orc_matmul_bf16(L->in_b, x, bt, NH, H);
-        orc_matmul_bf16(L->in_a, x, at, NH, H);
         for (int h = 0; h < NH; ++h) {
-            beta[(size_t)t * NH + h] = orc_sigmoid(bt[h]);
-            g[(size_t)t * NH + h] = -expf(L->A_log[h]) * orc_softplus(at[h] + L->dt_bias[h]);
+            beta[(size_t)t * NH + h] = orc_sigmoid(bt[(size_t)t * NH + h]);
+            g[(size_t)t * NH + h] = -expf(L->A_log[h]) * orc_softplus(at[(size_t)t * NH + h] + L->dt_bias[h]);
         }
     }
+    if (m->handoff) /* window [CONV][KER-1]: inputs of tokens seq-KER+1 .. seq-1, oldest first */
+        for (int c = 0; c < CONV; ++c)
+            for (int k = 0; k < KER - 1; ++k) {
+                const int s = seq - (KER - 1) + k;
+                m->cw[L->idx][(size_t)c * (KER - 1) + k] = s >= 0 ? qkv[(size_t)s * CONV + c] : 0.0f;
+            }
     float *conv = (float *)malloc(sizeof(float) * (size_t)seq * CONV);
     for (int c = 0; c < CONV; ++c) {
         const float *w4 = L->conv1d + (size_t)c * KER;
@@ -1215,43 +1282,53 @@ static void prefill_gdn(orc_model *m, const orc_layer *L, const float *in, float
             for (int i = 0; i < D; ++i) q[i] *= qs;
         }
     }
+    /* Heads are independent: each runs the reference's serial recurrence from S = 0, in the
+     * reference's order, on a thread of its own. */
     float *core = (float *)malloc(sizeof(float) * (size_t)seq * VD);
-    float *S = (float *)malloc(sizeof(float) * (size_t)D * D);
-    float *km = (float *)malloc(sizeof(float) * (size_t)D);
-    float *dl = (float *)malloc(sizeof(float) * (size_t)D);
-    for (int h = 0; h < NH; ++h) {
-        memset(S, 0, sizeof(float) * (size_t)D * D);
-        for (int t = 0; t < seq; ++t) {
-            const float gtt = expf(g[(size_t)t * NH + h]), b = beta[(size_t)t * NH + h];
-            const float *q = Q + ((size_t)t * NH + h) * D, *k = K + ((size_t)t * NH + h) * D,
-                        *v = V + ((size_t)t * NH + h) * D;
-            for (size_t i = 0; i < (size_t)D * D; ++i) S[i] *= gtt;
-            for (int vv = 0; vv < D; ++vv) {
-                float acc = 0.0f;
-                for (int kk = 0; kk < D; ++kk) acc += S[(size_t)kk * D + vv] * k[kk];
-                km[vv] = acc;
+#pragma omp parallel
+    {
+        float *S = (float *)malloc(sizeof(float) * (size_t)D * D);
+        float *km = (float *)malloc(sizeof(float) * (size_t)D);
+        float *dl = (float *)malloc(sizeof(float) * (size_t)D);
+#pragma omp for schedule(dynamic, 1)
+        for (int h = 0; h < NH; ++h) {
+            memset(S, 0, sizeof(float) * (size_t)D * D);
+            for (int t = 0; t < seq; ++t) {
+                const float gtt = expf(g[(size_t)t * NH + h]), b = beta[(size_t)t * NH + h];
+                const float *q = Q + ((size_t)t * NH + h) * D, *k = K + ((size_t)t * NH + h) * D,
+                            *v = V + ((size_t)t * NH + h) * D;
+                for (size_t i = 0; i < (size_t)D * D; ++i) S[i] *= gtt;
+                for (int vv = 0; vv < D; ++vv) {
+                    float acc = 0.0f;
+                    for (int kk = 0; kk < D; ++kk) acc += S[(size_t)kk * D + vv] * k[kk];
+                    km[vv] = acc;
+                }
+                for (int vv = 0; vv < D; ++vv) dl[vv] = (v[vv] - km[vv]) * b;
+                for (int kk = 0; kk < D; ++kk) {
+                    const float kv = k[kk];
+                    float *row = S + (size_t)kk * D;
+                    for (int vv = 0; vv < D; ++vv) row[vv] += kv * dl[vv];
+                }
+                float *o = core + ((size_t)t * NH + h) * D;
+                for (int vv = 0; vv < D; ++vv) {
+                    float acc = 0.0f;
+                    for (int kk = 0; kk < D; ++kk) acc += S[(size_t)kk * D + vv] * q[kk];
+                    o[vv] = acc;
+                }
             }
-            for (int vv = 0; vv < D; ++vv) dl[vv] = (v[vv] - km[vv]) * b;
-            for (int kk = 0; kk < D; ++kk) {
-                const float kv = k[kk];
-                float *row = S + (size_t)kk * D;
-                for (int vv = 0; vv < D; ++vv) row[vv] += kv * dl[vv];
-            }
-            float *o = core + ((size_t)t * NH + h) * D;
-            for (int vv = 0; vv < D; ++vv) {
-                float acc = 0.0f;
-                for (int kk = 0; kk < D; ++kk) acc += S[(size_t)kk * D + vv] * q[kk];
-                o[vv] = acc;
-            }
+            if (m->handoff)
+                memcpy(m->S[L->idx] + (size_t)h * D * D, S, sizeof(float) * (size_t)D * D);
         }
+        free(S);
+        free(km);
+        free(dl);
     }
-    float *gn = (float *)malloc(sizeof(float) * (size_t)VD);
-    for (int t = 0; t < seq; ++t) {
+    float *gn = (float *)malloc(sizeof(float) * (size_t)seq * VD);
+    for (int t = 0; t < seq; ++t)
         for (int h = 0; h < NH; ++h)
             orc_rmsnorm_gated(core + ((size_t)t * NH + h) * D, L->gdn_norm,
-                              zb + ((size_t)t * NH + h) * D, gn + (size_t)h * D, D, eps);
-        orc_matmul_bf16(L->out, gn, out + (size_t)t * H, H, VD);
-    }
+                              zb + ((size_t)t * NH + h) * D, gn + ((size_t)t * NH + h) * D, D, eps);
+    orc_matmul_bf16_rows(L->out, gn, VD, out, H, seq, H, VD);
     free(qkv);
     free(zb);
     free(beta);
@@ -1263,9 +1340,6 @@ static void prefill_gdn(orc_model *m, const orc_layer *L, const float *in, float
     free(K);
     free(V);
     free(core);
-    free(S);
-    free(km);
-    free(dl);
     free(gn);
 }
 
@@ -1276,6 +1350,10 @@ int orc_prefill(orc_model *m, const int *ids, int n, float *logits) {
     const float eps = d->rms_norm_eps;
     if (d->gdn_k_heads != d->gdn_v_heads || d->gdn_k_head_dim != d->gdn_v_head_dim) {
         set_err("prefill needs equal GDN key/value heads and dims");
+        return -1;
+    }
+    if (m->handoff && n > m->max_ctx) {
+        set_err("prefill of %d tokens exceeds max_context %d", n, m->max_ctx);
         return -1;
     }
     float *hidden = (float *)malloc(sizeof(float) * (size_t)n * H);
@@ -1300,11 +1378,9 @@ int orc_prefill(orc_model *m, const int *ids, int n, float *logits) {
         if (L->is_attn) prefill_attention(m, L, normed, mix, n);
         else prefill_gdn(m, L, normed, mix, n);
         for (size_t i = 0; i < (size_t)n * H; ++i) hidden[i] += mix[i];
-        for (int t = 0; t < n; ++t) {
+        for (int t = 0; t < n; ++t)
             orc_rmsnorm(hidden + (size_t)t * H, L->post_ln, normed + (size_t)t * H, H, eps);
-            ffn(m, L, normed + (size_t)t * H, ff);
-            for (int i = 0; i < H; ++i) mix[(size_t)t * H + i] = ff[i];
-        }
+        ffn_rows(m, L, normed, mix, n);
         for (size_t i = 0; i < (size_t)n * H; ++i) hidden[i] += mix[i];
         if (m->trace)
             for (int t = 0; t < n; ++t)
@@ -1313,10 +1389,14 @@ int orc_prefill(orc_model *m, const int *ids, int n, float *logits) {
     }
     if (logits) {
         const int64_t vocab = m->embed_rows;
-        for (int t = 0; t < n; ++t) {
-            orc_rmsnorm(hidden + (size_t)t * H, m->final_norm, ff, H, eps);
-            orc_matmul_bf16(m->embed, ff, logits + (size_t)t * vocab, (int)vocab, H);
-        }
+        float *fn = (float *)malloc(sizeof(float) * (size_t)n * H);
+        for (int t = 0; t < n; ++t) orc_rmsnorm(hidden + (size_t)t * H, m->final_norm, fn + (size_t)t * H, H, eps);
+        orc_matmul_bf16_rows(m->embed, fn, H, logits, vocab, n, (int)vocab, H);
+        free(fn);
+    }
+    if (m->handoff) {
+        memcpy(m->hidden, hidden + (size_t)(n - 1) * H, sizeof(float) * (size_t)H);
+        m->pos = n;
     }
     free(hidden);
     free(normed);

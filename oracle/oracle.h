@@ -40,6 +40,8 @@ float orc_softplus(float x);
 
 /* primitives: src/forward_pass.cpp */
 void orc_matmul_bf16(const uint16_t *W, const float *x, float *y, int out_dim, int in_dim);
+void orc_matmul_bf16_rows(const uint16_t *W, const float *X, int64_t ldx, float *Y, int64_t ldy,
+                          int n, int out_dim, int in_dim);
 void orc_matmul_f32(const float *W, const float *x, float *y, int out_dim, int in_dim);
 void orc_rmsnorm(const float *x, const float *w, float *y, int n, float eps);
 void orc_rmsnorm_gated(const float *x, const float *w, const float *gate, float *y, int n,
@@ -80,6 +82,8 @@ typedef struct orc_model orc_model;
 orc_model *orc_open(const char *dir, int max_context);  /* NULL on failure */
 void orc_close(orc_model *m);
 void orc_set_kv_bf16(orc_model *m, int on); /* store cache rows rounded to bf16 from now on */
+/* orc_prefill leaves its final state (GDN state, conv window, KV rows, residual, position) */
+void orc_set_prefill_handoff(orc_model *m, int on);
 const char *orc_error(void);
 void orc_get_dims(const orc_model *m, orc_dims *d);
 void orc_reset(orc_model *m);

@@ -51,6 +51,7 @@ def _load_oracle():
         "orc_round_bf16": (F, [F]),
         "orc_round_bf16_array": (None, [P, C.c_int64]),
         "orc_set_kv_bf16": (None, [P, I]),
+        "orc_set_prefill_handoff": (None, [P, I]),
         "orc_open": (P, [C.c_char_p, I]),
         "orc_close": (None, [P]),
         "orc_error": (C.c_char_p, []),
@@ -132,13 +133,17 @@ class Oracle:
             raise RuntimeError(olib.orc_error().decode())
         return out[:n_new]
 
-    def prefill(self, ids, rows: int | None = None) -> np.ndarray:
+    def prefill(self, ids, rows: int | None = None, want_logits: bool = True):
         ids = np.ascontiguousarray(ids, np.int32)
         vocab = rows or self.dims.vocab_size
-        lg = np.zeros((len(ids), vocab), np.float32)
-        if olib.orc_prefill(self.h, _p(ids), len(ids), _p(lg)) != 0:
+        lg = np.zeros((len(ids), vocab), np.float32) if want_logits else None
+        if olib.orc_prefill(self.h, _p(ids), len(ids), _p(lg) if want_logits else None) != 0:
             raise RuntimeError(olib.orc_error().decode())
         return lg
+
+    def set_prefill_handoff(self, on: bool):
+        """prefill() leaves its final state in the model, as token-serial steps would."""
+        olib.orc_set_prefill_handoff(self.h, int(on))
 
     def enable_trace(self, rows: int = 1):
         self._trace = np.zeros((rows, self.dims.n_layers_total, self.dims.hidden_size), np.float32)

@@ -8,7 +8,11 @@
 //            g = -exp(A_log) softplus(a + dt_bias); head-major outputs padded to whole chunks
 //            (padding rows have q = k = v = 0, beta = g = 0 and change nothing).
 //   ring     the last three raw inputs of the block go to their ring slots.
-//   chunk    per (v-head, chunk): gamma = cumsum(g); Q K^T and K K^T on the fp32 matrix cores;
+//   chunk    per (v-head, chunk): gamma = cumsum(g) in double (every decay factor below is
+//            e^(a difference of gammas) rounded once: an fp32 running sum would lose ~1e-6 of
+//            each exponent to cancellation, gamma reaching -40 within a chunk); the chunk's
+//            e^gamma and e^(gamma_last - gamma) go to the workspace for the later passes;
+//            Q K^T and K K^T on the fp32 matrix cores;
 //              P[i][j] = q_i.k_j e^(gamma_i - gamma_j)      (j <= i)
 //              A[i][j] = beta_i k_i.k_j e^(gamma_i - gamma_j)  (j < i)
 //              [U | W] = (I + A)^-1 [beta v | beta e^gamma k]  (forward substitution, one
@@ -170,7 +174,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     __shared__ __align__(16) float QA[kC * kLdC];
     float (*Qs)[kLdC] = reinterpret_cast<float (*)[kLdC]>(QA);
     float (*As)[kLdA] = reinterpret_cast<float (*)[kLdA]>(QA);
-    __shared__ float gam[kC], beta[kC];
+    __shared__ double gam[kC];
+    __shared__ float beta[kC];
     const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     for (int f = tid; f < kC * kD / 4; f += 256) {
@@ -179,14 +184,18 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     }
     if (tid < kC) beta[tid] = a.Bg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
     if (tid == 0) {
-        float s = 0.0f;
+        double s = 0.0;
         for (int i = 0; i < kC; ++i) {
-            s += a.Gg[static_cast<int64_t>(vh) * a.Tp + row0 + i];
+            s += static_cast<double>(a.Gg[static_cast<int64_t>(vh) * a.Tp + row0 + i]);
             gam[i] = s;
         }
     }
     __syncthreads();
-    if (tid < kC) a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid] = gam[tid];
+    if (tid < kC) {
+        const int64_t r = static_cast<int64_t>(vh) * a.Tp + row0 + tid;
+        a.Eg[r] = expf(static_cast<float>(gam[tid]));
+        a.Edl[r] = expf(static_cast<float>(gam[kC - 1] - gam[tid]));
+    }
     // P (j <= i) and A (j < i): S = Q K^T and KK = K K^T over the 128 dims; wave w owns rows
     // [16 w, 16 w + 16) and the 4 blocks of 16 columns; lane (lr, lg) ends with rows
     // 16 w + 4 lg + v of column 16 b + lr
@@ -213,7 +222,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 const int j = 16 * b + lr;
-                const float dec = j <= i ? expf(gam[i] - gam[j]) : 0.0f;
+                const float dec = j <= i ? expf(static_cast<float>(gam[i] - gam[j])) : 0.0f;
                 P[i * kC + j] = j <= i ? sq[b][v] * dec : 0.0f;
                 As[i][j] = j < i ? beta[i] * sk[b][v] * dec : 0.0f;
             }
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
         for (int i = 0; i < kC; ++i) col[i] = beta[i] * V[static_cast<int64_t>(i) * kD];
     } else {
 #pragma unroll
-        for (int i = 0; i < kC; ++i) col[i] = beta[i] * expf(gam[i]) * Ks[i][tid - kD];
+        for (int i = 0; i < kC; ++i) col[i] = beta[i] * expf(static_cast<float>(gam[i])) * Ks[i][tid - kD];
     }
 #pragma unroll
     for (int i = 1; i < kC; ++i) {
@@ -274,30 +283,29 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     // lane's U entries) is requested one chunk ahead, so the sequential chain only waits on LDS.
     constexpr int NF = kC * kD / 4 / kSThreads;
     float4 rw[NF], rk[NF];
-    float rgam[NF], rglast, ru[4];
+    float rdec[NF], relast, ru[4];  // e^(gamma_last - gamma) of the staged rows, e^gamma_last
     auto load_chunk = [&](int c) {
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
         const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-        const float* gam = a.Gam + static_cast<int64_t>(vh) * a.Tp + row0;
+        const float* edl = a.Edl + static_cast<int64_t>(vh) * a.Tp + row0;
         const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = tid + kSThreads * i;
             rw[i] = *reinterpret_cast<const float4*>(W + (f >> 5) * kD + (f & 31) * 4);
             rk[i] = *reinterpret_cast<const float4*>(K + (f >> 5) * kD + (f & 31) * 4);
-            rgam[i] = gam[f >> 5];
+            rdec[i] = edl[f >> 5];
         }
-        rglast = gam[kC - 1];
+        relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + kC - 1];
 #pragma unroll
         for (int v = 0; v < 4; ++v) ru[v] = U[(16 * vb + 4 * lg + v) * kD + lr];
     };
     auto store_chunk = [&]() {
-        const float glast = rglast;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = tid + kSThreads * i, r = f >> 5, c4 = (f & 31) * 4;
-            const float d = expf(glast - rgam[i]);
+            const float d = rdec[i];
             Wl[r][c4 + 0] = -rw[i].x;
             Wl[r][c4 + 1] = -rw[i].y;
             Wl[r][c4 + 2] = -rw[i].z;
@@ -316,7 +324,7 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     for (int c = 0; c < nchunk; ++c) {
         lds_barrier();  // previous chunk done with Wl / Kl / Ss
         store_chunk();
-        const float glast = rglast;
+        const float elast = relast;
         floatx4 vn;
 #pragma unroll
         for (int v = 0; v < 4; ++v) vn[v] = ru[v];
@@ -353,7 +361,7 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
         lds_barrier();  // VN complete, every wave done reading Ss
 
         // new state rows [16 w, 16 w + 16)
-        const float dl = expf(glast);
+        const float dl = elast;
         float* srow = &Ss[16 * wave + 4 * lg][lr];
         floatx4 sn;
 #pragma unroll
@@ -392,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     // 8 r + b), so a lane's eight column blocks of one B row are two 16-byte reads.
     __shared__ __align__(16) float A_s[kC][kLdQ];   // Q, then P
     __shared__ __align__(16) float B_s[kC][kLdS];   // S_c rows [0, 64), then [64, 128), then v_new
-    __shared__ float gam[kC];
+    __shared__ float eg[kC];  // e^gamma of the chunk's rows
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD;
     const float* P = a.P + (static_cast<int64_t>(vh) * nchunk + c) * kC * kC;
@@ -430,7 +438,7 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
         *reinterpret_cast<float4*>(&A_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
         put_b(f, *reinterpret_cast<const float4*>(Sc + f * 4));
     }
-    if (tid < kC) gam[tid] = a.Gam[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
+    if (tid < kC) eg[tid] = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
     __syncthreads();
     float4 rs[NQ4];  // S_c rows [64, 128)
 #pragma unroll
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     for (int blk = 0; blk < kC / 16; ++blk) mma16(kC + 16 * blk, 16 * blk);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        const float e = expf(gam[16 * wave + 4 * lg + v]);
+        const float e = eg[16 * wave + 4 * lg + v];
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[b][v] *= e;
     }
@@ -819,10 +827,10 @@ int blocks_for(int64_t n) {
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T) {
     const int64_t Tp = (T + kC - 1) / kC * kC;
     return (2 * KH + 3 * static_cast<int64_t>(VH)) * Tp * kD  // Qg Kg Vg U W
-           + 3 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Gam
+           + 4 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Eg Edl
            + static_cast<int64_t>(VH) * Tp * kC                // P
            + static_cast<int64_t>(VH) * (Tp / kC) * kD * kD    // Sc (chunk-start states)
-           + 64 * 8;                                           // alignment slack
+           + 64 * 9;                                           // alignment slack
 }
 
 void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
@@ -839,7 +847,8 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
     a.W = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
     a.Bg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Gg = take(static_cast<int64_t>(a.VH) * a.Tp);
-    a.Gam = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.Eg = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.Edl = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.P = take(static_cast<int64_t>(a.VH) * a.Tp * kC);
     a.Sc = take(static_cast<int64_t>(a.VH) * (a.Tp / kC) * kD * kD);
 }

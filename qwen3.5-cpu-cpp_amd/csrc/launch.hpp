@@ -167,8 +167,9 @@ struct GdnPrefillArgs {
     const float *conv_w, *A_log, *dt_bias, *norm_w;  // norm_w null: raw readout
     float *conv_ring, *state;
     float* out;        // [T][VH * 128]
-    // workspace (head-major, padded to Tp rows)
-    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Gam, *P;
+    // workspace (head-major, padded to Tp rows); Eg = e^gamma and Edl = e^(gamma_last - gamma)
+    // of each row, gamma the chunk-local cumulative decay
+    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Edl, *P;
     float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
 };
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);

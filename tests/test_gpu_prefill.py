@@ -41,7 +41,8 @@ class Bufs:
 @pytest.mark.parametrize("M,N,K,ldx,resid", [
     (1, 8, 32, 32, False), (130, 70, 64, 68, True), (257, 300, 520, 520, False),
     (64, 129, 8, 8, True), (512, 2048, 2048, 2048, True), (1000, 8224, 1024, 1024, False),
-    (300, 12290, 136, 136, True), (129, 12288, 64, 72, False)])  # the last two: 128 x 256 tiles
+    (300, 12290, 136, 136, True), (129, 12288, 64, 72, False),
+    (70, 96, 1000, 1000, True), (33, 40, 4104, 4104, False)])  # K past one block of 512 (ragged)
 def test_gemm_bf16(hip, M, N, K, ldx, resid):
     rng = np.random.default_rng(M * 7 + N + K)
     X = rng.standard_normal((M, ldx)).astype(np.float32)
@@ -61,6 +62,29 @@ def test_gemm_bf16(hip, M, N, K, ldx, resid):
         ref += R
     assert rel_l2(Y, ref) < 1e-6
     np.testing.assert_allclose(Y, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("N,K", [(6144, 2048), (2048, 6144)])
+def test_gemm_accuracy_at_projection_depth(hip, N, K):
+    """At the 2B projections' depths the GEMM stays as close to float64 as the matvec does
+    (about 1.2e-7 - 1.9e-7): products accumulated in blocks of K = 512 then summed. One fp32
+    accumulator over all of K measures 4.9e-7 (K = 2048) and 8.7e-7 (K = 6144) here."""
+    M = 256
+    rng = np.random.default_rng(N + K)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    W = bf16_bits(0.02 * rng.standard_normal((N, K)).astype(np.float32))
+    B = Bufs(hip)
+    try:
+        dX, dW, dY = B.up("X", X), B.up("W", W), B.alloc("Y", M * N * 4)
+        pyq35.check(pyq35.lib.q35_gemm_bf16(dX, K, dW, M, N, K, None, N, dY, N, None))
+        hip.sync()
+        Y = hip.download(dY, (M, N))
+    finally:
+        B.free()
+    ref = X.astype(np.float64) @ bf16_to_f32(W).astype(np.float64).T
+    err = rel_l2(Y, ref)
+    print(f"N={N} K={K}: rel_l2 vs float64 {err:.3g}")
+    assert err < 3.5e-7
 
 
 def test_gemm_rejects_bad_shapes(hip):

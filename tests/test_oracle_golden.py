@@ -140,3 +140,31 @@ def test_prefill_logits(model_dirs):
     assert rel_l2(lg, g["prefill_logits"]) < ORACLE_BAR
     # the reference's stateless prefill and its token-serial decode agree
     assert rel_l2(g["prefill_logits"], g["logits"]) < REL_L2
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
+def test_prefill_handoff_equals_token_serial_steps(model_dirs, name):
+    """The oracle's prefill with handoff on leaves exactly the state that token-serial steps
+    leave (GDN state, conv window, K / V rows, residual, position): the prefill and the step
+    restate the same reference arithmetic (src/qwen_forward.cpp:83-152 and
+    src/qwen_model.cpp:154-209 share their loops), so the two agree bit for bit."""
+    ids = pyq35.synth_token_ids(1, pyq35.dims_for(name).vocab_size, 150)
+    a = op.Oracle(model_dirs[name], 200)
+    a.set_prefill_handoff(True)
+    a.prefill(ids, want_logits=False)
+    b = op.Oracle(model_dirs[name], 200)
+    for t in ids:
+        b.step(int(t))
+    assert a.position == b.position == len(ids)
+    d = a.dims
+    n_gdn = d.n_layers_total - d.n_layers_total // d.attn_interval
+    for i in range(n_gdn):
+        np.testing.assert_array_equal(a.gdn_state(i), b.gdn_state(i))
+        np.testing.assert_array_equal(a.conv_state(i), b.conv_state(i))
+    for l in range(d.n_layers_total // d.attn_interval):
+        np.testing.assert_array_equal(a.kcache(l)[:len(ids)], b.kcache(l)[:len(ids)])
+        np.testing.assert_array_equal(a.vcache(l)[:len(ids)], b.vcache(l)[:len(ids)])
+    np.testing.assert_array_equal(a.hidden(), b.hidden())
+    np.testing.assert_array_equal(a.step(int(ids[0])), b.step(int(ids[0])))
+    a.close()
+    b.close()
