@@ -302,6 +302,18 @@ typedef struct q35_attn_decode_args {
 uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args *args);
 q35_status q35_attn_decode(const q35_attn_decode_args *args, q35_stream s);
 
+/* q35_attn_decode without a workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops or harnesses that forbid allocation). It has no
+ * counterpart in the reference. The split-K partials live in a device array the library
+ * owns, Q35_ATTN_STATIC_SCRATCH_BYTES on every GPU it runs on (held until the process ends):
+ * args->workspace and workspace_bytes are ignored, and a call whose partials
+ * (q35_attn_decode_workspace_bytes) exceed the array fails with Q35_ERR_RANGE. The call
+ * allocates nothing. All calls on one GPU share its array: calls that overlap in time on
+ * one GPU (other streams, other threads) race. The stream must belong to the current
+ * device. Results equal q35_attn_decode's. */
+#define Q35_ATTN_STATIC_SCRATCH_BYTES (8u << 20)
+q35_status q35_attn_decode_static(const q35_attn_decode_args *args, q35_stream s);
+
 /* GDN over a block of n_tokens prompt tokens at positions pos0 .. pos0 + n_tokens - 1, one
  * layer, chunked (WY form, chunk 64); the replacement of the sequential recurrence of
  * QwenForward::mix_gdn (src/qwen_forward.cpp:109-142). It continues from `state` and

@@ -3,8 +3,16 @@
 // that no kernel is launched with an extent it does not support.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "../host/q35_internal.h"
 #include "launch.hpp"
+
+// Device memory of q35_attn_decode_static: the split-K partials of callers that cannot
+// allocate. Every GPU the library runs on holds its own copy until the process ends. Host
+// code never uses this name as an address (on the host it is only a stand-in for the
+// symbol): the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) float scratch[Q35_ATTN_STATIC_SCRATCH_BYTES / sizeof(float)];
 
 namespace {
 
@@ -13,6 +21,93 @@ q35_status launched(hipError_t e, const char* what) {
 }
 
 hipStream_t as_stream(q35_stream s) { return static_cast<hipStream_t>(s); }
+
+// Device address of `scratch` on the current device (resolved at the first call on that
+// device, with the device current, and kept).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+q35_status scratch_of_current_device(hipStream_t s, float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return q35::fail(Q35_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return q35::fail(Q35_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    if (s) {
+        int sdev = -1;
+        e = hipStreamGetDevice(s, &sdev);
+        if (e != hipSuccess) return q35::fail(Q35_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+        if (sdev != dev)
+            return q35::fail(Q35_ERR_ARG, "the stream belongs to device %d but device %d is current", sdev, dev);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return q35::fail(Q35_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = static_cast<float*>(g_scratch_dev[dev]);
+    return Q35_OK;
+}
+
+// Shared by q35_attn_decode (partials in the caller's workspace) and q35_attn_decode_static
+// (partials in `scratch`): validates the arguments, then launches the split-K kernel and
+// the combine with the partials at `part`.
+q35_status attn_decode_checked(const q35_attn_decode_args* args, bool need_workspace, const char* who,
+                               int* splits_out) {
+    if (!args) return q35::fail(Q35_ERR_ARG, "%s: null args", who);
+    const q35_attn_decode_args& g = *args;
+    if (g.head_dim != 256) return q35::fail(Q35_ERR_UNSUPPORTED, "%s: head_dim must be 256", who);
+    if (g.kv_heads <= 0 || g.q_heads % g.kv_heads != 0) return q35::fail(Q35_ERR_ARG, "%s: bad head counts", who);
+    const int grp = g.q_heads / g.kv_heads;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16)
+        return q35::fail(Q35_ERR_UNSUPPORTED, "%s: GQA group %d", who, grp);
+    if (g.rotary_dim < 0 || g.rotary_dim > 256 || (g.rotary_dim & 1))
+        return q35::fail(Q35_ERR_ARG, "%s: rotary_dim %d", who, g.rotary_dim);
+    if (g.pos < 0 || g.pos >= g.max_context)
+        return q35::fail(Q35_ERR_RANGE, "%s: position %d outside [0, %lld)", who, g.pos,
+                         static_cast<long long>(g.max_context));
+    if (!g.qg || !g.k_new || !g.v_new || !g.q_norm || !g.k_norm || !g.k_cache || !g.v_cache || !g.out ||
+        (need_workspace && !g.workspace))
+        return q35::fail(Q35_ERR_ARG, "%s: null pointer", who);
+    if (g.n_splits < 0 || g.n_splits > 4096) return q35::fail(Q35_ERR_ARG, "%s: n_splits %d", who, g.n_splits);
+    if (g.kv_dtype != 0 && g.kv_dtype != 1) return q35::fail(Q35_ERR_ARG, "%s: kv_dtype %d", who, g.kv_dtype);
+    *splits_out = g.n_splits > 0 ? g.n_splits
+                                 : q35k::attn_default_splits(g.max_context, g.kv_heads * std::max(1, g.n_layers),
+                                                             q35k::device_cu_count());
+    return Q35_OK;
+}
+
+q35_status attn_decode_launch(const q35_attn_decode_args& g, int splits, float* part, hipStream_t st) {
+    const int grp = g.q_heads / g.kv_heads;
+    q35k::AttnDecodeArgs a{};
+    a.NQ = g.q_heads;
+    a.NKV = g.kv_heads;
+    a.HD = 256;
+    a.ROT = g.rotary_dim;
+    a.pos_val = g.pos;
+    a.max_ctx = g.max_context;
+    a.n_splits = splits;
+    a.theta = g.rope_theta;
+    a.eps = g.eps;
+    a.qg = g.qg;
+    a.k_new = g.k_new;
+    a.v_new = g.v_new;
+    a.q_norm = g.q_norm;
+    a.k_norm = g.k_norm;
+    a.k_cache = g.k_cache;
+    a.v_cache = g.v_cache;
+    a.kv_bf16 = g.kv_dtype == 1;
+    a.out = g.out;
+    a.n_layers = g.n_layers > 0 ? g.n_layers : 1;
+    a.part_o = part;
+    a.part_ml = a.part_o + static_cast<int64_t>(a.n_layers) * g.kv_heads * splits * grp * 256;
+    const q35_status r = launched(q35k::launch_attn_partial(a, st), "attn partial");
+    if (r != Q35_OK) return r;
+    return launched(q35k::launch_attn_combine(a, st), "attn combine");
+}
 
 }  // namespace
 
@@ -113,57 +208,34 @@ uint64_t q35_attn_decode_workspace_bytes(const q35_attn_decode_args* args) {
 }
 
 q35_status q35_attn_decode(const q35_attn_decode_args* args, q35_stream s) {
-    if (!args) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: null args");
-    const q35_attn_decode_args& g = *args;
-    if (g.head_dim != 256) return q35::fail(Q35_ERR_UNSUPPORTED, "q35_attn_decode: head_dim must be 256");
-    if (g.kv_heads <= 0 || g.q_heads % g.kv_heads != 0)
-        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: bad head counts");
-    const int grp = g.q_heads / g.kv_heads;
-    if (grp != 1 && grp != 2 && grp != 4 && grp != 8 && grp != 16)
-        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_attn_decode: GQA group %d", grp);
-    if (g.rotary_dim < 0 || g.rotary_dim > 256 || (g.rotary_dim & 1))
-        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: rotary_dim %d", g.rotary_dim);
-    if (g.pos < 0 || g.pos >= g.max_context)
-        return q35::fail(Q35_ERR_RANGE, "q35_attn_decode: position %d outside [0, %lld)", g.pos,
-                         static_cast<long long>(g.max_context));
-    if (!g.qg || !g.k_new || !g.v_new || !g.q_norm || !g.k_norm || !g.k_cache || !g.v_cache || !g.out ||
-        !g.workspace)
-        return q35::fail(Q35_ERR_ARG, "q35_attn_decode: null pointer");
-    if (g.n_splits < 0 || g.n_splits > 4096) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: n_splits %d", g.n_splits);
-    if (g.kv_dtype != 0 && g.kv_dtype != 1) return q35::fail(Q35_ERR_ARG, "q35_attn_decode: kv_dtype %d", g.kv_dtype);
-    if (g.workspace_bytes < q35_attn_decode_workspace_bytes(args))
+    int splits = 0;
+    const q35_status st = attn_decode_checked(args, true, "q35_attn_decode", &splits);
+    if (st != Q35_OK) return st;
+    const uint64_t need = q35_attn_decode_workspace_bytes(args);
+    if (args->workspace_bytes < need)
         return q35::fail(Q35_ERR_ARG, "q35_attn_decode: workspace of %llu bytes, needs %llu",
-                         static_cast<unsigned long long>(g.workspace_bytes),
-                         static_cast<unsigned long long>(q35_attn_decode_workspace_bytes(args)));
-    const int splits = g.n_splits > 0 ? g.n_splits
-                                      : q35k::attn_default_splits(g.max_context, g.kv_heads * std::max(1, g.n_layers),
-                                                                  q35k::device_cu_count());
-    q35k::AttnDecodeArgs a{};
-    a.NQ = g.q_heads;
-    a.NKV = g.kv_heads;
-    a.HD = 256;
-    a.ROT = g.rotary_dim;
-    a.pos_val = g.pos;
-    a.max_ctx = g.max_context;
-    a.n_splits = splits;
-    a.theta = g.rope_theta;
-    a.eps = g.eps;
-    a.qg = g.qg;
-    a.k_new = g.k_new;
-    a.v_new = g.v_new;
-    a.q_norm = g.q_norm;
-    a.k_norm = g.k_norm;
-    a.k_cache = g.k_cache;
-    a.v_cache = g.v_cache;
-    a.kv_bf16 = g.kv_dtype == 1;
-    a.out = g.out;
-    a.n_layers = g.n_layers > 0 ? g.n_layers : 1;
-    a.part_o = static_cast<float*>(g.workspace);
-    a.part_ml = a.part_o + static_cast<int64_t>(a.n_layers) * g.kv_heads * splits * grp * 256;
-    hipStream_t st = as_stream(s);
-    const q35_status r = launched(q35k::launch_attn_partial(a, st), "attn partial");
-    if (r != Q35_OK) return r;
-    return launched(q35k::launch_attn_combine(a, st), "attn combine");
+                         static_cast<unsigned long long>(args->workspace_bytes), static_cast<unsigned long long>(need));
+    return attn_decode_launch(*args, splits, static_cast<float*>(args->workspace), as_stream(s));
+}
+
+// The partials go to `scratch` instead of a workspace: nothing is allocated (no hipMalloc,
+// no allocating library call). Every partial the combine reads is written by the same
+// call's split-K kernel, so nothing needs clearing between calls.
+q35_status q35_attn_decode_static(const q35_attn_decode_args* args, q35_stream s) {
+    int splits = 0;
+    q35_status st = attn_decode_checked(args, false, "q35_attn_decode_static", &splits);
+    if (st != Q35_OK) return st;
+    const uint64_t need = q35_attn_decode_workspace_bytes(args);
+    if (need > Q35_ATTN_STATIC_SCRATCH_BYTES)
+        return q35::fail(Q35_ERR_RANGE,
+                         "q35_attn_decode_static: the split-K partials need %llu bytes, beyond the %llu of the "
+                         "static scratch (use fewer splits or layers per call, or q35_attn_decode)",
+                         static_cast<unsigned long long>(need),
+                         static_cast<unsigned long long>(Q35_ATTN_STATIC_SCRATCH_BYTES));
+    float* part = nullptr;
+    st = scratch_of_current_device(as_stream(s), &part);
+    if (st != Q35_OK) return st;
+    return attn_decode_launch(*args, splits, part, as_stream(s));
 }
 
 uint64_t q35_gdn_prefill_workspace_bytes(const q35_gdn_prefill_args* args) {

@@ -13,6 +13,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libq35.so")
+ATTN_STATIC_SCRATCH_BYTES = 8 << 20  # Q35_ATTN_STATIC_SCRATCH_BYTES of include/q35.h
 
 Q35_OK = 0
 KT_NAMES = ["gemv", "gdn_decode", "attn_decode", "attn_combine", "other", "gemm", "gdn_prefill",
@@ -157,6 +158,7 @@ def _load():
         "q35_gdn_decode": (S, [C.POINTER(GdnDecodeArgs), P]),
         "q35_attn_decode_workspace_bytes": (U64, [C.POINTER(AttnDecodeArgs)]),
         "q35_attn_decode": (S, [C.POINTER(AttnDecodeArgs), P]),
+        "q35_attn_decode_static": (S, [C.POINTER(AttnDecodeArgs), P]),
         "q35_gemm_bf16": (S, [P, I64, P, I32, I32, I32, P, I64, P, I64, P]),
         "q35_gdn_prefill_workspace_bytes": (U64, [C.POINTER(GdnPrefillArgs)]),
         "q35_gdn_prefill": (S, [C.POINTER(GdnPrefillArgs), P]),

@@ -240,3 +240,21 @@ def test_kernel_entry_points_validate_before_launch():
     assert b"kv_dtype" in pyq35.lib.q35_last_error()
     assert pyq35.lib.q35_matmul_bf16(None, None, None, 4, 8, None) == -1
     assert pyq35.lib.q35_matmul_bf16(1 << 20, 1 << 20, 1 << 20, 4, 12, None) == -7
+
+
+def test_attn_decode_static_refuses_oversized_partials():
+    """The no-allocation attention decode checks its split-K partials against the static
+    device array before any device call: beyond Q35_ATTN_STATIC_SCRATCH_BYTES it fails with
+    Q35_ERR_RANGE (the pointers below are never dereferenced)."""
+    fake = dict(qg=1 << 20, k_new=1 << 20, v_new=1 << 20, q_norm=1 << 20, k_norm=1 << 20,
+                k_cache=1 << 20, v_cache=1 << 20, out=1 << 20)
+    at = pyq35.AttnDecodeArgs(q_heads=16, kv_heads=2, head_dim=256, rotary_dim=64, pos=10, n_splits=4096,
+                              n_layers=2, max_context=1 << 20, **fake)
+    hdr = open(os.path.join(ROOT, "include", "q35.h")).read()
+    m = re.search(r"#define Q35_ATTN_STATIC_SCRATCH_BYTES \((\d+)u << (\d+)\)", hdr)
+    assert m and int(m.group(1)) << int(m.group(2)) == pyq35.ATTN_STATIC_SCRATCH_BYTES
+    assert pyq35.lib.q35_attn_decode_workspace_bytes(C.byref(at)) > pyq35.ATTN_STATIC_SCRATCH_BYTES
+    assert pyq35.lib.q35_attn_decode_static(C.byref(at), None) == -6
+    assert b"static scratch" in pyq35.lib.q35_last_error()
+    at.head_dim = 128  # shape checks as q35_attn_decode's
+    assert pyq35.lib.q35_attn_decode_static(C.byref(at), None) == -7
