@@ -65,7 +65,9 @@ typedef struct q35_dims {
     int32_t tie_word_embeddings;  /* tie_word_embeddings */
 } q35_dims;
 
-/* Bytes per arena. Mirrors MemoryBudget, include/memory_budget.h:6-19. */
+/* Bytes per arena. Mirrors MemoryBudget, include/memory_budget.h:6-19, plus the prompt arena
+ * of the chunked prefill (activations of one block of prompt tokens), which the reference
+ * does not have: q35_compute_budget leaves it 0, q35_model_budget reports the model's. */
 typedef struct q35_budget {
     uint64_t weight_bytes;
     uint64_t gdn_state_bytes;
@@ -73,6 +75,7 @@ typedef struct q35_budget {
     uint64_t kv_cache_bytes;
     uint64_t activation_bytes;
     uint64_t vision_scratch_bytes;
+    uint64_t prompt_arena_bytes;
 } q35_budget;
 
 /* ------------------------------------------------------------------------------------ */
@@ -81,8 +84,9 @@ typedef struct q35_budget {
 const char *q35_last_error(void);  /* message for the last failed call on this thread */
 const char *q35_version(void);
 /* Number of device allocations the library has made since load (they happen in
- * q35_model_open / q35_model_create, plus the prompt arena of a model's first prefill; a
- * decode step must leave this unchanged). */
+ * q35_model_open / q35_model_create, q35_model_reserve_context, the prompt arena of a
+ * model's first prefill when none was planned, and the staging buffer of the forward_pass.h
+ * functions' first call; a decode step must leave this unchanged). */
 int64_t q35_device_alloc_count(void);
 
 /* ------------------------------------------------------------------------------------ */
@@ -132,15 +136,22 @@ typedef struct q35_tensor {
 
 /* Plans the four device arenas (weights, recurrent state, KV cache, scratch) with the
  * memory equation, makes one hipMalloc for each and uploads the weights. max_context is
- * the KV capacity in positions. */
+ * the KV capacity in positions; max_context 0 plans it with solve_max_context
+ * (src/memory_budget.cpp:56-81) against the device's memory: weights, state, scratch, a
+ * planned prompt arena and a 1 GiB margin are fixed costs, the rest holds KV rows, up to
+ * native_max_context (q35_model_max_context reports the result). */
 q35_status q35_model_create(const q35_dims *d, const q35_tensor *tensors, int32_t n_tensors,
                             int64_t max_context, q35_model **out);
 /* Creation options. kv_bytes_per_elem is memory_budget's KV element width
  * (include/memory_budget.h:37-42): 4 = fp32 cache (the reference's; the default), 2 = bf16
- * cache (rows rounded to nearest even when appended; half the KV bytes and bandwidth). */
+ * cache (rows rounded to nearest even when appended; half the KV bytes and bandwidth).
+ * prefill_block > 0 plans the prompt arena at creation, for prefill blocks of up to that
+ * many tokens (a fifth hipMalloc, reported in q35_budget.prompt_arena_bytes; larger blocks
+ * are refused); 0 leaves it to the first prefill. */
 typedef struct q35_model_options {
     int32_t kv_bytes_per_elem;
-    int32_t reserved[7];
+    int32_t prefill_block;
+    int32_t reserved[6];
 } q35_model_options;
 q35_status q35_model_create_opts(const q35_dims *d, const q35_tensor *tensors, int32_t n_tensors,
                                  int64_t max_context, const q35_model_options *opt, q35_model **out);
@@ -173,8 +184,9 @@ q35_status q35_model_decode_greedy(q35_model *m, int32_t token, int32_t n_new, i
 /* Whole-prompt forward (QwenForward::prefill, src/qwen_forward.cpp:154-206): starts from a
  * zero state, runs the chunked GDN and flash attention prefill and leaves the model state
  * (GDN state, conv window, KV rows, pos = n) as n decode steps would. logits_host receives
- * n * vocab floats when not NULL. The first call makes the prompt arena (one more device
- * allocation, kept for later calls): activations for one block of tokens. */
+ * n rows of q35_model_prefill_logits_width floats when not NULL. Without a prompt arena
+ * planned at creation, the first call makes it (one more device allocation, kept for later
+ * calls): activations for one block of tokens. */
 q35_status q35_model_prefill(q35_model *m, const int32_t *ids, int32_t n, float *logits_host);
 /* The same chunked path continuing from the current position: ids are placed at positions
  * pos .. pos + n - 1 (no reset). trace_host, when not NULL, receives the hidden state after
@@ -183,9 +195,24 @@ q35_status q35_model_prefill(q35_model *m, const int32_t *ids, int32_t n, float 
  * q35_model_decode_greedy. */
 q35_status q35_model_extend(q35_model *m, const int32_t *ids, int32_t n, float *logits_host,
                             float *trace_host);
-/* Tokens per prefill block (0 = automatic: min(4096, max_context)). Larger blocks make
- * larger GEMMs and a larger prompt arena. */
+/* Tokens per prefill block (0 = automatic: the planned block, else min(4096, max_context)).
+ * Larger blocks make larger GEMMs and a larger prompt arena; a prompt arena planned at
+ * creation serves every block up to its size and refuses larger ones (Q35_ERR_RANGE), one
+ * made by a prefill is made again only for a larger block. */
 q35_status q35_model_set_prefill_block(q35_model *m, int32_t tokens);
+/* Output head of the prefill logits: Q35_HEAD_OUTPUT (the default) is the step's head
+ * (lm_head when the checkpoint has one, else the tied embedding; vocab_size rows),
+ * Q35_HEAD_EMBEDDING is QwenForward::prefill's rule (src/qwen_forward.cpp:193-199): the
+ * embedding over all its rows. The width of each logits row is
+ * q35_model_prefill_logits_width. Decoding after a prefill always uses the step's head. */
+#define Q35_HEAD_OUTPUT 0
+#define Q35_HEAD_EMBEDDING 1
+q35_status q35_model_set_prefill_head(q35_model *m, int32_t head);
+int64_t q35_model_prefill_logits_width(const q35_model *m);
+/* Grows the KV capacity to max_context positions (no change when it is not larger): the KV
+ * and scratch arenas are made again, the weights stay; the model is reset. For a caller
+ * that learns the context it needs after creating the model (a longer prompt). */
+q35_status q35_model_reserve_context(q35_model *m, int64_t max_context);
 
 /* Decode-step execution options. */
 q35_status q35_model_set_graph(q35_model *m, int32_t enable);        /* hipGraph replay */
@@ -235,6 +262,10 @@ q35_status q35_model_fill_synthetic(q35_model *m, int64_t pos, uint64_t seed, fl
 /* y = W x, W bf16 row-major [out_dim][in_dim] (forward_pass.cpp:65-75). in_dim % 8 == 0. */
 q35_status q35_matmul_bf16(const uint16_t *W, const float *x, float *y, int32_t out_dim,
                            int32_t in_dim, q35_stream s);
+/* y = W x with fp32 W row-major [out_dim][in_dim], any in_dim (forward_pass.cpp:29-33, the
+ * fp32 overload of matmul). */
+q35_status q35_matmul_f32(const float *W, const float *x, float *y, int32_t out_dim, int32_t in_dim,
+                          q35_stream s);
 /* Token-batched matmul for the prefill: Y[M][N] = (R ? R : 0) + X[M][K] . W[N][K]^T, fp32 X /
  * R / Y with leading dimensions (elements), bf16 W row-major (forward_pass.cpp:65-75 for M
  * rows at once). Requires K % 8 == 0, ldx % 4 == 0 and a 16-byte aligned X. R may alias Y. */
@@ -250,7 +281,9 @@ q35_status q35_rmsnorm_gated(const float *x, const float *w, const float *gate, 
 /* Row-wise in place x *= 1/sqrt(sum(x^2) + eps) (forward_pass.cpp:95-100). */
 q35_status q35_l2norm(float *x, int32_t rows, int32_t n, float eps, q35_stream s);
 /* Partial rotate-half RoPE in place on rows of head_dim; row r is at position pos[r]
- * (device int32 array) or at pos0 when pos is NULL (forward_pass.cpp:102-112). */
+ * (device int32 array) or at pos0 when pos is NULL (forward_pass.cpp:102-112). Pairs
+ * (i, i + rotary_dim / 2) for i < rotary_dim / 2: with an odd rotary_dim the last rotated
+ * index stays as it is, as in the reference. */
 q35_status q35_apply_rope(float *x, int32_t rows, int32_t head_dim, int32_t rotary_dim,
                           const int32_t *pos, int32_t pos0, double theta, q35_stream s);
 

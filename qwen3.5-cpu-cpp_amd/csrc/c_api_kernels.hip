@@ -131,6 +131,12 @@ q35_status q35_matmul_bf16(const uint16_t* W, const float* x, float* y, int32_t 
     return launched(q35k::launch_gemv(a, q35k::kProPlain, as_stream(s)), "q35_matmul_bf16");
 }
 
+q35_status q35_matmul_f32(const float* W, const float* x, float* y, int32_t out_dim, int32_t in_dim,
+                          q35_stream s) {
+    if (!W || !x || !y || out_dim <= 0 || in_dim <= 0) return q35::fail(Q35_ERR_ARG, "q35_matmul_f32: bad argument");
+    return launched(q35k::launch_matvec_f32(W, x, y, out_dim, in_dim, as_stream(s)), "q35_matmul_f32");
+}
+
 q35_status q35_gemm_bf16(const float* X, int64_t ldx, const uint16_t* W, int32_t M, int32_t N, int32_t K,
                          const float* R, int64_t ldr, float* Y, int64_t ldy, q35_stream s) {
     if (!X || !W || !Y || M <= 0 || N <= 0 || K <= 0 || ldx < K || ldy < N || (R && ldr < N))
@@ -161,7 +167,7 @@ q35_status q35_l2norm(float* x, int32_t rows, int32_t n, float eps, q35_stream s
 
 q35_status q35_apply_rope(float* x, int32_t rows, int32_t head_dim, int32_t rotary_dim, const int32_t* pos,
                           int32_t pos0, double theta, q35_stream s) {
-    if (!x || rows <= 0 || head_dim <= 0 || rotary_dim < 0 || rotary_dim > head_dim || (rotary_dim & 1))
+    if (!x || rows <= 0 || head_dim <= 0 || rotary_dim < 0 || rotary_dim > head_dim)
         return q35::fail(Q35_ERR_ARG, "q35_apply_rope: bad argument");
     return launched(q35k::launch_rope_rows(x, rows, head_dim, rotary_dim, pos, pos0, theta, as_stream(s)),
                     "q35_apply_rope");

@@ -100,6 +100,25 @@ __global__ __launch_bounds__(64) void rope_rows_kernel(float* x, int hd, int rot
     }
 }
 
+// y = W x with fp32 weights, W row-major [rows][n] (the fp32 overload of the reference's
+// matmul, src/forward_pass.cpp:29-33), any n: one row per wave, lanes striding the row
+// (coalesced), four independent partial sums per lane, then a wave reduction.
+__global__ __launch_bounds__(256) void matvec_f32_kernel(const float* W, const float* x, float* y, int rows, int n) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* w = W + static_cast<int64_t>(row) * n;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int i = lane;
+    for (; i + 192 < n; i += 256) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = fmaf(w[i + 64 * u], x[i + 64 * u], acc[u]);
+    }
+    for (; i < n; i += 64) acc[0] = fmaf(w[i], x[i], acc[0]);
+    const float t = wave_sum((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    if (lane == 0) y[row] = t;
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* embed, const int* token,
                                                     float* hidden, int H) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -241,6 +260,11 @@ hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t 
 hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
                             double theta, hipStream_t s) {
     klaunch(rope_rows_kernel, rows, 64, 0, s, x, hd, rot, pos, pos0, theta);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_f32(const float* W, const float* x, float* y, int rows, int n, hipStream_t s) {
+    klaunch(matvec_f32_kernel, (rows + 3) / 4, 256, 0, s, W, x, y, rows, n);
     return hipGetLastError();
 }
 

@@ -200,6 +200,8 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
 hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidden, int T, int H, hipStream_t s);
 
 // ---------------------------------------------------------------- small kernels
+// y = W x with fp32 weights [rows][n], any n
+hipError_t launch_matvec_f32(const float* W, const float* x, float* y, int rows, int n, hipStream_t s);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
                                float eps, int gated, const float* gate, hipStream_t s);
 hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s);

@@ -45,10 +45,18 @@ hipError_t dev_alloc(void** p, size_t bytes) {
     return hipMalloc(p, bytes);
 }
 
+}  // namespace
+
+void q35::count_device_alloc() { g_dev_allocs.fetch_add(1); }
+
+namespace {
+
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 // split-K workspace is sized for this many splits per kv head
 constexpr int kMaxSplits = 1024;
+// device memory left free when the KV capacity is planned from the device's memory
+constexpr size_t kSolveMarginBytes = size_t{1} << 30;
 
 struct LayerDev {
     bool attn = false;
@@ -104,12 +112,14 @@ struct q35_model {
     int64_t pos = 0;  // host mirror of *pos_dev
     int32_t* pinned_token = nullptr;
 
-    // prompt arena: token-block activations of the chunked prefill, made by the first
-    // prefill (one hipMalloc) and kept; pf_block tokens per block
+    // prompt arena: token-block activations of the chunked prefill (one hipMalloc), planned
+    // at creation for blocks of up to pf_planned tokens, or made by the first prefill when
+    // none was planned (and made again only for a larger block)
     uint8_t* pf_arena = nullptr;
     size_t pf_bytes = 0;
-    int pf_block = 0;        // requested block size (0 = automatic)
-    int pf_arena_block = 0;  // block size the arena was made for
+    int pf_block = 0;    // requested block size (0 = automatic)
+    int pf_planned = 0;  // block size planned at creation (0: none)
+    int prefill_head = 0;  // prefill logits: 0 = the step's output head, 1 = the embedding
 
     bool use_graph = true;
     bool graph_valid = false;
@@ -513,12 +523,175 @@ void destroy(q35_model* m) {
     delete m;
 }
 
+// ------------------------------------------------------------------ context arenas
+// Scratch arena layout for a given KV capacity (byte offsets, 256-B aligned): the decode
+// step's activations, split-K partials, logits, argmax partials, device token / position,
+// and the two context-sized tables (greedy id history, RoPE cos / sin per position).
+struct ScratchPlan {
+    size_t hidden, proj, mix, gu, part, logits, trace, am, ints, ids, rope, bytes;
+};
+
+ScratchPlan scratch_plan(const q35_dims& d, int64_t max_ctx) {
+    const int H = d.hidden_size, I = d.ffn_intermediate;
+    const int KD = d.gdn_k_heads * 128, VD = d.gdn_v_heads * 128, VH = d.gdn_v_heads, CONV = 2 * KD + VD;
+    const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    const int64_t proj_n = std::max<int64_t>(static_cast<int64_t>(CONV) + VD + 2 * VH, 2LL * NQ * HD + 2LL * NKV * HD);
+    ScratchPlan p{};
+    size_t sc = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = sc;
+        sc = align256(sc + bytes);
+        return o;
+    };
+    p.hidden = take(static_cast<size_t>(H) * 4);
+    p.proj = take(static_cast<size_t>(proj_n) * 4);
+    p.mix = take(static_cast<size_t>(std::max(VD, NQ * HD)) * 4);
+    p.gu = take(static_cast<size_t>(2) * I * 4);
+    p.part = take(static_cast<size_t>(q35k::attn_partial_floats(NQ, NKV, HD, kMaxSplits)) * 4);
+    p.logits = take(static_cast<size_t>(d.vocab_size) * 4);
+    p.trace = take(static_cast<size_t>(d.n_layers_total) * H * 4);
+    p.am = take(static_cast<size_t>(2) * q35k::kArgmaxBlocks * 4);
+    p.ints = take(16 * 4);
+    p.ids = take(static_cast<size_t>(max_ctx) * 4);
+    p.rope = take(static_cast<size_t>(max_ctx) * std::max(1, rot_dims(d)) * 4);
+    p.bytes = sc;
+    return p;
+}
+
+// (Re)makes the KV and scratch arenas for max_ctx positions (one hipMalloc each), zeroed,
+// with the RoPE table filled; the model is at position 0 afterwards.
+q35_status alloc_context(q35_model* m, int64_t max_ctx) {
+    const q35_dims& d = m->d;
+    if (m->kv_arena) HIPCHK(hipFree(m->kv_arena));
+    if (m->scratch) HIPCHK(hipFree(m->scratch));
+    m->kv_arena = nullptr;
+    m->scratch = nullptr;
+    m->max_ctx = max_ctx;
+    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * d.attn_kv_heads * static_cast<size_t>(max_ctx) *
+                  d.attn_head_dim * m->kv_elem;
+    m->n_splits = q35k::attn_default_splits(max_ctx, d.attn_kv_heads, m->n_cu);
+    const ScratchPlan sp = scratch_plan(d, max_ctx);
+    m->scratch_bytes = sp.bytes;
+    void* p = nullptr;
+    HIPCHK(dev_alloc(&p, std::max<size_t>(m->kv_bytes, 256)));
+    m->kv_arena = static_cast<float*>(p);
+    HIPCHK(dev_alloc(&p, m->scratch_bytes));
+    m->scratch = static_cast<uint8_t*>(p);
+    auto S32 = [&](size_t off) { return reinterpret_cast<float*>(m->scratch + off); };
+    const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    m->hidden = S32(sp.hidden);
+    m->proj = S32(sp.proj);
+    m->mix = S32(sp.mix);
+    m->gu = S32(sp.gu);
+    m->part_o = S32(sp.part);
+    m->part_ml = m->part_o + static_cast<int64_t>(NKV) * kMaxSplits * (NQ / NKV) * HD;
+    m->logits = S32(sp.logits);
+    m->trace = S32(sp.trace);
+    m->argmax_part = m->scratch + sp.am;
+    int* ints = reinterpret_cast<int*>(m->scratch + sp.ints);
+    m->token_dev = ints;
+    m->pos_dev = ints + 1;
+    m->ids_dev = reinterpret_cast<int*>(m->scratch + sp.ids);
+    m->rope_cs = S32(sp.rope);
+    HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
+    HIPCHK(q35k::launch_fill_f32(reinterpret_cast<float*>(m->scratch), static_cast<int64_t>(m->scratch_bytes / 4), 0.0f,
+                                 m->stream));
+    HIPCHK(q35k::launch_rope_table(m->rope_cs, max_ctx, rot_dims(d), d.rope_theta, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    m->pos = 0;
+    m->budget.kv_cache_bytes = m->kv_bytes;
+    m->budget.activation_bytes = m->scratch_bytes;
+    return Q35_OK;
+}
+
+// Layout of the prompt arena for blocks of `tb` tokens (offsets in floats, 256-B aligned).
+// The logits rows are wide enough for either output head (vocab_size or the embedding's rows).
+struct PrefillPlan {
+    int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
+    int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
+};
+
+int64_t proj_width(const q35_dims& d) {
+    const int64_t KD = d.gdn_k_heads * 128LL, VD = d.gdn_v_heads * 128LL;
+    return std::max<int64_t>(2 * KD + VD + VD + 2LL * d.gdn_v_heads,
+                             2LL * d.attn_q_heads * d.attn_head_dim + 2LL * d.attn_kv_heads * d.attn_head_dim);
+}
+
+PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
+    PrefillPlan p;
+    p.tb = tb;
+    p.lr = std::min(tb, 256);
+    const int64_t H = d.hidden_size, I = d.ffn_intermediate, T = tb;
+    const int64_t VD = d.gdn_v_heads * 128LL, QD = static_cast<int64_t>(d.attn_q_heads) * d.attn_head_dim;
+    int64_t cur = 0;
+    auto take = [&](int64_t n) {
+        const int64_t o = cur;
+        cur += (n + 63) / 64 * 64;
+        return o;
+    };
+    p.hidden = take(T * H);
+    p.xn = take(T * H);
+    p.proj = take(T * proj_width(d));
+    p.mix = take(T * std::max(VD, QD));
+    p.hb = take(T * I);
+    p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
+                         q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
+    p.logits = take(static_cast<int64_t>(p.lr) * logits_width);
+    p.ids = take(T);
+    p.total = cur;
+    return p;
+}
+
+int64_t logits_width(const q35_model* m) { return std::max<int64_t>(m->d.vocab_size, m->embed_rows); }
+
+size_t prompt_arena_bytes(const q35_model* m, int64_t tb) {
+    return static_cast<size_t>(plan_prefill(m->d, static_cast<int>(tb), logits_width(m)).total) * 4;
+}
+
+q35_status make_prompt_arena(q35_model* m, int64_t tb) {
+    if (m->pf_arena) {
+        HIPCHK(hipStreamSynchronize(m->stream));
+        HIPCHK(hipFree(m->pf_arena));
+        m->pf_arena = nullptr;
+        m->pf_bytes = 0;
+    }
+    void* p = nullptr;
+    const size_t bytes = prompt_arena_bytes(m, tb);
+    HIPCHK(dev_alloc(&p, bytes));
+    m->pf_arena = static_cast<uint8_t*>(p);
+    m->pf_bytes = bytes;
+    m->budget.prompt_arena_bytes = bytes;
+    return Q35_OK;
+}
+
+int prefill_block_tokens(const q35_model* m) {
+    const int64_t want = m->pf_block > 0 ? m->pf_block : m->pf_planned > 0 ? m->pf_planned : 4096;
+    return static_cast<int>(std::min<int64_t>(want, m->max_ctx));
+}
+
+// The prompt arena for the current block size: the one planned at creation, or the one the
+// last prefill made when it is large enough, else a new one (lazy mode only).
+q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
+    const int tb = prefill_block_tokens(m);
+    *plan = plan_prefill(m->d, tb, logits_width(m));
+    if (m->pf_arena && static_cast<size_t>(plan->total) * 4 <= m->pf_bytes) return Q35_OK;
+    if (m->pf_planned > 0)
+        return q35::fail(Q35_ERR_RANGE, "a prefill block of %d tokens exceeds the prompt arena planned for %d", tb,
+                         m->pf_planned);
+    const q35_status st = make_prompt_arena(m, tb);
+    if (st == Q35_OK)
+        std::cerr << "[q35] prompt arena: " << (m->pf_bytes >> 20) << " MiB for blocks of " << tb << " tokens\n";
+    return st;
+}
+
 q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int64_t max_ctx, int kv_elem,
-                        q35_model** out) {
+                        int prefill_block, q35_model** out) {
     if (!dims || !ts || !out || nt <= 0) return q35::fail(Q35_ERR_ARG, "q35_model_create: null argument");
     *out = nullptr;
-    if (max_ctx <= 0 || max_ctx > (int64_t{1} << 30))
+    if (max_ctx < 0 || max_ctx > (int64_t{1} << 30))
         return q35::fail(Q35_ERR_RANGE, "max_context %lld out of range", static_cast<long long>(max_ctx));
+    if (prefill_block < 0 || prefill_block > (1 << 20))
+        return q35::fail(Q35_ERR_RANGE, "prefill block %d out of range", prefill_block);
     if (kv_elem != 4 && kv_elem != 2)
         return q35::fail(Q35_ERR_UNSUPPORTED, "KV cache element of %d bytes (4 = fp32 or 2 = bf16)", kv_elem);
     q35_dims d = *dims;
@@ -616,49 +789,45 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->max_ctx = max_ctx;
     HIPCHK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
 
-    // state, kv and scratch plans
+    // state arena: GDN states and conv rings (fixed size)
     const size_t gdn_bytes = static_cast<size_t>(d.n_layers_gdn) * VH * 128 * 128 * 4;
     const size_t ring_bytes = static_cast<size_t>(d.n_layers_gdn) * 4 * CONV * 4;
     m->state_bytes = align256(gdn_bytes) + align256(ring_bytes);
     m->kv_elem = kv_elem;
-    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * static_cast<size_t>(max_ctx) * HD * kv_elem;
     m->n_cu = q35k::device_cu_count();
-    m->n_splits = q35k::attn_default_splits(max_ctx, NKV, m->n_cu);
-    const int64_t proj_n = std::max<int64_t>(static_cast<int64_t>(CONV) + VD + 2 * VH, 2LL * NQ * HD + 2LL * NKV * HD);
-    size_t sc = 0;
-    auto take = [&](size_t bytes) {
-        const size_t o = sc;
-        sc = align256(sc + bytes);
-        return o;
-    };
-    const size_t o_hidden = take(static_cast<size_t>(H) * 4);
-    const size_t o_proj = take(static_cast<size_t>(proj_n) * 4);
-    const size_t o_mix = take(static_cast<size_t>(std::max(VD, NQ * HD)) * 4);
-    const size_t o_gu = take(static_cast<size_t>(2) * I * 4);
-    const int64_t pf = q35k::attn_partial_floats(NQ, NKV, HD, kMaxSplits);
-    const size_t o_part = take(static_cast<size_t>(pf) * 4);
-    const size_t o_logits = take(static_cast<size_t>(d.vocab_size) * 4);
-    const size_t o_trace = take(static_cast<size_t>(d.n_layers_total) * H * 4);
-    const size_t o_am = take(static_cast<size_t>(2) * q35k::kArgmaxBlocks * 4);
-    const size_t o_ints = take(16 * 4);
-    const size_t o_ids = take(static_cast<size_t>(max_ctx) * 4);
-    const size_t o_rope = take(static_cast<size_t>(max_ctx) * std::max(1, rot_dims(d)) * 4);
-    m->scratch_bytes = sc;
     m->w_bytes = plan.bytes();
+    m->embed_rows = emb_rows;
+    m->pf_planned = prefill_block;
+    const size_t pf_bytes = prefill_block > 0 ? prompt_arena_bytes(m.get(), max_ctx > 0 ? std::min<int64_t>(prefill_block, max_ctx) : prefill_block) : 0;
 
-    std::cerr << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
-              << " MiB, state " << (m->state_bytes >> 10) << " KiB, kv " << (m->kv_bytes >> 20)
-              << " MiB, scratch " << (m->scratch_bytes >> 10) << " KiB\n";
+    if (max_ctx == 0) {
+        // KV capacity from the memory equation (src/memory_budget.cpp:56-81) against the
+        // device's memory: weights, recurrent state, the context-independent scratch, the
+        // planned prompt arena and a margin are fixed; the rest is KV, up to the model's
+        // native context
+        size_t free_b = 0, total_b = 0;
+        HIPCHK(hipMemGetInfo(&free_b, &total_b));
+        const size_t fixed = m->w_bytes + m->state_bytes + scratch_plan(d, 0).bytes + pf_bytes;
+        int64_t ctx = q35_solve_max_context(&d, total_b, m->w_bytes, m->state_bytes,
+                                            scratch_plan(d, 0).bytes + pf_bytes, 0, kSolveMarginBytes, kv_elem);
+        if (ctx <= 0)
+            return q35::fail(Q35_ERR_RANGE, "no KV capacity fits %zu bytes of device memory next to %zu of weights",
+                             total_b, m->w_bytes);
+        // the scratch also grows with the context (greedy ids, RoPE table): the equation's
+        // per-token KV cost plus those bytes per position must fit as well
+        const size_t per_pos = static_cast<size_t>(d.n_layers_attn) * 2 * NKV * HD * kv_elem +
+                               (scratch_plan(d, 1).bytes - scratch_plan(d, 0).bytes);
+        ctx = std::min<int64_t>(ctx, static_cast<int64_t>((total_b - fixed - kSolveMarginBytes) / per_pos));
+        max_ctx = std::min<int64_t>(ctx, int64_t{1} << 30);
+        std::cerr << "[q35] max_context " << max_ctx << " planned by the memory equation against "
+                  << (total_b >> 20) << " MiB of device memory\n";
+    }
 
     void* p = nullptr;
     HIPCHK(dev_alloc(&p, m->w_bytes));
     m->w_arena = static_cast<uint8_t*>(p);
     HIPCHK(dev_alloc(&p, m->state_bytes));
     m->state_arena = static_cast<float*>(p);
-    HIPCHK(dev_alloc(&p, std::max<size_t>(m->kv_bytes, 256)));
-    m->kv_arena = static_cast<float*>(p);
-    HIPCHK(dev_alloc(&p, m->scratch_bytes));
-    m->scratch = static_cast<uint8_t*>(p);
     HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&m->pinned_token), 64, hipHostMallocDefault));
 
     // upload
@@ -716,104 +885,28 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
         }
     }
     m->embed = W16(emb_off);
-    m->embed_rows = emb_rows;
     m->head = W16(head_off);
     m->final_norm = W32(fnorm_off);
     m->gdn_state = m->state_arena;
     m->conv_ring = m->state_arena + align256(gdn_bytes) / 4;
-    auto S32 = [&](size_t off) { return reinterpret_cast<float*>(m->scratch + off); };
-    m->hidden = S32(o_hidden);
-    m->proj = S32(o_proj);
-    m->mix = S32(o_mix);
-    m->gu = S32(o_gu);
-    m->part_o = S32(o_part);
-    m->part_ml = m->part_o + static_cast<int64_t>(NKV) * kMaxSplits * (NQ / NKV) * HD;
-    m->logits = S32(o_logits);
-    m->trace = S32(o_trace);
-    m->argmax_part = m->scratch + o_am;
-    int* ints = reinterpret_cast<int*>(m->scratch + o_ints);
-    m->token_dev = ints;
-    m->pos_dev = ints + 1;
-    m->ids_dev = reinterpret_cast<int*>(m->scratch + o_ids);
-    m->rope_cs = S32(o_rope);
-
-    // reset: zero state, kv and scratch with fill kernels
     HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
-    HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
-    HIPCHK(q35k::launch_fill_f32(reinterpret_cast<float*>(m->scratch), static_cast<int64_t>(m->scratch_bytes / 4), 0.0f, m->stream));
-    HIPCHK(q35k::launch_rope_table(m->rope_cs, max_ctx, rot_dims(d), d.rope_theta, m->stream));
-    HIPCHK(hipStreamSynchronize(m->stream));
 
     m->budget.weight_bytes = m->w_bytes;
     m->budget.gdn_state_bytes = gdn_bytes;
     m->budget.gdn_conv_bytes = ring_bytes;
-    m->budget.kv_cache_bytes = m->kv_bytes;
-    m->budget.activation_bytes = m->scratch_bytes;
     m->budget.vision_scratch_bytes = 0;
-    *out = m.release();
-    return Q35_OK;
-}
-
-// ------------------------------------------------------------------ chunked prefill
-// Layout of the prompt arena for blocks of `tb` tokens (offsets in floats, 256-B aligned).
-struct PrefillPlan {
-    int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
-    int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
-};
-
-int64_t proj_width(const q35_dims& d) {
-    const int64_t KD = d.gdn_k_heads * 128LL, VD = d.gdn_v_heads * 128LL;
-    return std::max<int64_t>(2 * KD + VD + VD + 2LL * d.gdn_v_heads,
-                             2LL * d.attn_q_heads * d.attn_head_dim + 2LL * d.attn_kv_heads * d.attn_head_dim);
-}
-
-PrefillPlan plan_prefill(const q35_dims& d, int tb) {
-    PrefillPlan p;
-    p.tb = tb;
-    p.lr = std::min(tb, 256);
-    const int64_t H = d.hidden_size, I = d.ffn_intermediate, T = tb;
-    const int64_t VD = d.gdn_v_heads * 128LL, QD = static_cast<int64_t>(d.attn_q_heads) * d.attn_head_dim;
-    int64_t cur = 0;
-    auto take = [&](int64_t n) {
-        const int64_t o = cur;
-        cur += (n + 63) / 64 * 64;
-        return o;
-    };
-    p.hidden = take(T * H);
-    p.xn = take(T * H);
-    p.proj = take(T * proj_width(d));
-    p.mix = take(T * std::max(VD, QD));
-    p.hb = take(T * I);
-    p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
-                         q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
-    p.logits = take(static_cast<int64_t>(p.lr) * d.vocab_size);
-    p.ids = take(T);
-    p.total = cur;
-    return p;
-}
-
-int prefill_block_tokens(const q35_model* m) {
-    const int64_t want = m->pf_block > 0 ? m->pf_block : 4096;
-    return static_cast<int>(std::min<int64_t>(want, m->max_ctx));
-}
-
-q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
-    const int tb = prefill_block_tokens(m);
-    *plan = plan_prefill(m->d, tb);
-    if (m->pf_arena && m->pf_arena_block == tb) return Q35_OK;
-    if (m->pf_arena) {
-        HIPCHK(hipStreamSynchronize(m->stream));
-        HIPCHK(hipFree(m->pf_arena));
-        m->pf_arena = nullptr;
-        m->pf_bytes = 0;
+    st = alloc_context(m.get(), max_ctx);
+    if (st != Q35_OK) return st;
+    if (prefill_block > 0) {
+        st = make_prompt_arena(m.get(), std::min<int64_t>(prefill_block, max_ctx));
+        if (st != Q35_OK) return st;
     }
-    void* p = nullptr;
-    const size_t bytes = static_cast<size_t>(plan->total) * 4;
-    HIPCHK(dev_alloc(&p, bytes));
-    m->pf_arena = static_cast<uint8_t*>(p);
-    m->pf_bytes = bytes;
-    m->pf_arena_block = tb;
-    std::cerr << "[q35] prompt arena: " << (bytes >> 20) << " MiB for blocks of " << tb << " tokens\n";
+    std::cerr << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
+              << " MiB, state " << (m->state_bytes >> 10) << " KiB, kv " << (m->kv_bytes >> 20)
+              << " MiB, scratch " << (m->scratch_bytes >> 10) << " KiB";
+    if (m->pf_arena) std::cerr << ", prompt " << (m->pf_bytes >> 20) << " MiB";
+    std::cerr << "\n";
+    *out = m.release();
     return Q35_OK;
 }
 
@@ -904,14 +997,17 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             });
     }
     if (logits_host) {
-        const int V = d.vocab_size;
+        // the step's output head over vocab_size rows, or (QwenForward::prefill's rule,
+        // src/qwen_forward.cpp:193-199) the embedding over all its rows
+        const int V = m->prefill_head ? static_cast<int>(m->embed_rows) : d.vocab_size;
+        const uint16_t* head = m->prefill_head ? m->embed : m->head;
         for (int r0 = 0; r0 < T; r0 += p.lr) {
             const int rows = std::min(p.lr, T - r0);
             Lr.run(Q35_KT_OTHER, [&] {
                 return q35k::launch_rmsnorm_rows(hidden + static_cast<int64_t>(r0) * H, m->final_norm, xn, rows, H,
                                                  eps, 0, nullptr, s);
             });
-            Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, m->head, rows, V, H, nullptr, lg, V, s); });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, head, rows, V, H, nullptr, lg, V, s); });
             Lr.run(Q35_KT_OTHER, [&] {
                 return hipMemcpyAsync(logits_host + (base + r0) * V, lg, static_cast<size_t>(rows) * V * 4,
                                       hipMemcpyDeviceToHost, s);
@@ -982,12 +1078,13 @@ int64_t q35_device_alloc_count(void) { return g_dev_allocs.load(); }
 
 q35_status q35_model_create(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
                             int64_t max_context, q35_model** out) {
-    return create_model(d, tensors, n_tensors, max_context, 4, out);
+    return create_model(d, tensors, n_tensors, max_context, 4, 0, out);
 }
 
 q35_status q35_model_create_opts(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
                                  int64_t max_context, const q35_model_options* opt, q35_model** out) {
-    return create_model(d, tensors, n_tensors, max_context, opt ? opt->kv_bytes_per_elem : 4, out);
+    return create_model(d, tensors, n_tensors, max_context, opt ? opt->kv_bytes_per_elem : 4,
+                        opt ? opt->prefill_block : 0, out);
 }
 
 q35_status q35_model_open(const char* model_dir, int64_t max_context, q35_model** out) {
@@ -1002,24 +1099,11 @@ q35_status q35_model_open_opts(const char* model_dir, int64_t max_context, const
     SafeTensors st;
     if (!st.load_model(model_dir)) return q35::fail(Q35_ERR_IO, "cannot load safetensors from %s", model_dir);
     std::vector<q35_tensor> table;
-    std::vector<std::string> names;
-    names.reserve(st.entries().size());
-    for (const auto& kv : st.entries()) names.push_back(kv.first);
-    table.reserve(names.size());
-    for (const std::string& nm : names) {
-        const SafeTensors::Entry* e = st.find(nm);
-        q35_tensor t{};
-        t.name = nm.c_str();
-        t.dtype = e->dtype == "BF16" ? 0 : e->dtype == "F32" ? 1 : 2;
-        t.ndim = static_cast<int32_t>(std::min<size_t>(4, e->shape.size()));
-        for (int i = 0; i < t.ndim; ++i) t.shape[i] = e->shape[static_cast<size_t>(i)];
-        t.data = st.data(nm);
-        table.push_back(t);
-    }
+    st.device_table(&table);
     q35_dims d;
     q35::dims_from_config(cfg, &d);
     return create_model(&d, table.data(), static_cast<int32_t>(table.size()), max_context,
-                        opt ? opt->kv_bytes_per_elem : 4, out);
+                        opt ? opt->kv_bytes_per_elem : 4, opt ? opt->prefill_block : 0, out);
 }
 
 void q35_model_destroy(q35_model* m) { destroy(m); }
@@ -1332,7 +1416,37 @@ q35_status q35_model_extend(q35_model* m, const int32_t* ids, int32_t n, float* 
 q35_status q35_model_set_prefill_block(q35_model* m, int32_t tokens) {
     if (!m) return q35::fail(Q35_ERR_ARG, "null model");
     if (tokens < 0 || tokens > (1 << 20)) return q35::fail(Q35_ERR_RANGE, "prefill block %d", tokens);
+    if (m->pf_planned > 0 && tokens > m->pf_planned)
+        return q35::fail(Q35_ERR_RANGE, "prefill block %d beyond the %d tokens the prompt arena was planned for", tokens,
+                         m->pf_planned);
     m->pf_block = tokens;
+    return Q35_OK;
+}
+
+q35_status q35_model_set_prefill_head(q35_model* m, int32_t head) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (head != Q35_HEAD_OUTPUT && head != Q35_HEAD_EMBEDDING) return q35::fail(Q35_ERR_ARG, "prefill head %d", head);
+    m->prefill_head = head;
+    return Q35_OK;
+}
+
+int64_t q35_model_prefill_logits_width(const q35_model* m) {
+    if (!m) return -1;
+    return m->prefill_head ? m->embed_rows : m->d.vocab_size;
+}
+
+q35_status q35_model_reserve_context(q35_model* m, int64_t max_context) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (max_context <= 0 || max_context > (int64_t{1} << 30))
+        return q35::fail(Q35_ERR_RANGE, "max_context %lld out of range", static_cast<long long>(max_context));
+    if (max_context <= m->max_ctx) return Q35_OK;
+    HIPCHK(hipStreamSynchronize(m->stream));
+    drop_graph(m);
+    q35_status st = alloc_context(m, max_context);
+    if (st != Q35_OK) return st;
+    // the recurrent state goes back to zero with the cache: the model is reset
+    HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
     return Q35_OK;
 }
 

@@ -230,6 +230,7 @@ q35_status q35_compute_budget(const q35_dims* d, int32_t bytes_per_weight, int64
     out->kv_cache_bytes = b.kv_cache_bytes;
     out->activation_bytes = b.activation_bytes;
     out->vision_scratch_bytes = b.vision_scratch_bytes;
+    out->prompt_arena_bytes = 0;  // no counterpart in the reference's equation
     return Q35_OK;
 }
 

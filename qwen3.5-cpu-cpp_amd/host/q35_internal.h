@@ -14,6 +14,9 @@ void clear_error();
 const char* last_error_cstr();
 
 void dims_from_config(const ModelConfig& c, q35_dims* d);
+
+// Counts a device allocation the library made (reported by q35_device_alloc_count).
+void count_device_alloc();
 ModelConfig config_from_dims(const q35_dims& d);
 
 }  // namespace q35

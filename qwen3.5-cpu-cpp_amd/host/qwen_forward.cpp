@@ -1,8 +1,11 @@
-// QwenForward over the device runtime: (re)plans a device model sized for the prompt and
-// calls q35_model_prefill. Logits rows cover the embedding rows, as in the reference
-// (src/qwen_forward.cpp:196-199).
+// QwenForward over the device runtime: one device model, made by the first prefill and kept,
+// runs every prompt through the chunked path (q35_model_prefill) with the reference
+// prefill's output head: the embedding over all its rows (src/qwen_forward.cpp:193-199).
+// A longer prompt grows the model's context (q35_model_reserve_context); the weights are
+// uploaded once.
 #include "qwen_forward.h"
 
+#include <algorithm>
 #include <iostream>
 
 #include "q35_internal.h"
@@ -12,32 +15,26 @@ QwenForward::~QwenForward() { q35_model_destroy(m_); }
 bool QwenForward::prefill(const std::vector<int>& ids, std::vector<float>& logits_out) {
     const int seq = static_cast<int>(ids.size());
     if (seq == 0) return false;
-    if (!m_ || planned_ < seq) {
-        q35_model_destroy(m_);
-        m_ = nullptr;
-        std::vector<std::string> names;
-        for (const auto& kv : w_.entries()) names.push_back(kv.first);
+    if (!m_) {
         std::vector<q35_tensor> table;
-        for (const std::string& nm : names) {
-            const SafeTensors::Entry* e = w_.find(nm);
-            q35_tensor t{};
-            t.name = nm.c_str();
-            t.dtype = e->dtype == "BF16" ? 0 : e->dtype == "F32" ? 1 : 2;
-            t.ndim = static_cast<int32_t>(e->shape.size() < 4 ? e->shape.size() : 4);
-            for (int i = 0; i < t.ndim; ++i) t.shape[i] = e->shape[static_cast<size_t>(i)];
-            t.data = w_.data(nm);
-            table.push_back(t);
-        }
+        w_.device_table(&table);
         q35_dims d;
         q35::dims_from_config(cfg_, &d);
-        if (q35_model_create(&d, table.data(), static_cast<int32_t>(table.size()), seq, &m_) != Q35_OK) {
+        if (q35_model_create(&d, table.data(), static_cast<int32_t>(table.size()), std::max(seq, kMinContext), &m_) !=
+                Q35_OK ||
+            q35_model_set_prefill_head(m_, Q35_HEAD_EMBEDDING) != Q35_OK) {
             std::cerr << "[qwen] " << q35_last_error() << "\n";
+            q35_model_destroy(m_);
             m_ = nullptr;
             return false;
         }
-        planned_ = seq;
     }
-    logits_out.assign(static_cast<size_t>(seq) * cfg_.vocab_size, 0.0f);
+    if (seq > q35_model_max_context(m_) &&
+        q35_model_reserve_context(m_, std::max<int64_t>(seq, 2 * q35_model_max_context(m_))) != Q35_OK) {
+        std::cerr << "[qwen] prefill: " << q35_last_error() << "\n";
+        return false;
+    }
+    logits_out.assign(static_cast<size_t>(seq) * static_cast<size_t>(q35_model_prefill_logits_width(m_)), 0.0f);
     std::vector<int32_t> v(ids.begin(), ids.end());
     if (q35_model_prefill(m_, v.data(), seq, logits_out.data()) != Q35_OK) {
         std::cerr << "[qwen] prefill: " << q35_last_error() << "\n";

@@ -2,8 +2,10 @@
 // Whole-prompt forward pass on one MI355X.
 //
 // Drop-in for the reference's include/qwen_forward.h:18-25: prefill(ids, logits) runs the
-// prompt from a zero state and writes [seq * vocab] logits. Device arenas are planned for
-// the prompt length on each call (the reference also allocates its buffers per call).
+// prompt from a zero state and writes [seq * embedding rows] logits from the embedding, as
+// the reference's prefill does (its output head is embed_tokens even when the checkpoint has
+// an lm_head). One device model serves every call: the weights are uploaded at the first
+// prefill, and a longer prompt grows only the KV and scratch arenas.
 #include <vector>
 
 #include "../../include/q35.h"
@@ -24,5 +26,5 @@ private:
     SafeTensors& w_;
     ModelConfig cfg_;
     q35_model* m_ = nullptr;
-    int planned_ = 0;
+    static constexpr int kMinContext = 4096;  // KV capacity of the first device model at least
 };

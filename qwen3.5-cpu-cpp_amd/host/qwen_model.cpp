@@ -8,20 +8,8 @@
 #include "q35_internal.h"
 
 QwenModel::QwenModel(SafeTensors& weights, const ModelConfig& cfg, int max_context) : cfg_(cfg) {
-    std::vector<std::string> names;
-    for (const auto& kv : weights.entries()) names.push_back(kv.first);
     std::vector<q35_tensor> table;
-    table.reserve(names.size());
-    for (const std::string& nm : names) {
-        const SafeTensors::Entry* e = weights.find(nm);
-        q35_tensor t{};
-        t.name = nm.c_str();
-        t.dtype = e->dtype == "BF16" ? 0 : e->dtype == "F32" ? 1 : 2;
-        t.ndim = static_cast<int32_t>(e->shape.size() < 4 ? e->shape.size() : 4);
-        for (int i = 0; i < t.ndim; ++i) t.shape[i] = e->shape[static_cast<size_t>(i)];
-        t.data = weights.data(nm);
-        table.push_back(t);
-    }
+    weights.device_table(&table);
     q35_dims d;
     q35::dims_from_config(cfg_, &d);
     const q35_status st = q35_model_create(&d, table.data(), static_cast<int32_t>(table.size()), max_context, &m_);

@@ -2,15 +2,17 @@
 // Safetensors checkpoint reader (8-byte little-endian header length, a JSON tensor table,
 // then raw little-endian tensor data).
 //
-// Drop-in for the reference's include/safetensors_loader.h:24-74 (same class and methods).
-// Shards are memory-mapped read-only instead of read into heap buffers, so a 3.5 GB
-// checkpoint costs no resident copy until the weights are uploaded to the device.
+// Drop-in for the reference's include/safetensors_loader.h:24-74 (same class and methods,
+// plus device_table). Shards are memory-mapped read-only instead of read into heap buffers,
+// so a 3.5 GB checkpoint costs no resident copy until the weights are uploaded to the
+// device; each tensor's byte range and size are checked against its shard when it loads.
 #include <cstdint>
 #include <cstring>
 #include <string>
 #include <unordered_map>
 #include <vector>
 
+#include "../../include/q35.h"
 #include "weight_view.h"
 
 class SafeTensors {
@@ -46,6 +48,10 @@ public:
     const void* data(const std::string& name) const;
 
     const std::unordered_map<std::string, Entry>& entries() const { return entries_; }
+
+    // The tensor table of q35_model_create: one q35_tensor per entry, pointing at the mapped
+    // bytes (valid while this object lives and is not reloaded).
+    void device_table(std::vector<q35_tensor>* out) const;
 
 private:
     struct Shard {

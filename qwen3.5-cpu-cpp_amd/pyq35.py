@@ -48,7 +48,7 @@ class Dims(C.Structure):
 class Budget(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
         "weight_bytes", "gdn_state_bytes", "gdn_conv_bytes", "kv_cache_bytes",
-        "activation_bytes", "vision_scratch_bytes")]
+        "activation_bytes", "vision_scratch_bytes", "prompt_arena_bytes")]
 
 
 class Tensor(C.Structure):
@@ -75,7 +75,7 @@ class AttnDecodeArgs(C.Structure):
 
 
 class ModelOptions(C.Structure):
-    _fields_ = [("kv_bytes_per_elem", C.c_int32), ("reserved", C.c_int32 * 7)]
+    _fields_ = [("kv_bytes_per_elem", C.c_int32), ("prefill_block", C.c_int32), ("reserved", C.c_int32 * 6)]
 
 
 class GdnPrefillArgs(C.Structure):
@@ -135,6 +135,9 @@ def _load():
         "q35_model_prefill": (S, [P, P, I32, P]),
         "q35_model_extend": (S, [P, P, I32, P, P]),
         "q35_model_set_prefill_block": (S, [P, I32]),
+        "q35_model_set_prefill_head": (S, [P, I32]),
+        "q35_model_prefill_logits_width": (I64, [P]),
+        "q35_model_reserve_context": (S, [P, I64]),
         "q35_model_set_graph": (S, [P, I32]),
         "q35_model_set_layer_trace": (S, [P, I32]),
         "q35_model_read_layer_trace": (S, [P, P]),
@@ -151,6 +154,7 @@ def _load():
         "q35_model_set_position": (S, [P, I64]),
         "q35_model_fill_synthetic": (S, [P, I64, U64, F]),
         "q35_matmul_bf16": (S, [P, P, P, I32, I32, P]),
+        "q35_matmul_f32": (S, [P, P, P, I32, I32, P]),
         "q35_rmsnorm": (S, [P, P, P, I32, I32, F, P]),
         "q35_rmsnorm_gated": (S, [P, P, P, P, I32, I32, F, P]),
         "q35_l2norm": (S, [P, I32, I32, F, P]),
@@ -222,9 +226,11 @@ def synth_normal(n: int, seed: int, stream: int, std: float = 1.0) -> np.ndarray
 class Model:
     """The device-resident decoder (QwenModel on the GPU)."""
 
-    def __init__(self, model_dir: str, max_context: int, kv_bytes_per_elem: int = 4):
+    def __init__(self, model_dir: str, max_context: int, kv_bytes_per_elem: int = 4, prefill_block: int = 0):
+        """max_context 0: planned by the memory equation against the device's memory;
+        prefill_block > 0: the prompt arena is planned at creation for blocks of that size."""
         h = C.c_void_p()
-        opt = ModelOptions(kv_bytes_per_elem=kv_bytes_per_elem)
+        opt = ModelOptions(kv_bytes_per_elem=kv_bytes_per_elem, prefill_block=prefill_block)
         check(lib.q35_model_open_opts(model_dir.encode(), max_context, C.byref(opt), C.byref(h)))
         self.h = h
         d = Dims()
@@ -276,9 +282,21 @@ class Model:
         check(lib.q35_model_decode_greedy(self.h, int(token), n_new, ptr(out)))
         return out[:n_new]
 
+    @property
+    def prefill_logits_width(self) -> int:
+        return lib.q35_model_prefill_logits_width(self.h)
+
+    def set_prefill_head(self, embedding: bool):
+        """Prefill logits from the embedding over all its rows (QwenForward::prefill's rule)
+        instead of the step's output head."""
+        check(lib.q35_model_set_prefill_head(self.h, 1 if embedding else 0))
+
+    def reserve_context(self, max_context: int):
+        check(lib.q35_model_reserve_context(self.h, int(max_context)))
+
     def prefill(self, ids, want_logits: bool = True):
         ids = np.ascontiguousarray(ids, np.int32)
-        lg = np.zeros((len(ids), self.dims.vocab_size), np.float32) if want_logits else None
+        lg = np.zeros((len(ids), self.prefill_logits_width), np.float32) if want_logits else None
         check(lib.q35_model_prefill(self.h, ptr(ids), len(ids), ptr(lg) if want_logits else None))
         return lg
 
@@ -286,7 +304,7 @@ class Model:
         """Chunked prefill of ids at the current position; (logits [n][V], trace [n][L][H])."""
         ids = np.ascontiguousarray(ids, np.int32)
         d = self.dims
-        lg = np.zeros((len(ids), d.vocab_size), np.float32) if want_logits else None
+        lg = np.zeros((len(ids), self.prefill_logits_width), np.float32) if want_logits else None
         tr = np.zeros((len(ids), d.n_layers_total, d.hidden_size), np.float32) if want_trace else None
         check(lib.q35_model_extend(self.h, ptr(ids), len(ids), ptr(lg) if want_logits else None,
                                    ptr(tr) if want_trace else None))
@@ -389,6 +407,7 @@ class Hip:
             "hipEventSynchronize": [P],
             "hipEventElapsedTime": [C.POINTER(C.c_float), P, P],
             "hipGetDeviceCount": [C.POINTER(C.c_int)],
+            "hipMemGetInfo": [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)],
             "hipGetErrorString": [C.c_int],
         }.items():
             fn = getattr(r, name)
@@ -403,6 +422,12 @@ class Hip:
         n = C.c_int(0)
         e = self.rt.hipGetDeviceCount(C.byref(n))
         return n.value if e == 0 else 0
+
+    def mem_info(self):
+        """(free, total) bytes of the current device."""
+        f, t = C.c_size_t(0), C.c_size_t(0)
+        self._ck(self.rt.hipMemGetInfo(C.byref(f), C.byref(t)), "hipMemGetInfo")
+        return f.value, t.value
 
     def malloc(self, nbytes: int) -> int:
         p = C.c_void_p()

@@ -9,6 +9,9 @@ synthetic checkpoints made by q35_synth_write_model and stores small input/outpu
                  reference truncated to 1..L layers), 16 greedy ids, GDN state / conv window /
                  K,V rows after 512 steps, and single-mixer cases with injected state
   tiny_gqa.npz   the same for a shape with v_heads = 2 k_heads and GQA group 4 (decode only)
+  untied_prefill.npz  the reference's QwenForward::prefill logits of the tiny shape with a
+                 separate lm_head: its output head is the embedding (src/qwen_forward.cpp:193-199),
+                 not the lm_head the step uses, over all the embedding's rows
   c1_08b.npz     0.8B shape: checkpoint sha256, prompt, 128 greedy ids,
                  top logits and per-layer residuals at three positions
 
@@ -148,6 +151,25 @@ def tiny_fixture(name: str, prefill: bool):
     print(f"{name}: sha256 {digest}, greedy {greedy.tolist()}")
 
 
+def untied_prefill_fixture():
+    dims = pyq35.dims_for("tiny_untied")
+    with tempfile.TemporaryDirectory() as tmp:
+        mdir = os.path.join(tmp, "tiny_untied")
+        pyq35.synth_write_model(mdir, dims, seed=0, std=0.02)
+        digest = sha256(os.path.join(mdir, "model.safetensors"))
+        prompt = pyq35.synth_token_ids(1, dims.vocab_size, 16)
+        n = len(prompt)
+        r = op.Ref(mdir, 600)
+        pr = r.prefill(prompt)
+        step = np.stack([r.step(int(t)) for t in prompt])
+        r.close()
+    assert pr.shape == (n, dims.vocab_size)
+    np.savez_compressed(os.path.join(OUT, "untied_prefill.npz"), sha256=np.array(digest), prompt=prompt,
+                        prefill_logits=pr, step_logits=step)
+    print(f"untied prefill: sha256 {digest}, rel distance of the two heads "
+          f"{np.linalg.norm(pr - step) / np.linalg.norm(step):.3g}")
+
+
 def c1_fixture(model_root: str):
     dims = pyq35.dims_for("0.8b")
     mdir = os.path.join(model_root, "q35_synth_0.8b_seed0")
@@ -184,13 +206,18 @@ def c1_fixture(model_root: str):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-08b", action="store_true")
+    ap.add_argument("--only", choices=["untied_prefill"], help="write one fixture only")
     ap.add_argument("--model-root", default=tempfile.gettempdir())
     a = ap.parse_args()
     if not op.ref_available():
         sys.exit("oracle/_ref/libq35ref.so missing: build it with make -C oracle (needs the reference tree)")
+    if a.only == "untied_prefill":
+        untied_prefill_fixture()
+        return
     tiny_fixture("tiny", prefill=True)
     tiny_fixture("tiny_gqa", prefill=False)
     tiny_fixture("tiny_untied", prefill=False)
+    untied_prefill_fixture()
     if not a.skip_08b:
         c1_fixture(a.model_root)
 

@@ -128,7 +128,8 @@ def test_memory_equation_matches_reference(tmp_path):
         mine = _budget(dt, bpw, ctx, kvb)
         out = np.zeros(6, np.uint64)
         op.Ref.lib().ref_budget(cfgp.encode(), bpw, ctx, kvb, out.ctypes.data)
-        assert [getattr(mine, k) for k, _ in mine._fields_] == out.tolist()
+        assert [getattr(mine, k) for k, _ in mine._fields_[:6]] == out.tolist()
+        assert mine.prompt_arena_bytes == 0  # the reference has no prompt arena
     args = (10**11, 5 * 10**9, 10**8, 10**7, 0, 10**9, 4)
     assert pyq35.lib.q35_solve_max_context(C.byref(dt), *args) == \
         op.Ref.lib().ref_solve_max_context(cfgp.encode(), *args)
@@ -195,7 +196,7 @@ def test_model_create_rejects_unsupported_shapes(model_dirs):
     d.attn_q_heads = 3
     assert pyq35.lib.q35_model_create(C.byref(d), tab, len(tab), 64, C.byref(h)) == -7
     d = pyq35.dims_for("tiny")
-    assert pyq35.lib.q35_model_create(C.byref(d), tab, len(tab), 0, C.byref(h)) == -6
+    assert pyq35.lib.q35_model_create(C.byref(d), tab, len(tab), -1, C.byref(h)) == -6
     opt = pyq35.ModelOptions(kv_bytes_per_elem=1)
     assert pyq35.lib.q35_model_create_opts(C.byref(d), tab, len(tab), 64, C.byref(opt), C.byref(h)) == -7
     assert b"KV cache element" in pyq35.lib.q35_last_error()
@@ -258,3 +259,24 @@ def test_attn_decode_static_refuses_oversized_partials():
     assert b"static scratch" in pyq35.lib.q35_last_error()
     at.head_dim = 128  # shape checks as q35_attn_decode's
     assert pyq35.lib.q35_attn_decode_static(C.byref(at), None) == -7
+
+
+CALLER = os.path.join(ROOT, "tests", "cpp", "forward_pass_caller")
+
+
+def test_forward_pass_dropin_links_and_exports():
+    """A caller written against the reference's forward_pass.h (include/forward_pass.h:21-54)
+    compiles with the host compiler and links against libq35.so, which exports the six
+    functions with the reference's C++ signatures; its inline activations equal the oracle's."""
+    assert os.path.exists(CALLER), "tests/cpp/forward_pass_caller is not built (make -C tests/cpp)"
+    out = subprocess.run(["nm", "-DC", "--defined-only", pyq35.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    for sig in ("l2norm(float*, int, float)", "matmul(float const*, float const*, float*, int, int)",
+                "matmul(WeightView const&, float const*, float*, int, int)",
+                "rmsnorm(float const*, float const*, float*, int, float)",
+                "rmsnorm_gated(float const*, float const*, float const*, float*, int, float)",
+                "apply_rope(float*, int, int, double)"):
+        assert sig in out, sig
+    r = subprocess.run([CALLER, "--host-only"], capture_output=True, text=True, timeout=60)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr

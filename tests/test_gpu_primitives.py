@@ -78,3 +78,17 @@ def test_l2norm_and_rope(hip):
         # angles in double on both sides: equal up to the fp32 rotation arithmetic
         np.testing.assert_allclose(rp[r], ref, rtol=1e-6, atol=1e-6)
         np.testing.assert_array_equal(rp[r, rot:], x[r, rot:])
+
+
+def test_forward_pass_dropin_vs_oracle():
+    """The forward_pass.h drop-in called from a C++ program built against the header:
+    l2norm, both matmul overloads (the matvec, blocks of rows beyond the staging buffer, rows
+    wider than the matvec, rows not a multiple of 8, fp32 weights), rmsnorm, rmsnorm_gated and
+    apply_rope (odd and full rotary widths) against the oracle, on the GPU."""
+    import os
+    import subprocess
+
+    caller = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "forward_pass_caller")
+    r = subprocess.run([caller], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr

@@ -1,6 +1,8 @@
 """The CPU oracle against the golden vectors written from the compiled reference engine
 (tests/golden/make_golden.py). These pin oracle/oracle.c before it is used as the checker
 of the HIP path."""
+import os
+
 import numpy as np
 import pytest
 
@@ -168,3 +170,19 @@ def test_prefill_handoff_equals_token_serial_steps(model_dirs, name):
     np.testing.assert_array_equal(a.step(int(ids[0])), b.step(int(ids[0])))
     a.close()
     b.close()
+
+
+def test_untied_prefill_uses_the_embedding_head(model_dirs):
+    """QwenForward::prefill's output head is the embedding over all its rows even when the
+    checkpoint has an lm_head (src/qwen_forward.cpp:193-199): the oracle's prefill equals the
+    reference's on the untied checkpoint, and differs from the step's logits (lm_head)."""
+    g = golden("untied_prefill")
+    assert sha256(os.path.join(model_dirs["tiny_untied"], "model.safetensors")) == str(g["sha256"])
+    o = op.Oracle(model_dirs["tiny_untied"], 64)
+    lg = o.prefill(g["prompt"])
+    o.reset()
+    step = np.stack([o.step(int(t)) for t in g["prompt"]])
+    o.close()
+    assert rel_l2(lg, g["prefill_logits"]) < 1e-6
+    assert rel_l2(step, g["step_logits"]) < 1e-6
+    assert rel_l2(g["prefill_logits"], g["step_logits"]) > 0.5
