@@ -96,15 +96,18 @@ def cpu_baseline(model_dir: str, dims, ctx: int, n_steps: int) -> dict:
     log(f"cpu baseline ({kind}) loaded in {time.time() - t_load:.1f} s; timing {n_steps} steps")
     tok = 1
     step(tok)  # untimed warm-up step
-    t0 = time.perf_counter()
+    times = []
     for _ in range(n_steps):
+        t0 = time.perf_counter()
         lg = step(tok)
+        times.append(time.perf_counter() - t0)
         tok = int(np.argmax(lg))
-    dt = time.perf_counter() - t0
+    med = float(np.median(times))
     threads = op.threads()
-    return {"value": n_steps / dt, "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n_steps} greedy decode steps of the same 2B-shaped checkpoint at positions "
-                      f"{ctx + 1}..{ctx + n_steps} (synthetic cache), {dt:.1f} s, OpenMP threads={threads}"}
+    return {"value": 1.0 / med, "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"median of {n_steps} timed greedy decode steps of the same 2B-shaped checkpoint at "
+                      f"positions {ctx + 2}..{ctx + n_steps + 1} (synthetic cache; {sum(times):.1f} s in all, "
+                      f"{min(times) * 1e3:.0f}-{max(times) * 1e3:.0f} ms per step), OpenMP threads={threads}"}
 
 
 def cpu_greedy_baseline(model_dir: str, dims, prompt_len: int, n_steps: int) -> dict:
@@ -121,13 +124,15 @@ def cpu_greedy_baseline(model_dir: str, dims, prompt_len: int, n_steps: int) -> 
     for t in prompt:
         lg = eng.step(int(t))
     tok = int(np.argmax(lg))
-    t0 = time.perf_counter()
+    times = []
     for _ in range(n_steps):
+        t0 = time.perf_counter()
         tok = int(np.argmax(eng.step(tok)))
-    dt = time.perf_counter() - t0
+        times.append(time.perf_counter() - t0)
     eng.close()
-    return {"value": n_steps / dt, "unit": "tok/s", "cores": op.threads(), "kind": kind,
-            "sample": f"{n_steps} greedy steps after the {prompt_len}-token prompt, {dt:.1f} s"}
+    return {"value": 1.0 / float(np.median(times)), "unit": "tok/s", "cores": op.threads(), "kind": kind,
+            "sample": f"median of {n_steps} timed greedy steps after the {prompt_len}-token prompt "
+                      f"({sum(times):.1f} s in all)"}
 
 
 def bench_gdn(a) -> dict:
@@ -379,12 +384,16 @@ def cpu_prefill_baseline(model_dir: str, dims, n_tok: int) -> dict:
     kind = "reference" if op.ref_available() else "port"
     r = op.Ref(model_dir, n_tok + 8) if kind == "reference" else op.Oracle(model_dir, n_tok + 8)
     r.prefill(ids[:1])  # first touch of every weight (the reference widens them once, cached)
-    t0 = time.perf_counter()
-    r.prefill(ids)
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        r.prefill(ids)
+        times.append(time.perf_counter() - t0)
     r.close()
+    dt = float(np.median(times))
     return {"value": n_tok / dt, "unit": "tok/s", "cores": op.threads(), "kind": kind,
-            "sample": f"prefill of the first {n_tok} prompt ids (every row's logits), {dt:.1f} s"}
+            "sample": f"median of 5 prefills of the first {n_tok} prompt ids (every row's logits), "
+                      f"{dt:.2f} s each"}
 
 
 def calibration_copy(nbytes: int = 256 << 20) -> None:
@@ -403,18 +412,20 @@ def calibration_copy(nbytes: int = 256 << 20) -> None:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 64; 256 for --workload long)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--model", choices=["2b", "0.8b"], default="2b",
                     help="decode: 2B shape at --ctx (synthetic cache) or the 0.8B shape after a prompt")
     ap.add_argument("--model-dir", default="", help="checkpoint directory (written when absent)")
     ap.add_argument("--prompt-len", type=int, default=32, help="0.8b decode: prompt tokens")
-    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-steps", type=int, default=5, help="timed CPU steps (the median is reported)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "gdn", "attn", "prefill"], default="decode",
-                    help="decode: full 2B-shaped decode step (default); gdn / attn: isolated mixers; "
-                         "prefill: 2B-shaped whole-prompt prefill")
+    ap.add_argument("--workload", choices=["decode", "long", "gdn", "attn", "prefill"], default="decode",
+                    help="decode: full 2B-shaped decode step (default); long: 2B-shaped decode at the end of "
+                         "a context planned by the memory equation (max_position_embeddings 131072); "
+                         "gdn / attn: isolated mixers; prefill: 2B-shaped whole-prompt prefill")
     ap.add_argument("--prompt", type=int, default=4096, help="prefill: prompt tokens")
     ap.add_argument("--prefill-block", type=int, default=0, help="prefill: tokens per block (0 = auto)")
     ap.add_argument("--cpu-prompt", type=int, default=32, help="prefill: prompt tokens of the CPU sample")
@@ -427,29 +438,48 @@ def main() -> None:
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()
+    if a.steps is None:
+        a.steps = 256 if a.workload == "long" else 64
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
               "(the multi-GPU sharding of the path is a design note, not built)", file=sys.stderr)
         sys.exit(2)
-    if a.workload != "decode":
+    if a.workload not in ("decode", "long"):
         result = {"gdn": bench_gdn, "attn": bench_attn, "prefill": bench_prefill}[a.workload](a)
         if a.calibration_copy:
             calibration_copy()
         print(json.dumps(result), flush=True)
         return
+    bench_decode(a)
 
+
+def bench_decode(a) -> None:
+    """The decode workloads: the 2B shape at --ctx positions of synthetic cache (default), the
+    0.8B shape after a prompt (--model 0.8b), or the 2B shape at the end of a context the
+    library plans itself (--workload long: KV arena sized by solve_max_context against the
+    device's memory, capped by max_position_embeddings = 131072; the cache is filled up to
+    the last warm-up + timed steps)."""
     import pyq35
 
-    small = a.model == "0.8b"
-    d = pyq35.dims_for(a.model)
-    model_dir = a.model_dir or ("/tmp/q35_synth_08b_seed0" if small else "/tmp/q35_synth_2b_seed0")
+    long_ctx = a.workload == "long"
+    small = a.model == "0.8b" and not long_ctx
+    d = pyq35.dims_for("0.8b" if small else "2b")
+    if long_ctx:
+        d.native_max_context = 131072
+    model_dir = a.model_dir or ("/tmp/q35_synth_08b_seed0" if small else
+                                "/tmp/q35_synth_2b_ctx131072_seed0" if long_ctx else "/tmp/q35_synth_2b_seed0")
     ensure_model(model_dir, d, pyq35)
-    ctx = a.prompt_len if small else a.ctx
-    max_ctx = ctx + a.warmup + 2 * a.steps + 4
     t = time.time()
     kv_elem = 2 if a.kv == "bf16" else 4
-    m = pyq35.Model(model_dir, max_ctx, kv_bytes_per_elem=kv_elem)
-    log(f"model uploaded in {time.time() - t:.1f} s; budget {m.budget()}")
+    if long_ctx:
+        m = pyq35.Model(model_dir, 0, kv_bytes_per_elem=kv_elem)
+        max_ctx = m.max_context
+        ctx = max_ctx - a.warmup - 2 * a.steps - 1
+    else:
+        ctx = a.prompt_len if small else a.ctx
+        max_ctx = ctx + a.warmup + 2 * a.steps + 4
+        m = pyq35.Model(model_dir, max_ctx, kv_bytes_per_elem=kv_elem)
+    log(f"model uploaded in {time.time() - t:.1f} s; max_context {max_ctx}; budget {m.budget()}")
     if a.attn_splits:
         m.set_attn_splits(a.attn_splits)
     hip = pyq35.Hip()
@@ -503,7 +533,10 @@ def main() -> None:
     kernels = {k: {"avg_us": 1e3 * v[0] / max(v[1], 1), "launches": v[1]} for k, v in kt.items()}
 
     result = {
-        "metric": METRIC,
+        "metric": (METRIC if not (small or long_ctx) else
+                   "decode tok/s, 0.8B-shaped greedy after a prompt, 1 MI355X" if small else
+                   "decode tok/s + mixer HBM GB/s (%peak), 2B-shaped @131072 ctx (KV planned by "
+                   "solve_max_context), 1 MI355X"),
         "value": a.steps / wall,
         "unit": "tok/s",
         "n_gpus": 1,
@@ -518,11 +551,13 @@ def main() -> None:
                  + (f"{ctx}-token prompt of uniform ids (seed 1) prefilled" if small
                     else "KV cache N(0,1), GDN state N(0,0.1)")),
         "config": {"workload": (f"{'0.8B' if small else '2B'}-shaped Qwen3.5 greedy decode at "
-                                f"{'a ' + str(ctx) + '-token prompt' if small else str(ctx) + ' context'}"),
+                                f"{'a ' + str(ctx) + '-token prompt' if small else str(ctx) + ' context'}"
+                                + (f", KV arena of {max_ctx} positions planned by solve_max_context against "
+                                   f"the device's memory" if long_ctx else "")),
                    "hidden": d.hidden_size, "layers": "24 = 18 GDN + 6 gated attention",
                    "gdn_heads": d.gdn_v_heads, "attn_heads": f"{NQ}q/{NKV}kv x {HD}",
                    "ffn": d.ffn_intermediate, "vocab": d.vocab_size, "context": ctx,
-                   "batch": 1, "kv_cache": a.kv},
+                   "batch": 1, "kv_cache": a.kv, "max_context": max_ctx},
         # the dominant kernel of the step by time: the bf16 matvec (every projection, the FFN
         # and the tied output head; 97 launches per step), bytes = the weights it streams
         "roofline": {"bound": "hbm", "kernel": "bf16 matvec (all projections + output head, per step)",
