@@ -11,14 +11,16 @@
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
 // of it: 2 x 8 MFMA blocks of 16 x 16 (64 accumulator registers per lane). K advances in
-// stages of 32 (one 16x16x32 MFMA deep): the X and W tiles of the next stage are loaded into
-// registers while the current stage runs from LDS (branch-free loads, LDS-only barriers, so
-// the loads stay in flight until the next stage's LDS store needs them). LDS holds the X
-// tile as fp32 ([row][k], rows padded to 36 floats) and the W tile as bf16 ([row][k], rows
-// padded to 40 elements); a wave reads its 8 fp32 k values of an X row (two 16-byte reads)
-// and splits them into the three bf16 A operands in registers, and each W operand is one
-// 16-byte read (16 consecutive rows at either padding hit distinct banks). The split of a
-// value happens once, in the one wave that uses it.
+// stages of 32 (one 16x16x32 MFMA deep).
+//   X (A operand): every X element of the tile is used by one wave only, so each wave loads
+//   its own rows straight from global memory into registers (8 consecutive k per lane, two
+//   16-byte loads per 16-row block), two stages ahead, and splits them in registers.
+//   W (B operand): shared by the four waves, staged through LDS in two buffers (rows padded
+//   to 40 bf16, so the 16 rows one read instruction touches hit distinct banks): stage f + 1
+//   is stored into one buffer while stage f is multiplied from the other, one LDS-only
+//   barrier per stage, and its global loads are issued a stage ahead.
+// LDS traffic is the W reads alone (the X tile no longer passes through LDS): measured 13-18%
+// faster than staging both operands in LDS, with bit-identical results.
 //
 // Accumulation: an MFMA adds its exact products into the accumulator with rounding, 3 K / 16
 // rounded additions per output over K in one fp32 accumulator (384 at K = 2048): four times
@@ -45,10 +47,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBK = 32;
-constexpr int kFlush = 16;    // stages per partial sum (K = 512)
-constexpr int kLdX = kBK + 4;  // padded X row (floats): 144 B, 16-byte reads of 8 rows hit distinct banks
-constexpr int kLd = kBK + 8;   // padded W row (bf16 elements): 80 B
+constexpr int kBM = 128, kBN = 128, kBK = 32;
+constexpr int kFlush = 16;   // stages per partial sum (K = 512)
+constexpr int kLd = kBK + 8;  // padded W row in LDS (bf16 elements): 80 B
+constexpr int kCB = kBN / 16;  // 16-column MFMA blocks per wave (two 16-row blocks)
 
 // the three bf16 parts of two floats a, b, each part's pair packed (a low, b high)
 __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint32_t& m, uint32_t& l) {
@@ -61,65 +63,63 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint3
     l = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xffff0000u);
 }
 
+// One 128 x 128 tile. MASK: some W rows of the tile lie past N or K is not a whole number of
+// flush blocks, so W and X chunks past N or K are zeroed (X rows past M are clamped to row 0
+// and their outputs dropped).
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs.
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
-    constexpr int kBN = 128;
-    __shared__ __align__(16) float Xs[kBM][kLdX];
-    __shared__ __align__(16) uint16_t Ws[kBN][kLd];
+template <int EPI, bool MASK>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (*Ws)[kLd]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-
-    // global -> register mapping: thread t loads X row t / 2 and W row t / 2, k half (t % 2)
-    constexpr int NXQ = kBK / 8, NWQ = kBK / 16;  // 16-byte X / W chunks per thread and stage
-    const int lr = tid >> 1, lk = (tid & 1) * (kBK / 2);
-    const int wr = lr, wk = lk;
-    const bool a_ok = m0 + lr < a.M, b_ok = n0 + wr < a.N;
-    const float* xrow = a.X + static_cast<int64_t>(a_ok ? m0 + lr : 0) * a.ldx;
+    const int l16 = lane & 15, kq = (lane >> 4) * 8;
+    const float* arow[2];  // this lane's X row in each of the wave's two 16-row blocks
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int row = m0 + wave * 32 + 16 * r + l16;
+        arow[r] = a.X + static_cast<int64_t>(row < a.M ? row : 0) * a.ldx;
+    }
+    // W staging: thread t loads 16 k of row t / 2 (half t % 2) of the tile, two 16-byte chunks
+    const int wr = tid >> 1, wk = (tid & 1) * 16;
+    const bool b_ok = n0 + wr < a.N;
     const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + wr : 0) * a.K;
-    // The next stage's X / W tiles are requested into registers right after the current
-    // stage is in LDS and stay in flight while it is multiplied. Loads are unconditional
-    // (clamped to element K - 8 of a valid row); chunks past K or past the last row are
-    // zeroed by a bit mask when the stage is stored. A load or a use under a branch would
-    // make the wait-count pass wait for every outstanding load at the join.
-    // K % 8 == 0: a 4-float or 8-bf16 chunk is wholly inside K or wholly past it (zeros)
-    uint4 raA[NXQ];  // fp32 bit patterns
-    uint4 rbA[NWQ];
-    auto load_stage = [&](uint4 (&ra)[NXQ], uint4 (&rb)[NWQ], int k0) {
+    // Loads are unconditional (addresses clamped into the row) so that no load sits under a
+    // branch: the wait-count pass would then wait for every outstanding load at the join.
+    auto load_a = [&](uint4 (&xa)[2][2], int k0) {
 #pragma unroll
-        for (int i = 0; i < NXQ; ++i)
-            ra[i] = *reinterpret_cast<const uint4*>(xrow + min(k0 + lk + 4 * i, a.K - 4));
+        for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int i = 0; i < NWQ; ++i) rb[i] = *reinterpret_cast<const uint4*>(wrow + min(k0 + wk + 8 * i, a.K - 8));
+            for (int i = 0; i < 2; ++i)
+                xa[r][i] = *reinterpret_cast<const uint4*>(arow[r] + min(k0 + kq + 4 * i, a.K - 4));
     };
-    auto masked = [](uint4 v, bool live) {
-        const uint32_t m = 0u - static_cast<uint32_t>(live);
-        return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+    auto load_w = [&](uint4 (&wb)[2], int k0) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) wb[q] = *reinterpret_cast<const uint4*>(wrow + min(k0 + wk + 8 * q, a.K - 8));
     };
-    auto store_stage = [&](const uint4 (&rx)[NXQ], const uint4 (&rw)[NWQ], int k0) {
+    auto store_w = [&](const uint4 (&wb)[2], int k0, int buf) {
 #pragma unroll
-        for (int i = 0; i < NXQ; ++i)
-            *reinterpret_cast<uint4*>(&Xs[lr][lk + 4 * i]) = masked(rx[i], a_ok && k0 + lk + 4 * i < a.K);
-#pragma unroll
-        for (int q = 0; q < NWQ; ++q)
-            *reinterpret_cast<uint4*>(&Ws[wr][wk + 8 * q]) = masked(rw[q], b_ok && k0 + wk + 8 * q < a.K);
+        for (int q = 0; q < 2; ++q) {
+            uint4 v = wb[q];
+            if constexpr (MASK) {  // K % 8 == 0: a chunk is wholly inside K or wholly past it
+                const uint32_t m = 0u - static_cast<uint32_t>(b_ok && k0 + wk + 8 * q < a.K);
+                v = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+            }
+            *reinterpret_cast<uint4*>(&Ws[buf * kBN + wr][wk + 8 * q]) = v;
+        }
     };
 
-    constexpr int kCB = kBN / 16;  // 16-column MFMA blocks per wave (two 16-row blocks)
     floatx4 acc[2][kCB], part[2][kCB];  // running total, partial sum of the current block
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int j = 0; j < kCB; ++j) acc[r][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    const int l16 = lane & 15, kq = (lane >> 4) * 8;
-    auto mma = [&](auto fresh) {
-        bf16x8 aop[2][3];
+    auto split_a = [&](const uint4 (&xa)[2][2], bf16x8 (&aop)[2][3], int k0) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const int ar = wave * 32 + 16 * r + l16;
-            const float4 x0 = *reinterpret_cast<const float4*>(&Xs[ar][kq]);
-            const float4 x1 = *reinterpret_cast<const float4*>(&Xs[ar][kq + 4]);
+            float4 x0 = __builtin_bit_cast(float4, xa[r][0]), x1 = __builtin_bit_cast(float4, xa[r][1]);
+            if constexpr (MASK) {  // k past K: zeros (the clamped values could be infinite)
+                if (k0 + kq >= a.K) x0 = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k0 + kq + 4 >= a.K) x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
             uint32_t h[4], m[4], l[4];
             split3_pair(x0.x, x0.y, h[0], m[0], l[0]);
             split3_pair(x0.z, x0.w, h[1], m[1], l[1]);
@@ -129,9 +129,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             aop[r][1] = __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]});
             aop[r][2] = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
         }
+    };
+    auto products = [&](const bf16x8 (&aop)[2][3], int buf, auto fresh) {
 #pragma unroll
         for (int j = 0; j < kCB; ++j) {
-            const bf16x8 bop = *reinterpret_cast<const bf16x8*>(&Ws[16 * j + l16][kq]);
+            const bf16x8 bop = *reinterpret_cast<const bf16x8*>(&Ws[buf * kBN + 16 * j + l16][kq]);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
@@ -145,18 +147,31 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
                 }
         }
     };
-    // LDS-only barriers: the next stages' global loads stay in flight through them
-    load_stage(raA, rbA, 0);
+
+    // Stage f: W of stage f is in LDS buffer f % 2, W of stage f + 1 and X of stages f, f + 1
+    // are in registers (in flight). Stages past K hold zero W (MASK) or are never reached
+    // (K a whole number of flush blocks).
+    uint4 xa[2][2][2], wb[2];
+    load_w(wb, 0);
+    load_a(xa[0], 0);
+    load_a(xa[1], kBK);
+    store_w(wb, 0, 0);
+    load_w(wb, kBK);
+    lds_barrier();
     for (int kb = 0; kb < a.K; kb += kFlush * kBK) {
 #pragma unroll
-        for (int f = 0; f < kFlush; ++f) {
-            const int k0 = kb + f * kBK;  // stages past K hold zeros (masked when stored)
-            lds_barrier();  // the previous stage's operands have been read
-            store_stage(raA, rbA, k0);
-            lds_barrier();
-            load_stage(raA, rbA, k0 + kBK);
-            if (f == 0) mma(std::true_type{});
-            else mma(std::false_type{});
+        for (int f = 0; f < kFlush; ++f) {  // kFlush is even: buffer and register set = f % 2
+            const int k0 = kb + f * kBK;
+            store_w(wb, k0 + kBK, (f + 1) & 1);  // its last readers passed the previous barrier
+            load_w(wb, k0 + 2 * kBK);
+            bf16x8 aop[2][3];
+            split_a(xa[f & 1], aop, k0);
+            load_a(xa[f & 1], k0 + 2 * kBK);
+            // keep the loads ahead of the products (the scheduler would sink them)
+            __builtin_amdgcn_sched_barrier(0);
+            if (f == 0) products(aop, f & 1, std::true_type{});
+            else products(aop, f & 1, std::false_type{});
+            lds_barrier();  // LDS only: the loads stay in flight
         }
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -198,10 +213,19 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     }
 }
 
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+    __shared__ __align__(16) uint16_t Ws[2 * kBN][kLd];
+    // tiles whose W rows all lie inside N (with whole flush blocks of K) store W unmasked
+    const bool full = (blockIdx.x + 1) * kBN <= a.N && a.K % (kFlush * kBK) == 0;
+    if (full) gemm_tile<EPI, false>(a, Ws);
+    else gemm_tile<EPI, true>(a, Ws);
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-    dim3 grid((a.N + 127) / 128, (a.M + kBM - 1) / kBM);
+    dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
     if (a.swiglu) klaunch(gemm_kernel<2>, grid, 256, 0, s, a);
     else if (a.R) klaunch(gemm_kernel<1>, grid, 256, 0, s, a);
     else klaunch(gemm_kernel<0>, grid, 256, 0, s, a);
