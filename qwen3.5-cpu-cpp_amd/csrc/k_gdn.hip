@@ -17,6 +17,9 @@
 // the workgroups that share the q/k channels of a k-head can all read the window while
 // one of them (v-head % rep == 0, slice 0) stores the new input, without a race.
 //
+// In the model's decode step the conv window already ran in the in-projection matvec's
+// epilogue (conv_done): q, k and v arrive as SiLU(conv) outputs, and the ring is up to date.
+//
 // With CS = 128 (one workgroup per head) the gated rmsnorm of the readout
 // (src/forward_pass.cpp:86-93) is fused too; with CS = 32 the raw readout is written and
 // the norm runs in the prologue of the out_proj matvec.
@@ -28,7 +31,7 @@ namespace {
 
 constexpr int kD = 128;  // DK == DV
 
-template <int CS, bool FUSE_NORM>
+template <int CS, bool FUSE_NORM, bool CONVD>
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     constexpr int NSPLIT = kD / CS;
     constexpr int NRG = 256 / CS;
@@ -64,14 +67,20 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     // there order LDS only, so the state loads stay in flight through the conv and the norm.
     const int chq = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
     const int chv = 2 * KD + vh * kD + split * CS + (tid % CS);
-    const float4 wq = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chq) * 4);
     const float xq = qkv[chq];
-    const float rq3 = ring[static_cast<int64_t>(s_m3) * CONV + chq], rq2 = ring[static_cast<int64_t>(s_m2) * CONV + chq],
-                rq1 = ring[static_cast<int64_t>(s_m1) * CONV + chq];
-    const float4 wv = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chv) * 4);
     const float xv = qkv[chv];
-    const float rv3 = ring[static_cast<int64_t>(s_m3) * CONV + chv], rv2 = ring[static_cast<int64_t>(s_m2) * CONV + chv],
-                rv1 = ring[static_cast<int64_t>(s_m1) * CONV + chv];
+    float4 wq{}, wv{};
+    float rq3 = 0.f, rq2 = 0.f, rq1 = 0.f, rv3 = 0.f, rv2 = 0.f, rv1 = 0.f;
+    if constexpr (!CONVD) {
+        wq = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chq) * 4);
+        rq3 = ring[static_cast<int64_t>(s_m3) * CONV + chq];
+        rq2 = ring[static_cast<int64_t>(s_m2) * CONV + chq];
+        rq1 = ring[static_cast<int64_t>(s_m1) * CONV + chq];
+        wv = *reinterpret_cast<const float4*>(convw + static_cast<int64_t>(chv) * 4);
+        rv3 = ring[static_cast<int64_t>(s_m3) * CONV + chv];
+        rv2 = ring[static_cast<int64_t>(s_m2) * CONV + chv];
+        rv1 = ring[static_cast<int64_t>(s_m1) * CONV + chv];
+    }
     const int c = tid % CS, rg = tid / CS, r0 = rg * RPT;
     float* Sc = S + split * CS + c;
     float s[RPT];
@@ -81,27 +90,32 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
 
     // causal conv (taps oldest first) + SiLU for the 128 q and 128 k channels of head kh ...
     {
-        float acc = 0.0f;
-        acc += wq.x * rq3;
-        acc += wq.y * rq2;
-        acc += wq.z * rq1;
-        acc += wq.w * xq;
-        const float y = silu_f(acc);
+        float y = xq;
+        if constexpr (!CONVD) {
+            float acc = 0.0f;
+            acc += wq.x * rq3;
+            acc += wq.y * rq2;
+            acc += wq.z * rq1;
+            acc += wq.w * xq;
+            y = silu_f(acc);
+            if (vh % rep == 0 && split == 0) ring[static_cast<int64_t>(s_new) * CONV + chq] = xq;
+        }
         if (tid < kD) q_s[tid] = y;
         else k_s[tid - kD] = y;
-        if (vh % rep == 0 && split == 0) ring[static_cast<int64_t>(s_new) * CONV + chq] = xq;
     }
     // ... and for this slice's v channels
     {
-        float acc = 0.0f;
-        acc += wv.x * rv3;
-        acc += wv.y * rv2;
-        acc += wv.z * rv1;
-        acc += wv.w * xv;
-        if (tid < CS) {
-            v_s[tid] = silu_f(acc);
-            ring[static_cast<int64_t>(s_new) * CONV + chv] = xv;
+        float y = xv;
+        if constexpr (!CONVD) {
+            float acc = 0.0f;
+            acc += wv.x * rv3;
+            acc += wv.y * rv2;
+            acc += wv.z * rv1;
+            acc += wv.w * xv;
+            y = silu_f(acc);
+            if (tid < CS) ring[static_cast<int64_t>(s_new) * CONV + chv] = xv;
         }
+        if (tid < CS) v_s[tid] = y;
     }
     lds_barrier();
 
@@ -193,16 +207,19 @@ hipError_t launch_gdn_decode(const GdnDecodeArgs& in, bool fuse_norm, hipStream_
     if (!a.ls_out) a.ls_out = VD;
     if (fuse_norm) {
         dim3 grid(a.VH, a.n_layers);
-        klaunch(gdn_decode_kernel<128, true>, grid, 256, 0, s, a);
+        if (a.conv_done) klaunch(gdn_decode_kernel<128, true, true>, grid, 256, 0, s, a);
+        else klaunch(gdn_decode_kernel<128, true, false>, grid, 256, 0, s, a);
     } else if (a.n_layers * a.VH * (kD / 64) >= 2 * device_cu_count()) {
         // several layers per launch: 64-column slices still give two workgroups per CU, and
         // fewer, fuller workgroups stream better (18 layers: 0.63 of HBM peak against 0.60
         // with 32 columns; 16 columns: 0.32)
         dim3 grid(a.VH * (kD / 64), a.n_layers);
-        klaunch(gdn_decode_kernel<64, false>, grid, 256, 0, s, a);
+        if (a.conv_done) klaunch(gdn_decode_kernel<64, false, true>, grid, 256, 0, s, a);
+        else klaunch(gdn_decode_kernel<64, false, false>, grid, 256, 0, s, a);
     } else {
         dim3 grid(a.VH * (kD / 32), a.n_layers);
-        klaunch(gdn_decode_kernel<32, false>, grid, 256, 0, s, a);
+        if (a.conv_done) klaunch(gdn_decode_kernel<32, false, true>, grid, 256, 0, s, a);
+        else klaunch(gdn_decode_kernel<32, false, false>, grid, 256, 0, s, a);
     }
     return hipGetLastError();
 }

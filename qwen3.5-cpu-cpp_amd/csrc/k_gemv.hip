@@ -7,6 +7,10 @@
 //   epilogue  y = resid + W x     residual add of the mixer / FFN output
 //             silu(y_2i) y_2i+1   SwiGLU of the interleaved gate / up projection (the
 //                                 down_proj matvec then reads silu(gate) * up directly)
+//             conv + SiLU          GDN in-projection: each conv channel's causal window
+//                                 (QwenModel::gdn_step's conv, src/qwen_model.cpp:173-186)
+//                                 runs once, in the wave that produced the channel, instead
+//                                 of in every mixer workgroup that reads it
 //
 // HBM-bound: every weight byte is read exactly once per step. A 256-thread workgroup
 // stages the transformed input vector in LDS once, then each 64-lane wave streams RPW
@@ -111,13 +115,58 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, int r0, u32x4 (&w)[
     }
 }
 
+// Conv-window inputs of a wave's rows (kEpiConvSilu): the four taps and the raw inputs of the
+// three previous positions (ring slots (pos - 3..pos - 1) % 4), requested early so that the
+// epilogue does not wait for them.
+template <int RPW>
+struct ConvIn {
+    float4 w[RPW];
+    float r3[RPW], r2[RPW], r1[RPW];
+};
+
+template <int RPW>
+__device__ __forceinline__ void load_conv(const GemvArgs& a, int r0, int pos, ConvIn<RPW>& cv) {
+    const int n = a.conv_rows;
+    const int64_t s3 = (pos + 1) & 3, s2 = (pos + 2) & 3, s1 = (pos + 3) & 3;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t ch = min(r0 + r, n - 1);  // rows past the conv channels: unused
+        cv.w[r] = *reinterpret_cast<const float4*>(a.conv_w + ch * 4);
+        cv.r3[r] = a.conv_ring[s3 * n + ch];
+        cv.r2[r] = a.conv_ring[s2 * n + ch];
+        cv.r1[r] = a.conv_ring[s1 * n + ch];
+    }
+}
+
 template <int EPI, int RPW>
-__device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const float (&acc)[RPW]) {
+__device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const float (&acc)[RPW],
+                                           const ConvIn<RPW>& cv, int pos) {
     const int lane = threadIdx.x & 63;
     float sum[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) sum[r] = wave_sum(acc[r]);
     if (lane != 0) return;
+    if (EPI == kEpiConvSilu) {
+        // taps oldest first, the raw projection as the newest input; the raw value goes to
+        // the ring slot of this position (read by the next three steps)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = r0 + r;
+            if (row >= a.rows) continue;
+            if (row < a.conv_rows) {
+                float c = 0.0f;
+                c += cv.w[r].x * cv.r3[r];
+                c += cv.w[r].y * cv.r2[r];
+                c += cv.w[r].z * cv.r1[r];
+                c += cv.w[r].w * sum[r];
+                a.y[row] = silu_f(c);
+                a.conv_ring[static_cast<int64_t>(pos & 3) * a.conv_rows + row] = sum[r];
+            } else {
+                a.y[row] = sum[r];
+            }
+        }
+        return;
+    }
     if (EPI == kEpiSwiGluPair) {
         // rows (2i, 2i + 1) = (gate_i, up_i) of the interleaved [gate|up] matrix
         if (r0 + 1 < a.rows) a.y[r0 >> 1] = silu_f(sum[0]) * sum[RPW - 1];
@@ -133,7 +182,8 @@ __device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const floa
 // chunk of the group is in flight at once.
 template <int EPI, int RPW, int KC, bool PF>
 __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, int r0,
-                                          const u32x4 (&pf)[pf_chunks(KC)][RPW]) {
+                                          const u32x4 (&pf)[pf_chunks(KC)][RPW], const ConvIn<RPW>& cv,
+                                          int pos) {
     const int lane = threadIdx.x & 63;
     float acc[RPW];
 #pragma unroll
@@ -156,7 +206,7 @@ __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, in
 #pragma unroll
             for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[u][r], x0, x1, acc[r]);
         }
-        store_rows<EPI, RPW>(a, r0, acc);
+        store_rows<EPI, RPW>(a, r0, acc, cv, pos);
         return;
     }
     const int n = a.in_dim;
@@ -214,7 +264,7 @@ __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, in
             acc[r] = dot8(w, x0, x1, acc[r]);
         }
     }
-    store_rows<EPI, RPW>(a, r0, acc);
+    store_rows<EPI, RPW>(a, r0, acc, cv, pos);
 }
 
 // Input staged through registers (n <= 1024 NX): the input loads are issued first, then
@@ -295,27 +345,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int row_step = gridDim.x * 4 * RPW;
     int r0 = (blockIdx.x * 4 + wave) * RPW;
+    // the position first (a scalar load: the ring loads below depend on it, and waiting for
+    // it must not wait for the vector loads)
+    const int pos = EPI == kEpiConvSilu ? *a.pos_dev : 0;
     float4 xv[NX > 0 ? NX : 1], gv[NX > 0 ? NX : 1], wv[NX > 0 ? NX : 1];
     if (NX > 0) load_input<PRO>(a, xv, gv, wv);
     // The first row group's weights do not depend on the input: their loads are in flight
     // while the prologue works.
     u32x4 pf[pf_chunks(KC)][RPW];
     load_rows<RPW, KC>(a, r0, pf);  // rows clamped: unconditional, see load_input
+    ConvIn<RPW> cv;
+    if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
     if (NX > 0) finish_input<PRO>(a, xv, gv, wv, xs);
     else stage_input<PRO>(a, xs);
     if (r0 >= a.rows) return;
     if (KC > 0) {
         // one register set: compute the group in `pf`, then load the next one into it
         for (;;) {
-            row_group<EPI, RPW, KC, true>(a, xs, r0, pf);
+            row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos);
             r0 += row_step;
             if (r0 >= a.rows) break;
             load_rows<RPW, KC>(a, r0, pf);
+            if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
         }
         return;
     }
-    row_group<EPI, RPW, KC, true>(a, xs, r0, pf);
-    for (r0 += row_step; r0 < a.rows; r0 += row_step) row_group<EPI, RPW, KC, false>(a, xs, r0, pf);
+    row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos);
+    for (r0 += row_step; r0 < a.rows; r0 += row_step) {
+        if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+        row_group<EPI, RPW, KC, false>(a, xs, r0, pf, cv, pos);
+    }
 }
 
 int gemv_max_blocks() {
@@ -359,6 +418,11 @@ hipError_t launch_rpw(const GemvArgs& a, hipStream_t s) {
 template <int PRO>
 hipError_t launch_pro(const GemvArgs& a, int epi, hipStream_t s) {
     if (epi == kEpiSwiGluPair) return launch_rpw<PRO, kEpiSwiGluPair>(a, s);
+    if (epi == kEpiConvSilu) {
+        if (PRO != kProRmsNorm || !a.conv_w || !a.conv_ring || !a.pos_dev || a.conv_rows <= 0 || a.conv_rows > a.rows)
+            return hipErrorInvalidValue;
+        return launch_rpw<kProRmsNorm, kEpiConvSilu>(a, s);
+    }
     return a.resid ? launch_rpw<PRO, kEpiResidual>(a, s) : launch_rpw<PRO, kEpiStore>(a, s);
 }
 

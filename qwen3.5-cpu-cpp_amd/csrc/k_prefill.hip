@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     float (*Qs)[kLdC] = reinterpret_cast<float (*)[kLdC]>(QA);
     float (*As)[kLdA] = reinterpret_cast<float (*)[kLdA]>(QA);
     __shared__ double gam[kC];
-    __shared__ float beta[kC];
+    __shared__ float beta[kC], edl[kC];
     const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
     for (int f = tid; f < kC * kD / 4; f += 256) {
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     if (tid < kC) {
         const int64_t r = static_cast<int64_t>(vh) * a.Tp + row0 + tid;
         a.Eg[r] = expf(static_cast<float>(gam[tid]));
-        a.Edl[r] = expf(static_cast<float>(gam[kC - 1] - gam[tid]));
+        edl[tid] = expf(static_cast<float>(gam[kC - 1] - gam[tid]));
     }
     // P (j <= i) and A (j < i): S = Q K^T and KK = K K^T over the 128 dims; wave w owns rows
     // [16 w, 16 w + 16) and the 4 blocks of 16 columns; lane (lr, lg) ends with rows
@@ -249,53 +249,62 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     float* dst = (tid < kD ? a.U : a.W) + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + (tid & (kD - 1));
 #pragma unroll
     for (int i = 0; i < kC; ++i) dst[static_cast<int64_t>(i) * kD] = col[i];
+    // the decayed keys of the state update, transposed: Kd[d][t] = K[t][d] e^(gamma_last - gamma_t)
+    float* kd = a.Kd + (static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kD * kC;
+    for (int e = tid; e < kD * kC; e += 256) kd[e] = Ks[e & (kC - 1)][e >> 6] * edl[e & (kC - 1)];
 }
 
 // ------------------------------------------------------------------ GDN state scan
-constexpr int kSW = 16;        // state columns per state-scan workgroup
-constexpr int kLdW = kD + 4;   // -W rows in LDS (A operand: 16 rows x 4 k per read, conflict-free)
-constexpr int kLdK = kD + 16;  // decayed K rows in LDS (A operand read transposed)
+constexpr int kSW = 16;         // state columns per state-scan workgroup
+constexpr int kLdSt = kD + 4;   // state slice in LDS, one row per state column (k contiguous)
+constexpr int kLdW = kD + 4;    // W rows
+constexpr int kLdKt = kC + 4;   // decayed K, transposed: one row per dim (t contiguous)
+constexpr int kLdV = kC + 4;    // v_new, transposed: one row per state column
 
 // grid (VH, 128 / kSW), 512 threads: sequential over the chunks of one state column slice.
 // Per chunk: store the chunk-start state, v_new = U - W S (written over U), then
 // S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Eight waves: v_new rows
 // [16 (w % 4), + 16) over the dims [64 (w / 4), + 64) (the two halves meet through LDS), and
-// the new state rows [16 w, 16 w + 16). The next chunk's W and K are loaded into registers
-// while the current one is computed.
+// the new state rows [16 w, 16 w + 16). The next chunk's W and decayed K are loaded into
+// registers while the current one is computed.
+// Operand layout: every matrix-core operand is read 16 bytes at a time. MFMA i of a 64-deep
+// product takes the reduction index 16 lg + i from lane group lg (i < 16), so a lane's
+// operands for four consecutive MFMAs are four consecutive floats of one LDS row: W rows and
+// the state slice (stored column-major) for v_new, the decayed K (transposed by the chunk
+// pass) and v_new (stored column-major) for the state update.
 constexpr int kSThreads = 512;
 __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int vb = wave & 3, kq = wave >> 2;  // v_new row block and dim half of this wave
-    const int kh = vh / (a.VH / a.KH);
     const int col0 = cs * kSW;
     const int nchunk = a.Tp / kC;
-    __shared__ float Ss[kD][kSW];
-    __shared__ float VN[kC][kSW];
-    __shared__ float VP[kC][kSW];  // partial v_new of the upper dim half
-    __shared__ float Wl[kC][kLdW];
-    __shared__ float Kl[kC][kLdK];
+    __shared__ __align__(16) float St[kSW][kLdSt];
+    __shared__ __align__(16) float Wl[kC][kLdW];
+    __shared__ __align__(16) float Kt[kD][kLdKt];
+    __shared__ __align__(16) float VNt[kSW][kLdV];
+    __shared__ __align__(16) float VPt[kSW][kLdV];  // partial v_new of the upper dim half
     float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
-    for (int i = tid; i < kD * kSW; i += kSThreads) Ss[i / kSW][i % kSW] = S[(i / kSW) * kD + col0 + i % kSW];
+    for (int i = tid; i < kD * kSW; i += kSThreads) St[i & 15][i >> 4] = S[(i >> 4) * kD + col0 + (i & 15)];
 
-    // staging map: float4 f = tid + 512 i (i < 4) of a 64 x 128 chunk -> row f / 32, col 4 (f % 32).
-    // Everything a chunk step reads from global memory (W, K, the cumulative decays and this
-    // lane's U entries) is requested one chunk ahead, so the sequential chain only waits on LDS.
+    // staging: float4 f = tid + 512 i of the chunk's W (64 rows x 128 dims: row f / 32) and of
+    // its decayed, transposed keys (128 dims x 64 rows: dim f / 16). Everything a chunk step
+    // reads from global memory (W, Kd, e^gamma_last and this lane's U entries) is requested
+    // one chunk ahead, so the sequential chain only waits on LDS.
     constexpr int NF = kC * kD / 4 / kSThreads;
-    float4 rw[NF], rk[NF];
-    float rdec[NF], relast, ru[4];  // e^(gamma_last - gamma) of the staged rows, e^gamma_last
+    // (vector-typed: an array of float4 structs here was moved into LDS by the compiler)
+    floatx4 rw[NF], rk[NF];
+    float relast, ru[4];
     auto load_chunk = [&](int c) {
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
-        const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-        const float* edl = a.Edl + static_cast<int64_t>(vh) * a.Tp + row0;
+        const float* Kd = a.Kd + (static_cast<int64_t>(vh) * nchunk + c) * kD * kC;
         const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int f = tid + kSThreads * i;
-            rw[i] = *reinterpret_cast<const float4*>(W + (f >> 5) * kD + (f & 31) * 4);
-            rk[i] = *reinterpret_cast<const float4*>(K + (f >> 5) * kD + (f & 31) * 4);
-            rdec[i] = edl[f >> 5];
+            rw[i] = *reinterpret_cast<const floatx4*>(W + f * 4);
+            rk[i] = *reinterpret_cast<const floatx4*>(Kd + f * 4);
         }
         relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + kC - 1];
 #pragma unroll
@@ -304,16 +313,9 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     auto store_chunk = [&]() {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
-            const int f = tid + kSThreads * i, r = f >> 5, c4 = (f & 31) * 4;
-            const float d = rdec[i];
-            Wl[r][c4 + 0] = -rw[i].x;
-            Wl[r][c4 + 1] = -rw[i].y;
-            Wl[r][c4 + 2] = -rw[i].z;
-            Wl[r][c4 + 3] = -rw[i].w;
-            Kl[r][c4 + 0] = rk[i].x * d;
-            Kl[r][c4 + 1] = rk[i].y * d;
-            Kl[r][c4 + 2] = rk[i].z * d;
-            Kl[r][c4 + 3] = rk[i].w * d;
+            const int f = tid + kSThreads * i;
+            *reinterpret_cast<floatx4*>(&Wl[f >> 5][(f & 31) * 4]) = rw[i];
+            *reinterpret_cast<floatx4*>(&Kt[f >> 4][(f & 15) * 4]) = rk[i];
         }
     };
     load_chunk(0);
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     // load, the prefetch included)
     __syncthreads();  // the state slice is in LDS
     for (int c = 0; c < nchunk; ++c) {
-        lds_barrier();  // previous chunk done with Wl / Kl / Ss
+        lds_barrier();  // previous chunk done with Wl / Kt / St
         store_chunk();
         const float elast = relast;
         floatx4 vn;
@@ -330,52 +332,62 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
         for (int v = 0; v < 4; ++v) vn[v] = ru[v];
         // chunk-start state for the output pass
         float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
-        for (int i = tid; i < kD * kSW; i += kSThreads) Sc[(i / kSW) * kD + i % kSW] = Ss[i / kSW][i % kSW];
+        for (int i = tid; i < kD * kSW; i += kSThreads) Sc[(i >> 4) * kD + (i & 15)] = St[i & 15][i >> 4];
         lds_barrier();
         load_chunk(min(c + 1, nchunk - 1));  // unconditional (the last chunk is requested twice)
 
-        // v_new rows [16 vb, 16 vb + 16) = U - W S, dims [64 kq, 64 kq + 64) in this wave
+        // W S for v_new rows [16 vb, 16 vb + 16), dims [64 kq, 64 kq + 64) in this wave: four
+        // independent accumulation chains (MFMA i on chain i % 4), summed in a fixed order
         floatx4 part;
-        {  // four independent accumulation chains (k-steps interleaved), summed in a fixed order
+        {
             floatx4 ch[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) ch[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int k0 = 64 * kq + 16 * lg;
 #pragma unroll
-            for (int k = 64 * kq; k < 64 * kq + 64; k += 4)
-                ch[(k >> 2) & 3] = mfma4(Wl[16 * vb + lr][k + lg], Ss[k + lg][lr], ch[(k >> 2) & 3]);
+            for (int q = 0; q < 4; ++q) {
+                const float4 wa = *reinterpret_cast<const float4*>(&Wl[16 * vb + lr][k0 + 4 * q]);
+                const float4 sb = *reinterpret_cast<const float4*>(&St[lr][k0 + 4 * q]);
+                ch[0] = mfma4(wa.x, sb.x, ch[0]);
+                ch[1] = mfma4(wa.y, sb.y, ch[1]);
+                ch[2] = mfma4(wa.z, sb.z, ch[2]);
+                ch[3] = mfma4(wa.w, sb.w, ch[3]);
+            }
             part = (ch[0] + ch[1]) + (ch[2] + ch[3]);
         }
-        if (kq == 1)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) VP[16 * vb + 4 * lg + v][lr] = part[v];
+        if (kq == 1) *reinterpret_cast<floatx4*>(&VPt[lr][16 * vb + 4 * lg]) = part;
         lds_barrier();
         if (kq == 0) {
             float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
+            const floatx4 hi = *reinterpret_cast<const floatx4*>(&VPt[lr][16 * vb + 4 * lg]);
+            floatx4 x;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float x = vn[v] + (part[v] + VP[16 * vb + 4 * lg + v][lr]);
-                U[(16 * vb + 4 * lg + v) * kD + lr] = x;
-                VN[16 * vb + 4 * lg + v][lr] = x;
+                x[v] = vn[v] - (part[v] + hi[v]);
+                U[(16 * vb + 4 * lg + v) * kD + lr] = x[v];
             }
+            *reinterpret_cast<floatx4*>(&VNt[lr][16 * vb + 4 * lg]) = x;
         }
-        lds_barrier();  // VN complete, every wave done reading Ss
+        lds_barrier();  // VNt complete, every wave done reading St
 
-        // new state rows [16 w, 16 w + 16)
-        const float dl = elast;
-        float* srow = &Ss[16 * wave + 4 * lg][lr];
-        floatx4 sn;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sn[v] = srow[v * kSW] * dl;
+        // new state rows [16 w, 16 w + 16): rows 16 w + 4 lg + v of column lr in this lane
+        floatx4 sn = *reinterpret_cast<const floatx4*>(&St[lr][16 * wave + 4 * lg]);
+        sn = sn * elast;
         floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int t = 0; t < kC; t += 4)
-            ch[(t >> 2) & 1] = mfma4(Kl[t + lg][16 * wave + lr], VN[t + lg][lr], ch[(t >> 2) & 1]);
+        for (int q = 0; q < 4; ++q) {
+            const float4 ka = *reinterpret_cast<const float4*>(&Kt[16 * wave + lr][16 * lg + 4 * q]);
+            const float4 vv = *reinterpret_cast<const float4*>(&VNt[lr][16 * lg + 4 * q]);
+            ch[0] = mfma4(ka.x, vv.x, ch[0]);
+            ch[1] = mfma4(ka.y, vv.y, ch[1]);
+            ch[0] = mfma4(ka.z, vv.z, ch[0]);
+            ch[1] = mfma4(ka.w, vv.w, ch[1]);
+        }
         sn = sn + (ch[0] + ch[1]);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) srow[v * kSW] = sn[v];
+        *reinterpret_cast<floatx4*>(&St[lr][16 * wave + 4 * lg]) = sn;
     }
     __syncthreads();
-    for (int i = tid; i < kD * kSW; i += kSThreads) S[(i / kSW) * kD + col0 + i % kSW] = Ss[i / kSW][i % kSW];
+    for (int i = tid; i < kD * kSW; i += kSThreads) S[(i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
 }
 
 // ------------------------------------------------------------------ GDN chunk output
@@ -827,7 +839,8 @@ int blocks_for(int64_t n) {
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T) {
     const int64_t Tp = (T + kC - 1) / kC * kC;
     return (2 * KH + 3 * static_cast<int64_t>(VH)) * Tp * kD  // Qg Kg Vg U W
-           + 4 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Eg Edl
+           + 3 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Eg
+           + static_cast<int64_t>(VH) * Tp * kD                // Kd
            + static_cast<int64_t>(VH) * Tp * kC                // P
            + static_cast<int64_t>(VH) * (Tp / kC) * kD * kD    // Sc (chunk-start states)
            + 64 * 9;                                           // alignment slack
@@ -848,7 +861,7 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
     a.Bg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Gg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Eg = take(static_cast<int64_t>(a.VH) * a.Tp);
-    a.Edl = take(static_cast<int64_t>(a.VH) * a.Tp);
+    a.Kd = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
     a.P = take(static_cast<int64_t>(a.VH) * a.Tp * kC);
     a.Sc = take(static_cast<int64_t>(a.VH) * (a.Tp / kC) * kD * kD);
 }

@@ -48,10 +48,18 @@ struct GemvArgs {
     float* y;
     int rows, in_dim, head_dim;
     float eps;
+    // kEpiConvSilu: rows [0, conv_rows) are the GDN conv channels; the epilogue runs their
+    // causal conv window (conv_w [conv_rows][4], ring [4][conv_rows], slot = position % 4 at
+    // *pos_dev) and stores SiLU of it, and writes the raw projection into the ring
+    const float* conv_w;
+    float* conv_ring;
+    const int* pos_dev;
+    int conv_rows;
 };
 // Epilogue: store y, add the residual (the default when resid is set), or, for an
-// interleaved [gate_0; up_0; gate_1; up_1; ...] matrix, y[i] = silu(row 2i) * row 2i+1.
-enum GemvEpilogue : int { kEpiAuto = -1, kEpiStore = 0, kEpiResidual = 1, kEpiSwiGluPair = 2 };
+// interleaved [gate_0; up_0; gate_1; up_1; ...] matrix, y[i] = silu(row 2i) * row 2i+1, or
+// the GDN in-projection's conv window + SiLU on its conv rows (kEpiConvSilu).
+enum GemvEpilogue : int { kEpiAuto = -1, kEpiStore = 0, kEpiResidual = 1, kEpiSwiGluPair = 2, kEpiConvSilu = 3 };
 hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue = kEpiAuto);
 // Largest in_dim the matvec stages in LDS.
 constexpr int kGemvMaxIn = 16384;
@@ -80,6 +88,7 @@ struct GdnDecodeArgs {
     const float *qkv, *z, *b, *a;                 // per-layer contiguous inputs
     const float *conv_w, *A_log, *dt_bias, *norm_w;
     float *conv_ring, *state, *out;
+    int conv_done;  // qkv already holds SiLU(conv) (the in-projection ran the window); no ring update
     // per-layer strides in elements (0 = derive the contiguous stride)
     int64_t ls_qkv, ls_z, ls_ba, ls_convw, ls_vh, ls_normw, ls_ring, ls_state, ls_out;
 };
@@ -167,9 +176,10 @@ struct GdnPrefillArgs {
     const float *conv_w, *A_log, *dt_bias, *norm_w;  // norm_w null: raw readout
     float *conv_ring, *state;
     float* out;        // [T][VH * 128]
-    // workspace (head-major, padded to Tp rows); Eg = e^gamma and Edl = e^(gamma_last - gamma)
-    // of each row, gamma the chunk-local cumulative decay
-    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Edl, *P;
+    // workspace (head-major, padded to Tp rows); Eg = e^gamma of each row, gamma the
+    // chunk-local cumulative decay; Kd = K e^(gamma_last - gamma) per (v-head, chunk),
+    // transposed ([128 dims][64 rows])
+    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Kd, *P;
     float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
 };
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);

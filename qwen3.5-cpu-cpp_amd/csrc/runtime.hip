@@ -346,7 +346,15 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
         g.rows = ly.in_rows;
         g.in_dim = H;
         g.eps = d.rms_norm_eps;
-        L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(g, q35k::kProRmsNorm, s); });
+        if (!ly.attn) {  // the conv window runs in the in-projection's epilogue
+            g.conv_w = ly.conv_w;
+            g.conv_ring = m->conv_ring + static_cast<int64_t>(ly.idx) * 4 * CONV;
+            g.pos_dev = m->pos_dev;
+            g.conv_rows = CONV;
+        }
+        L.run(Q35_KT_GEMV, [&] {
+            return q35k::launch_gemv(g, q35k::kProRmsNorm, s, ly.attn ? q35k::kEpiAuto : q35k::kEpiConvSilu);
+        });
         if (!ly.attn) {
             q35k::GdnDecodeArgs ga{};
             ga.n_layers = 1;
@@ -366,6 +374,7 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
             ga.conv_ring = m->conv_ring + static_cast<int64_t>(ly.idx) * 4 * CONV;
             ga.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
             ga.out = m->mix;
+            ga.conv_done = 1;
             L.run(Q35_KT_GDN_DECODE, [&] { return q35k::launch_gdn_decode(ga, false, s); });
             q35k::GemvArgs o{};
             o.W = ly.w_out;
