@@ -23,13 +23,14 @@
 //            The delta rule is column-separable, so the 8 slices of a head are independent.
 //   output   per (v-head, chunk), in parallel: o = e^gamma (Q S_c) + P v_new on the matrix
 //            cores, then rmsnorm_gated per (token, v-head) (src/forward_pass.cpp:86-93).
-// Causal attention, flash form on the matrix cores (v_mfma_f32_16x16x4_f32):
+// Causal attention, flash form on the bf16 matrix cores:
 //   prep     q_norm + RoPE of every query row (head-major), k_norm + RoPE of every key and
 //            the values appended to the KV cache at pos0 + t (angles in double; a bf16 cache
 //            stores them rounded to nearest even and the flash kernel widens them back).
 //   flash    grid (query tiles of 64, NQ): 4 waves of 16 query rows with their q in
-//            registers; 32-position K / V tiles in LDS; S = Q K^T and O += P V on MFMA;
-//            running max / sum per row; epilogue O / l * sigmoid(gate).
+//            registers (as three bf16 parts); 16-position K / V tiles in LDS (split into
+//            bf16 parts when staged); S = Q K^T and O += P V on the bf16 matrix cores from
+//            six part products each; running max / sum per row; epilogue O / l * sigmoid(gate).
 #include <math.h>
 
 #include "dev_common.hpp"
@@ -638,24 +639,49 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 }
 
 // ------------------------------------------------------------------ flash attention
-// 64 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
-// the cache. Per tile of 32 keys, two 16-key blocks: S^T = K Q^T on v_mfma_f32_16x16x4_f32
-// with the keys as rows, so a lane's score registers (keys 4g + v of its block, query row
-// l % 16) are directly the A operand of O += P V for k-step v; the head dims are permuted
-// consistently (dims 16c + 4g + i of a k-step, dims 64t + 4(l%16) + i of an output tile) so
-// every LDS operand read is one 16-byte vector. The next tile's K / V rows are loaded into
-// registers while the current one is computed.
 constexpr int kQT = 64;   // query rows per workgroup (16 per wave)
-constexpr int kKT = 32;   // key / value positions per tile
-constexpr int kLd = kHD + 4;
+
+// 64 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
+// the cache, 16-key tiles staged through LDS (the next tile's rows are loaded into registers
+// while the current one is multiplied), online softmax. Causal work grows with the query
+// block: workgroups are dispatched in linear order, S of them resident at once, ids c and
+// c + S/2 of a dispatch round on the same CU; work items are ranked longest first, and within
+// each full round of S the second half takes the ranks in reverse, so the two workgroups of a
+// CU carry complementary amounts of work (later rounds bring the shorter items).
+// Both products run on the bf16 matrix cores: every fp32 operand
+// is the exact sum of three bf16 parts (hi + mid + lo, as in the projection GEMM), and a
+// product a.b is the sum of the six part products a_i b_j with i + j <= 2 (parts counted
+// from 0): the three dropped ones (mid.lo, lo.mid, lo.lo) are below 2^-23 |a||b| together,
+// the size of an fp32 rounding, and each bf16 x bf16 part product is exact in fp32. A bf16
+// cache holds K and V exactly, so only Q and P are split (three products each). Six bf16
+// products cost 6/16 of one fp32 product on the matrix cores.
+//   S^T = K Q^T per 16-key tile on v_mfma_f32_16x16x32_bf16: keys as rows (K parts from LDS,
+//         8 consecutive dims per lane), the lane's own query row as the column (Q parts in
+//         registers, split once); lane (r16, g) ends with keys 4g + v of query r16.
+//   O += P V on v_mfma_f32_16x16x16_bf16: those four scores are the A operand (query r16,
+//         keys 4g .. 4g + 3) without data movement; V parts come from an LDS copy stored
+//         dim-major (keys 4g .. 4g + 3 of dim 16t + r16: one 8-byte read); lane (r16, g)
+//         ends with dims 16t + r16 of queries 4g + v.
+constexpr int kKT2 = 16;          // keys per tile
+constexpr int kLdK2 = kHD + 8;    // K part rows (bf16): 528 B, the 16 rows of a read on distinct banks
+constexpr int kLdV2 = kKT2 + 4;   // V part rows, dim-major (bf16): 40 B
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// the three bf16 parts of four floats, each part as four packed bf16 (element 0 low)
+__device__ __forceinline__ void split3_4(const float (&x)[4], uint2 (&part)[3]) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) split3(x[e], h[e], m[e], l[e]);
+    part[0] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    part[1] = make_uint2(m[0] | (m[1] << 16), m[2] | (m[3] << 16));
+    part[2] = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+}
 
 template <bool KVB>
-__global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
-    // Causal work grows with the query block. Workgroups are dispatched in linear order, S
-    // of them resident at once, ids c and c + S/2 of a dispatch round on the same CU. Work
-    // items are ranked longest first; within each full round of S the second half takes
-    // the ranks in reverse, so the two workgroups of a CU carry complementary amounts of
-    // work, and later rounds (more workgroups than slots) bring the shorter items.
+__global__ __launch_bounds__(256, 2) void flash_attn_split_kernel(AttnPrefillArgs a) {
+    constexpr int NP = KVB ? 1 : 3;  // parts of K and V
     const int nqt = gridDim.x, nlin = gridDim.x * gridDim.y;
     const int L = blockIdx.x + blockIdx.y * nqt, S = max(2, a.wg_slots & ~1);
     const int round0 = L - L % S, r = L - round0;
@@ -663,87 +689,138 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
     const int qt = nqt - 1 - rank / a.NQ, h = rank % a.NQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = a.NQ / a.NKV, kh = h / grp;
-    const int t0 = qt * kQT;                  // first query row (block-relative)
+    const int t0 = qt * kQT;
     const int r16 = lane & 15, g4 = lane >> 4;
-    __shared__ float Ks[kKT][kLd], Vs[kKT][kLd];
+    __shared__ __align__(16) uint16_t Kp[NP][kKT2][kLdK2];
+    __shared__ __align__(16) uint16_t Vt[NP][kHD][kLdV2];
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
-    // this lane's query row (the B operand column): Q[row r16][16c + 4 g4 + i]
-    const int qrow = t0 + wave * 16 + r16;  // block-relative
-    float4 qv[16];
+    // this lane's query row, dims 32c + 8 g4 .. + 7, as three bf16 parts (the B operand)
+    const int qrow = t0 + wave * 16 + r16;
+    bf16x8 qp[3][8];
     {
-        const float* src = a.Qa + (static_cast<int64_t>(h) * a.T + min(qrow, a.T - 1)) * kHD + 4 * g4;
+        const float* src = a.Qa + (static_cast<int64_t>(h) * a.T + min(qrow, a.T - 1)) * kHD + 8 * g4;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) qv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
+        for (int c = 0; c < 8; ++c) {
+            const float4 x0 = *reinterpret_cast<const float4*>(src + 32 * c);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + 32 * c + 4);
+            const float v0[4] = {x0.x, x0.y, x0.z, x0.w}, v1[4] = {x1.x, x1.y, x1.z, x1.w};
+            uint2 p0[3], p1[3];
+            split3_4(v0, p0);
+            split3_4(v1, p1);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                qp[p][c] = __builtin_bit_cast(bf16x8, make_uint4(p0[p].x, p0[p].y, p1[p].x, p1[p].y));
+        }
     }
-    const int qpos = a.pos0 + qrow;  // absolute position of this lane's query row
-    floatx4 o[16];
+    const int qpos = a.pos0 + qrow;
+    floatx4 o[16];  // dims 16 t + r16 of query rows 4 g4 + v
 #pragma unroll
     for (int t = 0; t < 16; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f;  // of query row r16 (same in the 4 lane groups)
+    float m_run = -INFINITY, l_run = 0.0f;
 
-    const int kv_end = a.pos0 + min(a.T, t0 + kQT);  // exclusive, causal for the tile
-    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
-    // staging of one tile: thread tid holds rows tid / 64 + 4 j (j < 8), float4 column lane
-    constexpr int SR = kKT / 4;
-    float4 kst[SR], vst[SR];
+    const int kv_end = a.pos0 + min(a.T, t0 + kQT);
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    // staging of one tile, in registers while the previous tile is multiplied: K rows
+    // tid / 16, dims 16 (tid % 16) .. + 15 (four float4); V keys 4 (tid / 64) .. + 3, dims
+    // 4 (tid % 64) .. + 3 (one float4 per key); split (or widened) when stored to LDS
+    const int ks_row = tid >> 4, ks_d = (tid & 15) * 16;
+    const int vs_k = (tid >> 6) * 4, vs_d = (tid & 63) * 4;
+    float4 kst[4], vst[4];
     auto load_tile = [&](int kv0) {
         const bool live = kv0 < kv_end;
 #pragma unroll
-        for (int j = 0; j < SR; ++j) {
-            const int p = min(kv0 + wave + 4 * j, kv_end - 1);
-            const int64_t off = live ? static_cast<int64_t>(p) * kHD + 4 * lane : 0;  // past the end: one line
+        for (int j = 0; j < 4; ++j) {
+            const int pk = min(kv0 + ks_row, kv_end - 1), pv = min(kv0 + vs_k + j, kv_end - 1);
+            const int64_t ok = live ? static_cast<int64_t>(pk) * kHD + ks_d + 4 * j : 0;
+            const int64_t ov = live ? static_cast<int64_t>(pv) * kHD + vs_d : 0;
             if constexpr (KVB) {
-                const uint2 kb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff + off);
-                const uint2 vb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff + off);
+                const uint2 kb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff + ok);
+                const uint2 vb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff + ov);
                 kst[j] = make_float4(bf16_lo(kb.x), bf16_hi(kb.x), bf16_lo(kb.y), bf16_hi(kb.y));
                 vst[j] = make_float4(bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y));
             } else {
-                kst[j] = *reinterpret_cast<const float4*>(a.k_cache + hoff + off);
-                vst[j] = *reinterpret_cast<const float4*>(a.v_cache + hoff + off);
+                kst[j] = *reinterpret_cast<const float4*>(a.k_cache + hoff + ok);
+                vst[j] = *reinterpret_cast<const float4*>(a.v_cache + hoff + ov);
             }
         }
     };
     auto store_tile = [&](int kv0) {
+        // K: rows past the end are zero (their scores are masked anyway)
+        const bool kok = kv0 + ks_row < kv_end;
 #pragma unroll
-        for (int j = 0; j < SR; ++j) {
-            const int r = wave + 4 * j;
-            const bool ok = kv0 + r < kv_end;  // rows past the end are zero (masked anyway)
-            *reinterpret_cast<float4*>(&Ks[r][4 * lane]) = ok ? kst[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            *reinterpret_cast<float4*>(&Vs[r][4 * lane]) = ok ? vst[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < 4; ++j) {
+            const float x[4] = {kok ? kst[j].x : 0.f, kok ? kst[j].y : 0.f, kok ? kst[j].z : 0.f, kok ? kst[j].w : 0.f};
+            if constexpr (KVB) {
+                *reinterpret_cast<uint2*>(&Kp[0][ks_row][ks_d + 4 * j]) =
+                    make_uint2(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
+                               __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u));
+            } else {
+                uint2 pt[3];
+                split3_4(x, pt);
+#pragma unroll
+                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Kp[p][ks_row][ks_d + 4 * j]) = pt[p];
+            }
+        }
+        // V, transposed: dim vs_d + e gets the four keys vs_k .. + 3 (zero past the end: 0 * V
+        // must stay 0, and P is 0 there)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float x[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = vst[j];
+                const float ve = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+                x[j] = kv0 + vs_k + j < kv_end ? ve : 0.0f;
+            }
+            if constexpr (KVB) {
+                *reinterpret_cast<uint2*>(&Vt[0][vs_d + e][vs_k]) =
+                    make_uint2(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
+                               __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u));
+            } else {
+                uint2 pt[3];
+                split3_4(x, pt);
+#pragma unroll
+                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Vt[p][vs_d + e][vs_k]) = pt[p];
+            }
         }
     };
     load_tile(0);
     store_tile(0);
     lds_barrier();
-    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
-        load_tile(kv0 + kKT);  // in flight during this tile's products
-        float sv[2][4];
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT2) {
+        load_tile(kv0 + kKT2);  // in flight during this tile's products
+        // S^T[key 4 g4 + v][query r16]: the hi.hi products and the smaller part products in
+        // separate accumulators, each split over even / odd dim blocks (four chains)
+        floatx4 sa[2], sb[2];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            floatx4 S4[4];
+        for (int e = 0; e < 2; ++e) sa[e] = sb[e] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < 8; ++c) {
+            bf16x8 kop[NP];
 #pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const float4 k = *reinterpret_cast<const float4*>(&Ks[b * 16 + r16][16 * c + 4 * g4]);
-                S4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.x, qv[c].x, S4[0], 0, 0, 0);
-                S4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.y, qv[c].y, S4[1], 0, 0, 0);
-                S4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.z, qv[c].z, S4[2], 0, 0, 0);
-                S4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(k.w, qv[c].w, S4[3], 0, 0, 0);
+            for (int p = 0; p < NP; ++p) kop[p] = *reinterpret_cast<const bf16x8*>(&Kp[p][r16][32 * c + 8 * g4]);
+            floatx4& b = sb[c & 1];
+            if constexpr (KVB) {
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
+            } else {
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[2 % NP], qp[0][c], b, 0, 0, 0);
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[1][c], b, 0, 0, 0);
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[0][c], b, 0, 0, 0);
+                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
             }
-            const floatx4 S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int key = kv0 + b * 16 + 4 * g4 + v;  // S^T[key][query r16]
-                sv[b][v] = key <= qpos && key < kv_end ? S[v] * sc : -INFINITY;
-            }
+            sa[c & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[0][c], sa[c & 1], 0, 0, 0);
         }
-        float tm = -INFINITY;
+        const floatx4 St = (sb[0] + sb[1]) + (sa[0] + sa[1]);
+        float sv[4];
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) tm = fmaxf(tm, sv[b][v]);
+        for (int v = 0; v < 4; ++v) {
+            const int key = kv0 + 4 * g4 + v;
+            sv[v] = key <= qpos && key < kv_end ? St[v] * sc : -INFINITY;
+        }
+        float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         tm = fmaxf(tm, __shfl_xor(tm, 16));
         tm = fmaxf(tm, __shfl_xor(tm, 32));
         // the reference max moves only when a score exceeds it by more than 8; a row with no
@@ -751,14 +828,12 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
         const float m_new = tm > m_run + 8.0f ? tm : m_run;
         const bool live = m_new != -INFINITY;
         const float f = live ? expf(m_run - m_new) : 1.0f;
-        float p[2][4], ps = 0.0f;
+        float p[4], ps = 0.0f;
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                p[b][v] = live ? expf(sv[b][v] - m_new) : 0.0f;
-                ps += p[b][v];
-            }
+        for (int v = 0; v < 4; ++v) {
+            p[v] = live ? expf(sv[v] - m_new) : 0.0f;
+            ps += p[v];
+        }
         ps += __shfl_xor(ps, 16);
         ps += __shfl_xor(ps, 32);
         l_run = l_run * f + ps;
@@ -766,7 +841,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
         if (__any(f != 1.0f)) {  // rescale output rows 4 g4 + r
             float fr[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) fr[r] = __shfl(f, 4 * g4 + r);
+            for (int rr = 0; rr < 4; ++rr) fr[rr] = __shfl(f, 4 * g4 + rr);
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
                 o[t][0] *= fr[0];
@@ -775,46 +850,50 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnPrefillArgs a) {
                 o[t][3] *= fr[3];
             }
         }
-        // O[query row][64 t + 4 r16 + i] += P[query row][key] V[key][.]
+        // O[query 4 g4 + v][dim 16 t + r16] += P[query][keys 4 g4 ..] V[keys][dim]
+        uint2 pp[3];
+        split3_4(p, pp);
+        const short4_t pa0 = __builtin_bit_cast(short4_t, pp[0]), pa1 = __builtin_bit_cast(short4_t, pp[1]),
+                       pa2 = __builtin_bit_cast(short4_t, pp[2]);
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int t = 0; t < 16; ++t) {
+            short4_t vb[NP];
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const float4 vv = *reinterpret_cast<const float4*>(&Vs[b * 16 + 4 * g4 + v][64 * t + 4 * r16]);
-                    o[4 * t + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.x, o[4 * t + 0], 0, 0, 0);
-                    o[4 * t + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.y, o[4 * t + 1], 0, 0, 0);
-                    o[4 * t + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.z, o[4 * t + 2], 0, 0, 0);
-                    o[4 * t + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[b][v], vv.w, o[4 * t + 3], 0, 0, 0);
-                }
+            for (int q = 0; q < NP; ++q)
+                vb[q] = __builtin_bit_cast(short4_t, *reinterpret_cast<const uint2*>(&Vt[q][16 * t + r16][4 * g4]));
+            floatx4 ob = floatx4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (KVB) {
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa2, vb[0], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[0], ob, 0, 0, 0);
+            } else {
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa2, vb[0], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[1 % NP], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[2 % NP], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[0], ob, 0, 0, 0);
+                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[1 % NP], ob, 0, 0, 0);
+            }
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[0], o[t] + ob, 0, 0, 0);
+        }
         lds_barrier();  // every wave is done with this tile
-        if (kv0 + kKT < kv_end) {
-            store_tile(kv0 + kKT);
+        if (kv0 + kKT2 < kv_end) {
+            store_tile(kv0 + kKT2);
             lds_barrier();
         }
     }
-    // epilogue: lane holds rows 4 g4 + r, dims 64 t + 4 r16 + i
     float lr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) lr[r] = __shfl(l_run, 4 * g4 + r);
+    for (int rr = 0; rr < 4; ++rr) lr[rr] = __shfl(l_run, 4 * g4 + rr);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int t = t0 + wave * 16 + 4 * g4 + r;
+    for (int rr = 0; rr < 4; ++rr) {
+        const int t = t0 + wave * 16 + 4 * g4 + rr;
         if (t >= a.T) continue;
-        const float inv = 1.0f / lr[r];
+        const float inv = 1.0f / lr[rr];
         const float* gate = a.qkv + static_cast<int64_t>(t) * a.ld_qkv + static_cast<int64_t>(h) * 2 * kHD + kHD;
         float* out = a.out + static_cast<int64_t>(t) * (a.NQ * kHD) + static_cast<int64_t>(h) * kHD;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const int dd = 64 * tt + 4 * r16;
-            const float4 gv = *reinterpret_cast<const float4*>(gate + dd);
-            float4 y;
-            y.x = (o[4 * tt + 0][r] * inv) * sigmoid_f(gv.x);
-            y.y = (o[4 * tt + 1][r] * inv) * sigmoid_f(gv.y);
-            y.z = (o[4 * tt + 2][r] * inv) * sigmoid_f(gv.z);
-            y.w = (o[4 * tt + 3][r] * inv) * sigmoid_f(gv.w);
-            *reinterpret_cast<float4*>(out + dd) = y;
+        for (int tt = 0; tt < 16; ++tt) {
+            const int dd = 16 * tt + r16;
+            out[dd] = (o[tt][rr] * inv) * sigmoid_f(gate[dd]);
         }
     }
 }
@@ -883,8 +962,9 @@ hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
     a.wg_slots = 2 * device_cu_count();  // two flash workgroups per CU (LDS and registers)
     if (a.ROT % 8 == 0) klaunch(attn_prefill_prep_kernel, a.T, 256, 0, s, a);
     else klaunch(attn_prefill_prep_any_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
-    if (a.kv_bf16) klaunch(flash_attn_kernel<true>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
-    else klaunch(flash_attn_kernel<false>, dim3((a.T + kQT - 1) / kQT, a.NQ), 256, 0, s, a);
+    const dim3 grid((a.T + kQT - 1) / kQT, a.NQ);
+    if (a.kv_bf16) klaunch(flash_attn_split_kernel<true>, grid, 256, 0, s, a);
+    else klaunch(flash_attn_split_kernel<false>, grid, 256, 0, s, a);
     return hipGetLastError();
 }
 
