@@ -25,6 +25,14 @@ HBM_PEAK_GBS = 8000.0
 GDN_LAYER_BYTES = 2_384_640  # per token per GDN layer (state r/w, conv window r/w, conv w, inputs, output)
 
 
+def gdn_step_kernel_bytes(d) -> int:
+    """Bytes of the decode step's GDN mixer kernel per layer: the conv window runs in the
+    in-projection's epilogue, so the kernel moves the state (read and written), the convolved
+    q / k / v, b / a, A_log / dt_bias and the readout (2,130,176 B at the 2B shape)."""
+    KH, VH = d.gdn_k_heads, d.gdn_v_heads
+    return 4 * (2 * VH * 128 * 128 + (2 * KH + VH) * 128 + 4 * VH + VH * 128)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -345,8 +353,10 @@ def bench_prefill(a) -> dict:
     ach = {"gemm": gemm_tfs, "attn_prefill": attn_tfs, "gdn_prefill": gdn_tfs}[dominant]
     # The projection GEMM runs each fp32 product as three exact bf16 products on the bf16
     # matrix cores, so its ceiling is the dense bf16 peak over 3 in fp32-product terms; the
-    # mixers run on the fp32 matrix cores.
-    peak = BF16_MFMA_PEAK_TFS / 3 if dominant == "gemm" else FP32_MFMA_PEAK_TFS
+    # flash attention as six bf16 part products (peak / 6); the chunked GDN on the fp32
+    # matrix cores.
+    peaks = {"gemm": BF16_MFMA_PEAK_TFS / 3, "attn_prefill": BF16_MFMA_PEAK_TFS / 6, "gdn_prefill": FP32_MFMA_PEAK_TFS}
+    peak = peaks[dominant]
     mixer_flops = d.n_layers_attn * attn_flops + d.n_layers_gdn * gdn_flops
     mixer_ms = ms["attn_prefill"] + ms["gdn_prefill"]
     res = {
@@ -360,8 +370,10 @@ def bench_prefill(a) -> dict:
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": ach, "peak": peak,
                      "unit": "TFLOP/s", "frac": ach / peak, "traffic": None,
                      "note": "fp32 flops of the algorithm; GEMM peak = dense bf16 MFMA peak / 3 (exact "
-                             "three-way bf16 split of the fp32 activations)"},
-        "mixers": {"attn_prefill_TFs": attn_tfs, "attn_prefill_frac": attn_tfs / FP32_MFMA_PEAK_TFS,
+                             "three-way bf16 split of the fp32 activations); flash attention = bf16 peak / 6 "
+                             "(six part products per fp32 product); GDN = fp32 MFMA peak"},
+        "mixers": {"attn_prefill_TFs": attn_tfs, "attn_prefill_frac": attn_tfs / peaks["attn_prefill"],
+                   "gdn_prefill_frac": gdn_tfs / FP32_MFMA_PEAK_TFS,
                    "gdn_prefill_TFs": gdn_tfs, "gemm_TFs": gemm_tfs,
                    "mixer_TFs": mixer_flops / (mixer_ms / 1e3) / 1e12,
                    "mixer_ms": mixer_ms, "gemm_ms": ms["gemm"], "other_ms": ms["other"]},
@@ -526,7 +538,7 @@ def bench_decode(a) -> None:
     mixer_bytes = 2 * NKV * HD * kv_elem * mean_n + 59_392  # per layer incl. projection outputs, append, output
     mixer_gbs = mixer_bytes * attn_n / (mixer_ms / 1e3) / 1e9
     gdn_ms, gdn_n = kt["gdn_decode"]
-    gdn_gbs = GDN_LAYER_BYTES * gdn_n / (gdn_ms / 1e3) / 1e9
+    gdn_gbs = gdn_step_kernel_bytes(d) * gdn_n / (gdn_ms / 1e3) / 1e9
     gemv_ms, gemv_n = kt["gemv"]
     wb = weight_bytes_per_step(d)
     gemv_gbs = wb * a.steps / (gemv_ms / 1e3) / 1e9
