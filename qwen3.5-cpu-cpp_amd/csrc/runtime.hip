@@ -55,6 +55,8 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 
 // split-K workspace is sized for this many splits per kv head
 constexpr int kMaxSplits = 1024;
+// greedy runs replay a graph of this many consecutive steps (one launch per run)
+constexpr int kGraphRun = 8;
 // device memory left free when the KV capacity is planned from the device's memory
 constexpr size_t kSolveMarginBytes = size_t{1} << 30;
 
@@ -125,8 +127,10 @@ struct q35_model {
     bool graph_valid = false;
     bool trace_on = false;
     bool timing_on = false;
-    hipGraph_t graph = nullptr;
+    hipGraph_t graph = nullptr;        // one step
     hipGraphExec_t exec = nullptr;
+    hipGraph_t graph_run = nullptr;    // kGraphRun steps back to back (greedy runs)
+    hipGraphExec_t exec_run = nullptr;
 
     std::vector<hipEvent_t> ev;  // timing event pairs
     std::vector<int> ev_class;
@@ -464,15 +468,20 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
 void drop_graph(q35_model* m) {
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
-    m->exec = nullptr;
-    m->graph = nullptr;
+    if (m->exec_run) (void)hipGraphExecDestroy(m->exec_run);
+    if (m->graph_run) (void)hipGraphDestroy(m->graph_run);
+    m->exec = m->exec_run = nullptr;
+    m->graph = m->graph_run = nullptr;
     m->graph_valid = false;
 }
 
-q35_status build_graph(q35_model* m) {
-    drop_graph(m);
+// `steps` consecutive decode steps captured into one graph. Every step reads its token and
+// position from token_dev / pos_dev and leaves the next ones there, so the same graph
+// serves any position.
+q35_status capture_steps(q35_model* m, int steps, hipGraph_t* graph, hipGraphExec_t* exec) {
     HIPCHK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-    const q35_status st = enqueue_step(m, m->stream, false);
+    q35_status st = Q35_OK;
+    for (int i = 0; i < steps && st == Q35_OK; ++i) st = enqueue_step(m, m->stream, false);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(m->stream, &g);
     if (st != Q35_OK) {
@@ -480,27 +489,42 @@ q35_status build_graph(q35_model* m) {
         return st;
     }
     if (e != hipSuccess) return q35::fail(Q35_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
-    m->graph = g;
-    HIPCHK(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    *graph = g;
+    HIPCHK(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+    return Q35_OK;
+}
+
+q35_status build_graph(q35_model* m) {
+    drop_graph(m);
+    q35_status st = capture_steps(m, 1, &m->graph, &m->exec);
+    if (st == Q35_OK) st = capture_steps(m, kGraphRun, &m->graph_run, &m->exec_run);
+    if (st != Q35_OK) {
+        drop_graph(m);
+        return st;
+    }
     m->graph_valid = true;
     return Q35_OK;
 }
 
-// Enqueue one step for the token already in token_dev.
-q35_status launch_one_step(q35_model* m) {
+// Enqueue `steps` (1 or kGraphRun) steps for the token already in token_dev.
+q35_status launch_steps(q35_model* m, int steps) {
     if (m->timing_on || m->trace_on || !m->use_graph) {
-        const q35_status st = enqueue_step(m, m->stream, m->timing_on);
-        if (st != Q35_OK) return st;
+        for (int i = 0; i < steps; ++i) {
+            const q35_status st = enqueue_step(m, m->stream, m->timing_on);
+            if (st != Q35_OK) return st;
+        }
     } else {
         if (!m->graph_valid) {
             const q35_status st = build_graph(m);
             if (st != Q35_OK) return st;
         }
-        HIPCHK(hipGraphLaunch(m->exec, m->stream));
+        HIPCHK(hipGraphLaunch(steps == kGraphRun ? m->exec_run : m->exec, m->stream));
     }
-    m->pos += 1;
+    m->pos += steps;
     return Q35_OK;
 }
+
+q35_status launch_one_step(q35_model* m) { return launch_steps(m, 1); }
 
 q35_status collect_timing(q35_model* m) {
     if (!m->timing_on || m->ev_used == 0) return Q35_OK;
@@ -1182,13 +1206,16 @@ q35_status run_greedy(q35_model* m, int32_t token, int32_t n_steps) {
                          n_steps, (long long)m->max_ctx);
     *m->pinned_token = token;
     HIPCHK(hipMemcpyAsync(m->token_dev, m->pinned_token, 4, hipMemcpyHostToDevice, m->stream));
-    for (int i = 0; i < n_steps; ++i) {
-        const q35_status st = launch_one_step(m);
+    const bool runs = m->use_graph && !m->timing_on && !m->trace_on;
+    for (int i = 0; i < n_steps;) {
+        const int k = runs && n_steps - i >= kGraphRun ? kGraphRun : 1;
+        const q35_status st = launch_steps(m, k);
         if (st != Q35_OK) return st;
         if (m->timing_on) {
             const q35_status t = collect_timing(m);
             if (t != Q35_OK) return t;
         }
+        i += k;
     }
     return Q35_OK;
 }

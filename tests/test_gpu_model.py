@@ -78,6 +78,17 @@ def test_graph_replay_matches_eager(model_dirs):
         m.step(int(t))
     ids = m.decode_greedy(int(g["prompt"][-1]), 16)
     np.testing.assert_array_equal(ids, g["greedy"])
+    # runs of eight steps in one graph plus single-step replays for the remainder (19 =
+    # 2 x 8 + 3), then a step after them: the same ids and logits as the eager loop
+    out = []
+    for graph in (False, True):
+        m.set_graph(graph)
+        m.reset()
+        ids = m.decode_greedy(int(g["prompt"][0]), 19)
+        out.append((ids, m.step(int(ids[-1]))[0], m.position))
+    np.testing.assert_array_equal(out[0][0], out[1][0])
+    np.testing.assert_array_equal(out[0][1], out[1][1])
+    assert out[0][2] == out[1][2] == 20
     m.close()
 
 
