@@ -27,8 +27,8 @@
 //   prep     q_norm + RoPE of every query row (head-major), k_norm + RoPE of every key and
 //            the values appended to the KV cache at pos0 + t (angles in double; a bf16 cache
 //            stores them rounded to nearest even and the flash kernel widens them back).
-//   flash    grid (query tiles of 64, NQ): 4 waves of 16 query rows with their q in
-//            registers (as three bf16 parts); 16-position K / V tiles in LDS (split into
+//   flash    grid (query tiles of 128, NQ): 8 waves of 16 query rows with their q in
+//            registers (as three bf16 parts); 32-position K / V tiles in LDS (split into
 //            bf16 parts when staged); S = Q K^T and O += P V on the bf16 matrix cores from
 //            six part products each; running max / sum per row; epilogue O / l * sigmoid(gate).
 #include <math.h>
@@ -639,35 +639,36 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 }
 
 // ------------------------------------------------------------------ flash attention
-constexpr int kQT = 64;   // query rows per workgroup (16 per wave)
+constexpr int kFW = 8;            // waves per workgroup
+constexpr int kQT = 16 * kFW;     // query rows per workgroup (16 per wave)
+constexpr int kKT = 32;           // keys per tile
+constexpr int kLdK2 = kHD + 8;    // K part rows (bf16): 528 B, the 16 rows of a read on distinct banks
+constexpr int kLdV2 = kKT + 8;    // V part rows, dim-major (bf16): 80 B
 
-// 64 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
-// the cache, 16-key tiles staged through LDS (the next tile's rows are loaded into registers
-// while the current one is multiplied), online softmax. Causal work grows with the query
-// block: workgroups are dispatched in linear order, S of them resident at once, ids c and
-// c + S/2 of a dispatch round on the same CU; work items are ranked longest first, and within
-// each full round of S the second half takes the ranks in reverse, so the two workgroups of a
-// CU carry complementary amounts of work (later rounds bring the shorter items).
-// Both products run on the bf16 matrix cores: every fp32 operand
+// 128 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
+// the cache, 32-key tiles staged through LDS (the next tile's rows are loaded into registers
+// while the current one is multiplied), online softmax. One workgroup per CU (112 KB of LDS
+// with three parts); causal work grows with the query block, and workgroups are dispatched
+// in linear order, so block L takes the L-th longest item (query blocks from the last).
+// Both products run on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16): every fp32 operand
 // is the exact sum of three bf16 parts (hi + mid + lo, as in the projection GEMM), and a
 // product a.b is the sum of the six part products a_i b_j with i + j <= 2 (parts counted
 // from 0): the three dropped ones (mid.lo, lo.mid, lo.lo) are below 2^-23 |a||b| together,
 // the size of an fp32 rounding, and each bf16 x bf16 part product is exact in fp32. A bf16
-// cache holds K and V exactly, so only Q and P are split (three products each). Six bf16
-// products cost 6/16 of one fp32 product on the matrix cores.
-//   S^T = K Q^T per 16-key tile on v_mfma_f32_16x16x32_bf16: keys as rows (K parts from LDS,
-//         8 consecutive dims per lane), the lane's own query row as the column (Q parts in
-//         registers, split once); lane (r16, g) ends with keys 4g + v of query r16.
-//   O += P V on v_mfma_f32_16x16x16_bf16: those four scores are the A operand (query r16,
-//         keys 4g .. 4g + 3) without data movement; V parts come from an LDS copy stored
-//         dim-major (keys 4g .. 4g + 3 of dim 16t + r16: one 8-byte read); lane (r16, g)
-//         ends with dims 16t + r16 of queries 4g + v.
-constexpr int kKT2 = 16;          // keys per tile
-constexpr int kLdK2 = kHD + 8;    // K part rows (bf16): 528 B, the 16 rows of a read on distinct banks
-constexpr int kLdV2 = kKT2 + 4;   // V part rows, dim-major (bf16): 40 B
-
-typedef short short4_t __attribute__((ext_vector_type(4)));
+// cache holds K and V exactly, so only Q and P are split (three products each).
+//   S^T = K Q^T per 16-key half of the tile: keys as rows (K parts from LDS, 8 consecutive
+//         dims per lane), the lane's own query row as the column (Q parts in registers, split
+//         once); lane (r16, g) ends with keys 4g + v of each half for query r16.
+//   O += P V, 32 keys deep: those eight scores are the A operand (query r16) without data
+//         movement, taking the k slots 8g .. 8g + 7 of the product as keys 4g .. 4g + 3 of the
+//         first half and of the second; the dim-major V rows in LDS store the keys in that
+//         order (one 16-byte read per lane and dim block); lane (r16, g) ends with dims
+//         16t + r16 of queries 4g + v. (16-key tiles would need the 16-deep bf16 product,
+//         which the gfx950 matrix cores run at half the 32-deep one's rate.)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// position of a tile's key in the V rows (and k slot of the P operand)
+__device__ __forceinline__ int vslot(int key) { return 8 * ((key & 15) >> 2) + 4 * (key >> 4) + (key & 3); }
 
 // the three bf16 parts of four floats, each part as four packed bf16 (element 0 low)
 __device__ __forceinline__ void split3_4(const float (&x)[4], uint2 (&part)[3]) {
@@ -680,18 +681,16 @@ __device__ __forceinline__ void split3_4(const float (&x)[4], uint2 (&part)[3]) 
 }
 
 template <bool KVB>
-__global__ __launch_bounds__(256, 2) void flash_attn_split_kernel(AttnPrefillArgs a) {
+__global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs a) {
     constexpr int NP = KVB ? 1 : 3;  // parts of K and V
-    const int nqt = gridDim.x, nlin = gridDim.x * gridDim.y;
-    const int L = blockIdx.x + blockIdx.y * nqt, S = max(2, a.wg_slots & ~1);
-    const int round0 = L - L % S, r = L - round0;
-    const int rank = round0 + S <= nlin ? round0 + (r < S / 2 ? r : 3 * S / 2 - 1 - r) : L;
+    const int nqt = gridDim.x;
+    const int rank = blockIdx.x + blockIdx.y * nqt;
     const int qt = nqt - 1 - rank / a.NQ, h = rank % a.NQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = a.NQ / a.NKV, kh = h / grp;
     const int t0 = qt * kQT;
     const int r16 = lane & 15, g4 = lane >> 4;
-    __shared__ __align__(16) uint16_t Kp[NP][kKT2][kLdK2];
+    __shared__ __align__(16) uint16_t Kp[NP][kKT][kLdK2];
     __shared__ __align__(16) uint16_t Vt[NP][kHD][kLdV2];
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
@@ -714,6 +713,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_split_kernel(AttnPrefillArg
         }
     }
     const int qpos = a.pos0 + qrow;
+    // the wave's last query position: tiles starting past it hold no key its rows attend
+    const int wlast = a.pos0 + min(t0 + wave * 16 + 15, a.T - 1);
     floatx4 o[16];  // dims 16 t + r16 of query rows 4 g4 + v
 #pragma unroll
     for (int t = 0; t < 16; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -762,8 +763,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_split_kernel(AttnPrefillArg
                 for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Kp[p][ks_row][ks_d + 4 * j]) = pt[p];
             }
         }
-        // V, transposed: dim vs_d + e gets the four keys vs_k .. + 3 (zero past the end: 0 * V
-        // must stay 0, and P is 0 there)
+        // V, transposed: dim vs_d + e gets the four keys vs_k .. + 3 at their slots (zero past
+        // the end: 0 * V must stay 0, and P is 0 there)
+        const int slot = vslot(vs_k);  // the four keys take four consecutive slots
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float x[4];
@@ -774,109 +776,125 @@ __global__ __launch_bounds__(256, 2) void flash_attn_split_kernel(AttnPrefillArg
                 x[j] = kv0 + vs_k + j < kv_end ? ve : 0.0f;
             }
             if constexpr (KVB) {
-                *reinterpret_cast<uint2*>(&Vt[0][vs_d + e][vs_k]) =
+                *reinterpret_cast<uint2*>(&Vt[0][vs_d + e][slot]) =
                     make_uint2(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
                                __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u));
             } else {
                 uint2 pt[3];
                 split3_4(x, pt);
 #pragma unroll
-                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Vt[p][vs_d + e][vs_k]) = pt[p];
+                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Vt[p][vs_d + e][slot]) = pt[p];
             }
         }
     };
     load_tile(0);
     store_tile(0);
     lds_barrier();
-    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT2) {
-        load_tile(kv0 + kKT2);  // in flight during this tile's products
-        // S^T[key 4 g4 + v][query r16]: the hi.hi products and the smaller part products in
-        // separate accumulators, each split over even / odd dim blocks (four chains)
-        floatx4 sa[2], sb[2];
+    for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
+        load_tile(kv0 + kKT);  // in flight during this tile's products
+        if (kv0 <= wlast) {    // uniform per wave
+            // S^T[key 16 hf + 4 g4 + v][query r16]: the hi.hi products and the smaller part
+            // products in separate accumulators, each split over even / odd dim blocks
+            floatx4 St[2];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) sa[e] = sb[e] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int hf = 0; hf < 2; ++hf) {
+                floatx4 sa[2], sb[2];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            bf16x8 kop[NP];
+                for (int e = 0; e < 2; ++e) sa[e] = sb[e] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int p = 0; p < NP; ++p) kop[p] = *reinterpret_cast<const bf16x8*>(&Kp[p][r16][32 * c + 8 * g4]);
-            floatx4& b = sb[c & 1];
-            if constexpr (KVB) {
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
-            } else {
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[2 % NP], qp[0][c], b, 0, 0, 0);
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[1][c], b, 0, 0, 0);
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[0][c], b, 0, 0, 0);
-                b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
+                for (int c = 0; c < 8; ++c) {
+                    bf16x8 kop[NP];
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        kop[p] = *reinterpret_cast<const bf16x8*>(&Kp[p][16 * hf + r16][32 * c + 8 * g4]);
+                    floatx4& b = sb[c & 1];
+                    if constexpr (KVB) {
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
+                    } else {
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[2 % NP], qp[0][c], b, 0, 0, 0);
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[1][c], b, 0, 0, 0);
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[1 % NP], qp[0][c], b, 0, 0, 0);
+                        b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[1][c], b, 0, 0, 0);
+                    }
+                    sa[c & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[0][c], sa[c & 1], 0, 0, 0);
+                }
+                St[hf] = (sb[0] + sb[1]) + (sa[0] + sa[1]);
             }
-            sa[c & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[0][c], sa[c & 1], 0, 0, 0);
-        }
-        const floatx4 St = (sb[0] + sb[1]) + (sa[0] + sa[1]);
-        float sv[4];
+            float sv[8];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int key = kv0 + 4 * g4 + v;
-            sv[v] = key <= qpos && key < kv_end ? St[v] * sc : -INFINITY;
-        }
-        float tm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16));
-        tm = fmaxf(tm, __shfl_xor(tm, 32));
-        // the reference max moves only when a score exceeds it by more than 8; a row with no
-        // key yet keeps -inf and weight 0
-        const float m_new = tm > m_run + 8.0f ? tm : m_run;
-        const bool live = m_new != -INFINITY;
-        const float f = live ? expf(m_run - m_new) : 1.0f;
-        float p[4], ps = 0.0f;
+            for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            p[v] = live ? expf(sv[v] - m_new) : 0.0f;
-            ps += p[v];
-        }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
-        l_run = l_run * f + ps;
-        m_run = m_new;
-        if (__any(f != 1.0f)) {  // rescale output rows 4 g4 + r
-            float fr[4];
+                for (int v = 0; v < 4; ++v) {
+                    const int key = kv0 + 16 * hf + 4 * g4 + v;
+                    sv[4 * hf + v] = key <= qpos && key < kv_end ? St[hf][v] * sc : -INFINITY;
+                }
+            float tm = sv[0];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) fr[rr] = __shfl(f, 4 * g4 + rr);
+            for (int i = 1; i < 8; ++i) tm = fmaxf(tm, sv[i]);
+            tm = fmaxf(tm, __shfl_xor(tm, 16));
+            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            // the reference max moves only when a score exceeds it by more than 8; a row with
+            // no key yet keeps -inf and weight 0
+            const float m_new = tm > m_run + 8.0f ? tm : m_run;
+            const bool live = m_new != -INFINITY;
+            const float f = live ? expf(m_run - m_new) : 1.0f;
+            float p[8], ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                p[i] = live ? expf(sv[i] - m_new) : 0.0f;
+                ps += p[i];
+            }
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            l_run = l_run * f + ps;
+            m_run = m_new;
+            if (__any(f != 1.0f)) {  // rescale output rows 4 g4 + r
+                float fr[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) fr[rr] = __shfl(f, 4 * g4 + rr);
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    o[t][0] *= fr[0];
+                    o[t][1] *= fr[1];
+                    o[t][2] *= fr[2];
+                    o[t][3] *= fr[3];
+                }
+            }
+            // O[query 4 g4 + v][dim 16 t + r16] += P[query][keys] V[keys][dim], k slots
+            // 8 g4 .. + 7 = keys 4 g4 .. + 3 of both halves
+            bf16x8 pa[3];
+            {
+                const float p0[4] = {p[0], p[1], p[2], p[3]}, p1[4] = {p[4], p[5], p[6], p[7]};
+                uint2 q0[3], q1[3];
+                split3_4(p0, q0);
+                split3_4(p1, q1);
+#pragma unroll
+                for (int q = 0; q < 3; ++q) pa[q] = __builtin_bit_cast(bf16x8, make_uint4(q0[q].x, q0[q].y, q1[q].x, q1[q].y));
+            }
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
-                o[t][0] *= fr[0];
-                o[t][1] *= fr[1];
-                o[t][2] *= fr[2];
-                o[t][3] *= fr[3];
-            }
-        }
-        // O[query 4 g4 + v][dim 16 t + r16] += P[query][keys 4 g4 ..] V[keys][dim]
-        uint2 pp[3];
-        split3_4(p, pp);
-        const short4_t pa0 = __builtin_bit_cast(short4_t, pp[0]), pa1 = __builtin_bit_cast(short4_t, pp[1]),
-                       pa2 = __builtin_bit_cast(short4_t, pp[2]);
+                bf16x8 vb[NP];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            short4_t vb[NP];
-#pragma unroll
-            for (int q = 0; q < NP; ++q)
-                vb[q] = __builtin_bit_cast(short4_t, *reinterpret_cast<const uint2*>(&Vt[q][16 * t + r16][4 * g4]));
-            floatx4 ob = floatx4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (KVB) {
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa2, vb[0], ob, 0, 0, 0);
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[0], ob, 0, 0, 0);
-            } else {
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa2, vb[0], ob, 0, 0, 0);
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[1 % NP], ob, 0, 0, 0);
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[2 % NP], ob, 0, 0, 0);
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, vb[0], ob, 0, 0, 0);
-                ob = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[1 % NP], ob, 0, 0, 0);
+                for (int q = 0; q < NP; ++q) vb[q] = *reinterpret_cast<const bf16x8*>(&Vt[q][16 * t + r16][8 * g4]);
+                floatx4 ob = floatx4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (KVB) {
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], ob, 0, 0, 0);
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], ob, 0, 0, 0);
+                } else {
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], ob, 0, 0, 0);
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[1 % NP], ob, 0, 0, 0);
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[2 % NP], ob, 0, 0, 0);
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], ob, 0, 0, 0);
+                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[1 % NP], ob, 0, 0, 0);
+                }
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[0], o[t] + ob, 0, 0, 0);
             }
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, vb[0], o[t] + ob, 0, 0, 0);
         }
         lds_barrier();  // every wave is done with this tile
-        if (kv0 + kKT2 < kv_end) {
-            store_tile(kv0 + kKT2);
+        if (kv0 + kKT < kv_end) {
+            store_tile(kv0 + kKT);
             lds_barrier();
         }
     }
@@ -959,12 +977,11 @@ int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
     AttnPrefillArgs a = in;
-    a.wg_slots = 2 * device_cu_count();  // two flash workgroups per CU (LDS and registers)
     if (a.ROT % 8 == 0) klaunch(attn_prefill_prep_kernel, a.T, 256, 0, s, a);
     else klaunch(attn_prefill_prep_any_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
     const dim3 grid((a.T + kQT - 1) / kQT, a.NQ);
-    if (a.kv_bf16) klaunch(flash_attn_split_kernel<true>, grid, 256, 0, s, a);
-    else klaunch(flash_attn_split_kernel<false>, grid, 256, 0, s, a);
+    if (a.kv_bf16) klaunch(flash_attn_kernel<true>, grid, kFW * 64, 0, s, a);
+    else klaunch(flash_attn_kernel<false>, grid, kFW * 64, 0, s, a);
     return hipGetLastError();
 }
 

@@ -200,7 +200,6 @@ struct AttnPrefillArgs {
     int kv_bf16;
     float* Qa;                 // workspace [NQ][T][HD]
     float* out;                // [T][NQ * HD]
-    int wg_slots;              // flash workgroups resident at once (set by the launcher)
     const float* rope_cs;      // optional [max_ctx][ROT] cos | sin table (else computed)
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
