@@ -68,9 +68,9 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint3
 // and their outputs dropped).
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs.
 template <int EPI, bool MASK>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (*Ws)[kLd]) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uint16_t (*Ws)[kLd]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int m0 = ty * kBM, n0 = tx * kBN;
     const int l16 = lane & 15, kq = (lane >> 4) * 8;
     const float* arow[2];  // this lane's X row in each of the wave's two 16-row blocks
 #pragma unroll
@@ -130,9 +130,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (*Ws)[kLd]
             aop[r][2] = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
         }
     };
+    // MASK: 16-column blocks wholly past N are skipped (a ragged last column tile, e.g. the
+    // 32-column tail of an 8224-row projection, costs its live blocks only)
+    const int jlive = MASK ? min(kCB, (a.N - n0 + 15) / 16) : kCB;
     auto products = [&](const bf16x8 (&aop)[2][3], int buf, auto fresh) {
 #pragma unroll
         for (int j = 0; j < kCB; ++j) {
+            if (MASK && j >= jlive) {
+                if constexpr (decltype(fresh)::value) part[0][j] = part[1][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                continue;
+            }
             const bf16x8 bop = *reinterpret_cast<const bf16x8*>(&Ws[buf * kBN + 16 * j + l16][kq]);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
@@ -216,10 +223,24 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, uint16_t (*Ws)[kLd]
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) uint16_t Ws[2 * kBN][kLd];
+    // tile (tx, ty) of workgroup L = x + X y (dispatch order): with a ragged last column
+    // tile, its row tiles come first (they are cheaper, so the full tiles fill the rounds
+    // behind them instead of a tail of ragged tiles running on a few CUs)
+    int tx = blockIdx.x, ty = blockIdx.y;
+    if (a.N % kBN != 0) {
+        const int nt = gridDim.x, mt = gridDim.y, L = blockIdx.x + nt * blockIdx.y;
+        if (L < mt) {
+            tx = nt - 1;
+            ty = L;
+        } else {
+            tx = (L - mt) % (nt - 1);
+            ty = (L - mt) / (nt - 1);
+        }
+    }
     // tiles whose W rows all lie inside N (with whole flush blocks of K) store W unmasked
-    const bool full = (blockIdx.x + 1) * kBN <= a.N && a.K % (kFlush * kBK) == 0;
-    if (full) gemm_tile<EPI, false>(a, Ws);
-    else gemm_tile<EPI, true>(a, Ws);
+    const bool full = (tx + 1) * kBN <= a.N && a.K % (kFlush * kBK) == 0;
+    if (full) gemm_tile<EPI, false>(a, tx, ty, Ws);
+    else gemm_tile<EPI, true>(a, tx, ty, Ws);
 }
 
 }  // namespace
