@@ -44,79 +44,97 @@ constexpr int kC = 64;    // chunk length
 constexpr int kHD = 256;  // attention head dim
 
 // ------------------------------------------------------------------ GDN prep
-// grid (T, KH), 256 threads: conv + SiLU for the k-head's q, k and its rep v-heads' v
-// channels, l2norm of q and k, beta / g of the rep v-heads.
-// kPT consecutive tokens per workgroup: each thread owns one channel, reads the kPT + 3 raw
-// inputs of its window once and its four taps once, and serves all kPT tokens.
-constexpr int kPT = 8;
+// grid (T / 16, KH), 384 threads: conv + SiLU of the k-head's q, k and its rep v-heads' v
+// channels for 16 tokens, l2norm of q and k, beta / g of the rep v-heads. Threads
+// 128 g .. 128 g + 127 take channel group g (q, k, v: two waves each); within a group, thread
+// t handles four consecutive tokens (group (t / 32) % 4) and four consecutive channels
+// (quad t % 32), so every load and store is 16 bytes and each 32-lane half-wave holds one
+// head's 128 channels of a token; its seven input rows (the four tokens and the three
+// before them) are read once.
+constexpr int kPT = 16;   // tokens per workgroup
+constexpr int kPTT = 4;   // tokens per thread
 
-__global__ __launch_bounds__(256) void gdn_prep_kernel(GdnPrefillArgs a) {
-    const int t0 = blockIdx.x * kPT, kh = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+__global__ __launch_bounds__(384) void gdn_prep_kernel(GdnPrefillArgs a) {
+    const int kh = blockIdx.y, tid = threadIdx.x;
+    const int grp = tid >> 7;                       // 0 q, 1 k, 2 v (uniform per wave)
+    const int tg = (tid >> 5) & 3, c4 = (tid & 31) * 4;  // token group; first channel in the head
+    const int t0 = blockIdx.x * kPT + kPTT * tg;
     const int rep = a.VH / a.KH;
     const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
-    const int nt = min(kPT, a.T - t0);
-    __shared__ double red[4][kPT];
-    auto xin = [&](int s, int ch) -> float {  // raw input of token s (relative) for channel ch
-        if (s >= 0) return a.qkv[static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch];
-        return a.conv_ring[static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch];
+    const int nt = min(kPTT, a.T - t0);  // may be <= 0 for the last block's groups
+    // raw inputs of tokens t0 - 3 + j (the conv ring before the block), channels ch .. ch + 3
+    auto xin = [&](int s, int ch) -> float4 {
+        if (s >= 0) return *reinterpret_cast<const float4*>(a.qkv + static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch);
+        return *reinterpret_cast<const float4*>(a.conv_ring + static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch);
     };
-    // causal conv + SiLU of channel ch for the kPT tokens (the reference's 4-tap window,
-    // src/qwen_forward.cpp:109-118)
-    auto conv = [&](int ch, float (&y)[kPT]) {
-        const float4 w4 = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(ch) * 4);
-        float x[kPT + 3];
+    // causal conv + SiLU of four channels for the thread's tokens (the reference's 4-tap
+    // window, src/qwen_forward.cpp:109-118)
+    auto conv = [&](int ch, float (&y)[kPTT][4]) {
+        float4 x[kPTT + 3];
 #pragma unroll
-        for (int j = 0; j < kPT + 3; ++j) x[j] = xin(t0 - 3 + j, ch);
+        for (int j = 0; j < kPTT + 3; ++j) x[j] = xin(t0 - 3 + j, ch);
 #pragma unroll
-        for (int j = 0; j < kPT; ++j) {
-            float acc = 0.0f;
-            acc += w4.x * x[j];
-            acc += w4.y * x[j + 1];
-            acc += w4.z * x[j + 2];
-            acc += w4.w * x[j + 3];
-            y[j] = silu_f(acc);
+        for (int e = 0; e < 4; ++e) {
+            const float4 w4 = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(ch + e) * 4);
+            float xs[kPTT + 3];
+#pragma unroll
+            for (int j = 0; j < kPTT + 3; ++j) xs[j] = e == 0 ? x[j].x : e == 1 ? x[j].y : e == 2 ? x[j].z : x[j].w;
+#pragma unroll
+            for (int j = 0; j < kPTT; ++j) {
+                float acc = 0.0f;
+                acc += w4.x * xs[j];
+                acc += w4.y * xs[j + 1];
+                acc += w4.z * xs[j + 2];
+                acc += w4.w * xs[j + 3];
+                y[j][e] = silu_f(acc);
+            }
         }
     };
-    // q (threads 0..127) and k (128..255): l2norm per token, sums of squares in double
-    const int ch = tid < kD ? kh * kD + tid : KD + kh * kD + (tid - kD);
-    float y[kPT];
-    conv(ch, y);
+    float y[kPTT][4];
+    if (grp < 2) {
+        conv(grp * KD + kh * kD + c4, y);
+        // l2norm per token over the head's 128 channels (this half-wave): sums in double
 #pragma unroll
-    for (int j = 0; j < kPT; ++j) {
-        double ss = static_cast<double>(y[j]) * y[j];
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave][j] = ss;
-    }
-    __syncthreads();
+        for (int j = 0; j < kPTT; ++j) {
+            double ss = 0.0;
 #pragma unroll
-    for (int j = 0; j < kPT; ++j) {
-        if (j >= nt) break;
-        const int64_t row = static_cast<int64_t>(kh) * a.Tp + t0 + j;
-        if (tid < kD) {
-            const float inv = 1.0f / sqrtf(static_cast<float>(red[0][j] + red[1][j]) + 1e-6f);
-            a.Qg[row * kD + tid] = (y[j] * inv) * (1.0f / sqrtf(static_cast<float>(kD)));
-        } else {
-            const float inv = 1.0f / sqrtf(static_cast<float>(red[2][j] + red[3][j]) + 1e-6f);
-            a.Kg[row * kD + (tid - kD)] = y[j] * inv;
+            for (int e = 0; e < 4; ++e) ss += static_cast<double>(y[j][e]) * y[j][e];
+            ss = half_wave_sum(ss);
+            if (j >= nt) continue;
+            const float inv = 1.0f / sqrtf(static_cast<float>(ss) + 1e-6f);
+            const int64_t row = static_cast<int64_t>(kh) * a.Tp + t0 + j;
+            float4 o;
+            if (grp == 0) {
+                const float qs = 1.0f / sqrtf(static_cast<float>(kD));
+                o = make_float4((y[j][0] * inv) * qs, (y[j][1] * inv) * qs, (y[j][2] * inv) * qs, (y[j][3] * inv) * qs);
+                *reinterpret_cast<float4*>(a.Qg + row * kD + c4) = o;
+            } else {
+                o = make_float4(y[j][0] * inv, y[j][1] * inv, y[j][2] * inv, y[j][3] * inv);
+                *reinterpret_cast<float4*>(a.Kg + row * kD + c4) = o;
+            }
         }
+        return;
     }
-    // v channels and beta / g of the v-heads served by this k-head
+    // v channels of the v-heads served by this k-head
     for (int r = 0; r < rep; ++r) {
         const int vh = kh * rep + r;
-        if (tid < kD) {
-            float yv[kPT];
-            conv(2 * KD + vh * kD + tid, yv);
+        conv(2 * KD + vh * kD + c4, y);
 #pragma unroll
-            for (int j = 0; j < kPT; ++j)
-                if (j < nt) a.Vg[(static_cast<int64_t>(vh) * a.Tp + t0 + j) * kD + tid] = yv[j];
-        } else if (tid - kD < nt) {
-            const int t = t0 + tid - kD;
-            const float bb = a.b[static_cast<int64_t>(t) * a.ld_ba + vh];
-            const float aa = a.a[static_cast<int64_t>(t) * a.ld_ba + vh];
-            a.Bg[static_cast<int64_t>(vh) * a.Tp + t] = sigmoid_f(bb);
-            a.Gg[static_cast<int64_t>(vh) * a.Tp + t] = -expf(a.A_log[vh]) * softplus_f(aa + a.dt_bias[vh]);
-        }
+        for (int j = 0; j < kPTT; ++j)
+            if (j < nt)
+                *reinterpret_cast<float4*>(a.Vg + (static_cast<int64_t>(vh) * a.Tp + t0 + j) * kD + c4) =
+                    make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+    }
+    // beta / g of (v-head, token) pairs: the v threads of token group 0
+    if (tg != 0) return;
+    for (int i = tid & 31; i < rep * kPT; i += 32) {
+        const int r = i / kPT, j = i - r * kPT, t = blockIdx.x * kPT + j;
+        if (t >= a.T) continue;
+        const int vh = kh * rep + r;
+        const float bb = a.b[static_cast<int64_t>(t) * a.ld_ba + vh];
+        const float aa = a.a[static_cast<int64_t>(t) * a.ld_ba + vh];
+        a.Bg[static_cast<int64_t>(vh) * a.Tp + t] = sigmoid_f(bb);
+        a.Gg[static_cast<int64_t>(vh) * a.Tp + t] = -expf(a.A_log[vh]) * softplus_f(aa + a.dt_bias[vh]);
     }
 }
 
@@ -964,7 +982,7 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
 }
 
 hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
-    klaunch(gdn_prep_kernel, dim3((a.T + kPT - 1) / kPT, a.KH), 256, 0, s, a);
+    klaunch(gdn_prep_kernel, dim3((a.T + kPT - 1) / kPT, a.KH), 384, 0, s, a);
     if (a.Tp > a.T) klaunch(gdn_pad_kernel, blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s, a);
     klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
     klaunch(gdn_chunk_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
