@@ -416,9 +416,9 @@ constexpr int kLdS = kD + 16;   // state / v_new rows (B operand)
 // grid (VH, Tp / 64), 256 threads: o = e^gamma (Q S_c) + P v_new for one chunk of one v-head,
 // then the gated rmsnorm (src/forward_pass.cpp:86-93, sum of squares in double) or the raw
 // readout. Wave w owns output rows [16w, 16w + 16), all 128 columns (8 blocks of 16).
-// S_c goes through LDS in two halves of 64 rows (71 KB of LDS, two workgroups per CU), and
-// each phase's operands are requested into registers while the previous phase multiplies:
-// the second half of S_c during Q S_c[0:64), P and v_new during Q S_c[64:128).
+// S_c goes through LDS in two halves of 64 rows (71 KB of LDS, two workgroups per CU); every
+// operand is requested into registers at the start, so the later phases' loads (the second
+// half of S_c, P and v_new) arrive while the earlier phases multiply.
 __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
@@ -438,11 +438,10 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const float* Vn = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
     constexpr int NQ4 = kC * kD / 4 / 256;  // float4 per thread of a 64 x 128 tile (8)
     constexpr int NP4 = kC * kC / 4 / 256;  // of the 64 x 64 P tile (4)
-    auto put_b = [&](int f, float4 v) {  // float4 f of a row-major 64 x 128 tile -> B_s, permuted
+    auto put_b = [&](int f, floatx4 v) {  // float4 f of a row-major 64 x 128 tile -> B_s, permuted
         const int r = f >> 5, c0 = (f & 31) * 4;
-        const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) B_s[r][((c0 + i) & 15) * 8 + ((c0 + i) >> 4)] = e[i];
+        for (int i = 0; i < 4; ++i) B_s[r][((c0 + i) & 15) * 8 + ((c0 + i) >> 4)] = v[i];
     };
     floatx4 acc[8];
 #pragma unroll
@@ -465,26 +464,36 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
             acc[7] = mfma4(av[j], b1.w, acc[7]);
         }
     };
-    for (int f = tid; f < kC * kD / 4; f += 256) {
-        *reinterpret_cast<float4*>(&A_s[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
-        put_b(f, *reinterpret_cast<const float4*>(Sc + f * 4));
-    }
-    if (tid < kC) eg[tid] = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
-    __syncthreads();
-    float4 rs[NQ4];  // S_c rows [64, 128)
+    // every operand is requested up front (Q and S_c[0:64) first: loads complete in order
+    // for the wait counter, so the first phase waits for those alone)
+    // (vector-typed register arrays: arrays of float4 structs were placed in scratch)
+    floatx4 rq[NQ4], rs0[NQ4], rs[NQ4], rp[NP4], rv[NQ4];
 #pragma unroll
-    for (int i = 0; i < NQ4; ++i) rs[i] = *reinterpret_cast<const float4*>(Sc + kC * kD + (tid + 256 * i) * 4);
+    for (int i = 0; i < NQ4; ++i) {
+        rq[i] = *reinterpret_cast<const floatx4*>(Q + (tid + 256 * i) * 4);
+        rs0[i] = *reinterpret_cast<const floatx4*>(Sc + (tid + 256 * i) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) rs[i] = *reinterpret_cast<const floatx4*>(Sc + kC * kD + (tid + 256 * i) * 4);
+#pragma unroll
+    for (int i = 0; i < NP4; ++i) rp[i] = *reinterpret_cast<const floatx4*>(P + (tid + 256 * i) * 4);
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) rv[i] = *reinterpret_cast<const floatx4*>(Vn + (tid + 256 * i) * 4);
+    const float egv = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + (tid & (kC - 1))];
+#pragma unroll
+    for (int i = 0; i < NQ4; ++i) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<floatx4*>(&A_s[f >> 5][(f & 31) * 4]) = rq[i];
+        put_b(f, rs0[i]);
+    }
+    if (tid < kC) eg[tid] = egv;
+    lds_barrier();  // LDS only: S_c[64:128), P and v_new stay in flight
 #pragma unroll
     for (int blk = 0; blk < kC / 16; ++blk) mma16(16 * blk, 16 * blk);
     lds_barrier();  // done with S_c[0:64)
 #pragma unroll
     for (int i = 0; i < NQ4; ++i) put_b(tid + 256 * i, rs[i]);
     lds_barrier();
-    float4 rp[NP4], rv[NQ4];
-#pragma unroll
-    for (int i = 0; i < NP4; ++i) rp[i] = *reinterpret_cast<const float4*>(P + (tid + 256 * i) * 4);
-#pragma unroll
-    for (int i = 0; i < NQ4; ++i) rv[i] = *reinterpret_cast<const float4*>(Vn + (tid + 256 * i) * 4);
 #pragma unroll
     for (int blk = 0; blk < kC / 16; ++blk) mma16(kC + 16 * blk, 16 * blk);
 #pragma unroll
@@ -497,7 +506,7 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < NP4; ++i) {
         const int f = tid + 256 * i;
-        *reinterpret_cast<float4*>(&A_s[f >> 4][(f & 15) * 4]) = rp[i];
+        *reinterpret_cast<floatx4*>(&A_s[f >> 4][(f & 15) * 4]) = rp[i];
     }
 #pragma unroll
     for (int i = 0; i < NQ4; ++i) put_b(tid + 256 * i, rv[i]);
