@@ -259,7 +259,8 @@ q35_status q35_model_fill_synthetic(q35_model *m, int64_t pos, uint64_t seed, fl
 /* ------------------------------------------------------------------------------------ */
 /* primitives on device pointers (include/forward_pass.h:21-54)                           */
 /* ------------------------------------------------------------------------------------ */
-/* y = W x, W bf16 row-major [out_dim][in_dim] (forward_pass.cpp:65-75). in_dim % 8 == 0. */
+/* y = W x, W bf16 row-major [out_dim][in_dim] (forward_pass.cpp:65-75). in_dim % 8 == 0 and
+ * in_dim <= 32768 (the input is staged in LDS); Q35_ERR_UNSUPPORTED otherwise. */
 q35_status q35_matmul_bf16(const uint16_t *W, const float *x, float *y, int32_t out_dim,
                            int32_t in_dim, q35_stream s);
 /* y = W x with fp32 W row-major [out_dim][in_dim], any in_dim (forward_pass.cpp:29-33, the

@@ -122,6 +122,8 @@ q35_status q35_matmul_bf16(const uint16_t* W, const float* x, float* y, int32_t 
                          q35k::kGemvMaxIn);
     if ((reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(x) & 15))
         return q35::fail(Q35_ERR_ARG, "q35_matmul_bf16: W and x must be 16-byte aligned");
+    if (in_dim > 16384 && q35k::gemv_enable_wide_inputs() != hipSuccess)
+        return q35::fail(Q35_ERR_HIP, "q35_matmul_bf16: cannot enable %d-wide inputs", in_dim);
     q35k::GemvArgs a{};
     a.W = W;
     a.x = x;

@@ -426,7 +426,38 @@ hipError_t launch_pro(const GemvArgs& a, int epi, hipStream_t s) {
     return a.resid ? launch_rpw<PRO, kEpiResidual>(a, s) : launch_rpw<PRO, kEpiStore>(a, s);
 }
 
+template <int PRO, int EPI>
+hipError_t allow_wide() {
+    const int bytes = (kGemvMaxIn + 4) * static_cast<int>(sizeof(float));
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<PRO, EPI, 1, 0, 0>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<PRO, EPI, 2, 0, 0>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return e;
+}
+
+template <int PRO>
+hipError_t allow_wide_pro() {
+    hipError_t e = allow_wide<PRO, kEpiStore>();
+    if (e == hipSuccess) e = allow_wide<PRO, kEpiResidual>();
+    if (e == hipSuccess) e = allow_wide<PRO, kEpiSwiGluPair>();
+    if (e == hipSuccess && PRO == kProRmsNorm) e = allow_wide<kProRmsNorm, kEpiConvSilu>();
+    return e;
+}
+
 }  // namespace
+
+hipError_t gemv_enable_wide_inputs() {
+    static const hipError_t e = [] {
+        hipError_t r = allow_wide_pro<kProPlain>();
+        if (r == hipSuccess) r = allow_wide_pro<kProRmsNorm>();
+        if (r == hipSuccess) r = allow_wide_pro<kProSwiGlu>();
+        if (r == hipSuccess) r = allow_wide_pro<kProGatedNorm>();
+        return r;
+    }();
+    return e;
+}
 
 hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue) {
     switch (prologue) {

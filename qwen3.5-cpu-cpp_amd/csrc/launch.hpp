@@ -61,8 +61,11 @@ struct GemvArgs {
 // the GDN in-projection's conv window + SiLU on its conv rows (kEpiConvSilu).
 enum GemvEpilogue : int { kEpiAuto = -1, kEpiStore = 0, kEpiResidual = 1, kEpiSwiGluPair = 2, kEpiConvSilu = 3 };
 hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue = kEpiAuto);
-// Largest in_dim the matvec stages in LDS.
-constexpr int kGemvMaxIn = 16384;
+// Largest in_dim the matvec stages in LDS (128 KB of the 160 KB a gfx950 workgroup may use).
+constexpr int kGemvMaxIn = 32768;
+// Raises the dynamic-LDS limit of the matvec instantiations that stage inputs wider than
+// 16384 (64 KB); once per process, before any launch is captured into a graph.
+hipError_t gemv_enable_wide_inputs();
 
 // ---------------------------------------------------------------- token-batched GEMM
 // Y[M][N] = (R ? R : 0) + X[M][K] . W[N][K]^T; K % 8 == 0, ldx % 4 == 0, 16-byte aligned X.

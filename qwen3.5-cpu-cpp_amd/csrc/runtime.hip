@@ -821,6 +821,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->d = d;
     m->max_ctx = max_ctx;
     HIPCHK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    HIPCHK(q35k::gemv_enable_wide_inputs());  // before any launch is captured into a graph
 
     // state arena: GDN states and conv rings (fixed size)
     const size_t gdn_bytes = static_cast<size_t>(d.n_layers_gdn) * VH * 128 * 128 * 4;

@@ -266,3 +266,26 @@ def test_prefill_wide_ffn_matches_decode(tmp_path):
     ref = np.stack([m.step(int(t))[0] for t in prompt])
     m.close()
     assert rel_l2(lg, ref) < REL_L2
+
+
+def test_ffn_wider_than_64kb_of_lds(tmp_path):
+    """An FFN 20480 wide: the down projection's input (80 KB as fp32) is staged in more than
+    the 64 KB of LDS the matvec used to cap its input at; decode logits equal the oracle's
+    step by step, and the prefill (GEMM K = 20480) equals the decode."""
+    d = pyq35.default_dims(hidden_size=256, n_layers_total=4, gdn_k_heads=2, gdn_v_heads=2,
+                           attn_q_heads=2, attn_kv_heads=1, ffn_intermediate=20480,
+                           vocab_size=1024, native_max_context=4096)
+    path = str(tmp_path / "wideffn")
+    pyq35.synth_write_model(path, d, seed=4, std=0.02)
+    prompt = pyq35.synth_token_ids(6, d.vocab_size, 24)
+    m = pyq35.Model(path, 64)
+    o = op.Oracle(path, 64)
+    lg = np.stack([m.step(int(t))[0] for t in prompt])
+    ref = np.stack([o.step(int(t)) for t in prompt])
+    o.close()
+    m.close()
+    assert rel_l2(lg, ref) < REL_L2
+    m = pyq35.Model(path, 64)
+    pf = m.prefill(prompt)
+    m.close()
+    assert rel_l2(pf, lg) < REL_L2
