@@ -342,6 +342,10 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     // stores stay in flight through them (a full barrier would wait for every outstanding
     // load, the prefetch included)
     __syncthreads();  // the state slice is in LDS
+    // chunk-start states for the output pass: chunk 0's from LDS here, every later one from
+    // the registers that computed it (the end of the previous chunk step)
+    for (int i = tid; i < kD * kSW; i += kSThreads)
+        a.Sc[static_cast<int64_t>(vh) * nchunk * kD * kD + (i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
     for (int c = 0; c < nchunk; ++c) {
         lds_barrier();  // previous chunk done with Wl / Kt / St
         store_chunk();
@@ -349,9 +353,6 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
         floatx4 vn;
 #pragma unroll
         for (int v = 0; v < 4; ++v) vn[v] = ru[v];
-        // chunk-start state for the output pass
-        float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
-        for (int i = tid; i < kD * kSW; i += kSThreads) Sc[(i >> 4) * kD + (i & 15)] = St[i & 15][i >> 4];
         lds_barrier();
         load_chunk(min(c + 1, nchunk - 1));  // unconditional (the last chunk is requested twice)
 
@@ -404,6 +405,11 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
         }
         sn = sn + (ch[0] + ch[1]);
         *reinterpret_cast<floatx4*>(&St[lr][16 * wave + 4 * lg]) = sn;
+        if (c + 1 < nchunk) {  // uniform
+            float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c + 1) * kD * kD + col0 + lr;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) Sc[(16 * wave + 4 * lg + v) * kD] = sn[v];
+        }
     }
     __syncthreads();
     for (int i = tid; i < kD * kSW; i += kSThreads) S[(i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
