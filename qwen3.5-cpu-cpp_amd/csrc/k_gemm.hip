@@ -45,6 +45,8 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
@@ -63,25 +65,56 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint3
     l = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xffff0000u);
 }
 
+// the two fp16 parts of two (scaled) floats a, b: h = rn(x), l = rn(x - h), each pair packed
+__device__ __forceinline__ void split2h_pair(float a, float b, uint32_t& h, uint32_t& l) {
+    const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+    const _Float16 la = static_cast<_Float16>(a - static_cast<float>(ha));
+    const _Float16 lb = static_cast<_Float16>(b - static_cast<float>(hb));
+    h = __builtin_bit_cast(uint32_t, half2_t{ha, hb});
+    l = __builtin_bit_cast(uint32_t, half2_t{la, lb});
+}
+
 // One 128 x 128 tile. MASK: some W rows of the tile lie past N or K is not a whole number of
 // flush blocks, so W and X chunks past N or K are zeroed (X rows past M are clamped to row 0
 // and their outputs dropped).
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs.
-template <int EPI, bool MASK>
+// F16: two fp16 parts per activation against the fp16 weight copy (see launch_gemm).
+template <int EPI, bool MASK, bool F16>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uint16_t (*Ws)[kLd]) {
+    using OpT = typename std::conditional<F16, halfx8, bf16x8>::type;
+    constexpr int NP = F16 ? 2 : 3;  // parts per activation
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = ty * kBM, n0 = tx * kBN;
     const int l16 = lane & 15, kq = (lane >> 4) * 8;
     const float* arow[2];  // this lane's X row in each of the wave's two 16-row blocks
+    int arow_i[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int row = m0 + wave * 32 + 16 * r + l16;
-        arow[r] = a.X + static_cast<int64_t>(row < a.M ? row : 0) * a.ldx;
+        arow_i[r] = row < a.M ? row : 0;
+        arow[r] = a.X + static_cast<int64_t>(arow_i[r]) * a.ldx;
+    }
+    // F16: each row's scale 2^xe, xe = 15 - (exponent of its maximum |x| as in frexp), so
+    // the row lies in (-2^15, 2^15) with its maximum at or above 2^14; exact in fp32
+    int xe[2] = {0, 0};
+    float xs[2] = {1.0f, 1.0f};
+    if constexpr (F16) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            float mx = 0.0f;
+            for (int j = lane >> 4; j < a.xmax_n; j += 4) mx = fmaxf(mx, a.xmax[static_cast<int64_t>(arow_i[r]) * a.xmax_n + j]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            int ex = 0;
+            (void)frexpf(mx, &ex);
+            xe[r] = mx > 0.0f && mx < INFINITY ? min(max(15 - ex, -100), 100) : 0;
+            xs[r] = ldexpf(1.0f, xe[r]);
+        }
     }
     // W staging: thread t loads 16 k of row t / 2 (half t % 2) of the tile, two 16-byte chunks
     const int wr = tid >> 1, wk = (tid & 1) * 16;
     const bool b_ok = n0 + wr < a.N;
-    const uint16_t* wrow = a.W + static_cast<int64_t>(b_ok ? n0 + wr : 0) * a.K;
+    const uint16_t* wrow = (F16 ? a.Wh : a.W) + static_cast<int64_t>(b_ok ? n0 + wr : 0) * a.K;
     // Loads are unconditional (addresses clamped into the row) so that no load sits under a
     // branch: the wait-count pass would then wait for every outstanding load at the join.
     auto load_a = [&](uint4 (&xa)[2][2], int k0) {
@@ -112,7 +145,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
     for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int j = 0; j < kCB; ++j) acc[r][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto split_a = [&](const uint4 (&xa)[2][2], bf16x8 (&aop)[2][3], int k0) {
+    auto split_a = [&](const uint4 (&xa)[2][2], OpT (&aop)[2][NP], int k0) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             float4 x0 = __builtin_bit_cast(float4, xa[r][0]), x1 = __builtin_bit_cast(float4, xa[r][1]);
@@ -120,36 +153,50 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
                 if (k0 + kq >= a.K) x0 = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (k0 + kq + 4 >= a.K) x1 = make_float4(0.f, 0.f, 0.f, 0.f);
             }
+            if constexpr (F16) {
+                const float sc = xs[r];
+                uint32_t h[4], l[4];
+                split2h_pair(x0.x * sc, x0.y * sc, h[0], l[0]);
+                split2h_pair(x0.z * sc, x0.w * sc, h[1], l[1]);
+                split2h_pair(x1.x * sc, x1.y * sc, h[2], l[2]);
+                split2h_pair(x1.z * sc, x1.w * sc, h[3], l[3]);
+                aop[r][0] = __builtin_bit_cast(OpT, u32x4{h[0], h[1], h[2], h[3]});
+                aop[r][1] = __builtin_bit_cast(OpT, u32x4{l[0], l[1], l[2], l[3]});
+                continue;
+            }
             uint32_t h[4], m[4], l[4];
             split3_pair(x0.x, x0.y, h[0], m[0], l[0]);
             split3_pair(x0.z, x0.w, h[1], m[1], l[1]);
             split3_pair(x1.x, x1.y, h[2], m[2], l[2]);
             split3_pair(x1.z, x1.w, h[3], m[3], l[3]);
-            aop[r][0] = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
-            aop[r][1] = __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]});
-            aop[r][2] = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
+            aop[r][0] = __builtin_bit_cast(OpT, u32x4{h[0], h[1], h[2], h[3]});
+            aop[r][1] = __builtin_bit_cast(OpT, u32x4{m[0], m[1], m[2], m[3]});
+            aop[r][NP - 1] = __builtin_bit_cast(OpT, u32x4{l[0], l[1], l[2], l[3]});
         }
     };
     // MASK: 16-column blocks wholly past N are skipped (a ragged last column tile, e.g. the
     // 32-column tail of an 8224-row projection, costs its live blocks only)
     const int jlive = MASK ? min(kCB, (a.N - n0 + 15) / 16) : kCB;
-    auto products = [&](const bf16x8 (&aop)[2][3], int buf, auto fresh) {
+    auto mfma = [](const OpT& x, const OpT& w, const floatx4& c) {
+        if constexpr (F16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, w, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, w, c, 0, 0, 0);
+    };
+    auto products = [&](const OpT (&aop)[2][NP], int buf, auto fresh) {
 #pragma unroll
         for (int j = 0; j < kCB; ++j) {
             if (MASK && j >= jlive) {
                 if constexpr (decltype(fresh)::value) part[0][j] = part[1][j] = floatx4{0.f, 0.f, 0.f, 0.f};
                 continue;
             }
-            const bf16x8 bop = *reinterpret_cast<const bf16x8*>(&Ws[buf * kBN + 16 * j + l16][kq]);
+            const OpT bop = *reinterpret_cast<const OpT*>(&Ws[buf * kBN + 16 * j + l16][kq]);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int p = 2; p >= 0; --p) {  // lo, mid, hi
+                for (int p = NP - 1; p >= 0; --p) {  // smallest part first
                     if constexpr (decltype(fresh)::value) {
-                        part[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            aop[r][p], bop, p == 2 ? floatx4{0.f, 0.f, 0.f, 0.f} : part[r][j], 0, 0, 0);
+                        part[r][j] = mfma(aop[r][p], bop, p == NP - 1 ? floatx4{0.f, 0.f, 0.f, 0.f} : part[r][j]);
                     } else {
-                        part[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r][p], bop, part[r][j], 0, 0, 0);
+                        part[r][j] = mfma(aop[r][p], bop, part[r][j]);
                     }
                 }
         }
@@ -171,7 +218,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
             const int k0 = kb + f * kBK;
             store_w(wb, k0 + kBK, (f + 1) & 1);  // its last readers passed the previous barrier
             load_w(wb, k0 + 2 * kBK);
-            bf16x8 aop[2][3];
+            OpT aop[2][NP];
             split_a(xa[f & 1], aop, k0);
             load_a(xa[f & 1], k0 + 2 * kBK);
             // keep the loads ahead of the products (the scheduler would sink them)
@@ -186,8 +233,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
             for (int j = 0; j < kCB; ++j) acc[r][j] += part[r][j];
     }
     const int rbase = m0 + wave * 32 + 4 * (lane >> 4);
+    if constexpr (F16) {
+        // undo the scales: output row rbase + 16 r + v is the A row of lane 4 (lane / 16) + v
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float f = ldexpf(1.0f, -(__shfl(xe[r], 4 * (lane >> 4) + v) + a.w_exp));
+#pragma unroll
+                for (int j = 0; j < kCB; ++j) acc[r][j][v] *= f;
+            }
+    }
     if constexpr (EPI == 2) {
         // the pair (gate, up) of one output sits in adjacent lanes (even, odd column)
+        float ym[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int j = 0; j < kCB; ++j) {
             const int col = n0 + 16 * j + l16;
@@ -197,8 +256,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
                 for (int v = 0; v < 4; ++v) {
                     const float up = __shfl_xor(acc[r][j][v], 1);
                     const int row = rbase + 16 * r + v;
-                    if (!(lane & 1) && col + 1 < a.N && row < a.M)
-                        a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = silu_f(acc[r][j][v]) * up;
+                    const float h = silu_f(acc[r][j][v]) * up;
+                    if (!(lane & 1) && col + 1 < a.N) {
+                        ym[r][v] = fmaxf(ym[r][v], fabsf(h));
+                        if (row < a.M) a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = h;
+                    }
+                }
+        }
+        if (a.ymax) {  // uniform: each row's maximum over this tile's outputs
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float m = ym[r][v];
+                    m = fmaxf(m, __shfl_xor(m, 1));
+                    m = fmaxf(m, __shfl_xor(m, 2));
+                    m = fmaxf(m, __shfl_xor(m, 4));
+                    m = fmaxf(m, __shfl_xor(m, 8));
+                    const int row = rbase + 16 * r + v;
+                    if (l16 == 0 && row < a.M) a.ymax[static_cast<int64_t>(row) * gridDim.x + tx] = m;
                 }
         }
         return;
@@ -220,7 +296,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
     }
 }
 
-template <int EPI>
+template <int EPI, bool F16>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) uint16_t Ws[2 * kBN][kLd];
     // tile (tx, ty) of workgroup L = x + X y (dispatch order): with a ragged last column
@@ -239,17 +315,24 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     }
     // tiles whose W rows all lie inside N (with whole flush blocks of K) store W unmasked
     const bool full = (tx + 1) * kBN <= a.N && a.K % (kFlush * kBK) == 0;
-    if (full) gemm_tile<EPI, false>(a, tx, ty, Ws);
-    else gemm_tile<EPI, true>(a, tx, ty, Ws);
+    if (full) gemm_tile<EPI, false, F16>(a, tx, ty, Ws);
+    else gemm_tile<EPI, true, F16>(a, tx, ty, Ws);
 }
 
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-    dim3 grid((a.N + kBN - 1) / kBN, (a.M + kBM - 1) / kBM);
-    if (a.swiglu) klaunch(gemm_kernel<2>, grid, 256, 0, s, a);
-    else if (a.R) klaunch(gemm_kernel<1>, grid, 256, 0, s, a);
-    else klaunch(gemm_kernel<0>, grid, 256, 0, s, a);
+    dim3 grid(gemm_col_tiles(a.N), (a.M + kBM - 1) / kBM);
+    const bool f16 = a.Wh && a.xmax && a.xmax_n > 0;
+    if (f16) {
+        if (a.swiglu) klaunch(gemm_kernel<2, true>, grid, 256, 0, s, a);
+        else if (a.R) klaunch(gemm_kernel<1, true>, grid, 256, 0, s, a);
+        else klaunch(gemm_kernel<0, true>, grid, 256, 0, s, a);
+    } else {
+        if (a.swiglu) klaunch(gemm_kernel<2, false>, grid, 256, 0, s, a);
+        else if (a.R) klaunch(gemm_kernel<1, false>, grid, 256, 0, s, a);
+        else klaunch(gemm_kernel<0, false>, grid, 256, 0, s, a);
+    }
     return hipGetLastError();
 }
 

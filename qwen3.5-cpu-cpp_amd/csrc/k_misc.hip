@@ -16,8 +16,9 @@ namespace {
 // y = w * (x * rsqrt(mean(x^2) + eps)) * silu(gate).
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const float* w,
                                                            float* y, int n, float eps,
-                                                           int gated, const float* gate) {
+                                                           int gated, const float* gate, float* ymax) {
     __shared__ double red[4];
+    __shared__ float mred[4];
     const int64_t off = static_cast<int64_t>(blockIdx.x) * n;
     double ss = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) {
@@ -26,9 +27,18 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
     }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + eps);
+    float mx = 0.0f;
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = x[off + i];
-        y[off + i] = gated ? w[i] * (v * inv) * silu_f(gate[off + i]) : v * inv * (1.0f + w[i]);
+        const float o = gated ? w[i] * (v * inv) * silu_f(gate[off + i]) : v * inv * (1.0f + w[i]);
+        y[off + i] = o;
+        mx = fmaxf(mx, fabsf(o));
+    }
+    if (ymax) {  // uniform
+        mx = wave_max(mx);
+        if ((threadIdx.x & 63) == 0) mred[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        if (threadIdx.x == 0) ymax[blockIdx.x] = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
     }
 }
 
@@ -38,7 +48,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
 template <int NV4>
 __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const float* w, float* y,
                                                                 int rows, float eps, int gated,
-                                                                const float* gate) {
+                                                                const float* gate, float* ymax) {
     constexpr int n = NV4 * 256;
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;  // whole waves
@@ -53,6 +63,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
               static_cast<double>(v[i].z) * v[i].z + static_cast<double>(v[i].w) * v[i].w;
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(static_cast<float>(ss / n) + eps);
+    float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV4; ++i) {
         const int c = (64 * i + lane) * 4;
@@ -67,6 +78,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
                             v[i].w * inv * (1.0f + w4.w));
         }
         *reinterpret_cast<float4*>(y + off + c) = o;
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+    }
+    if (ymax) {  // uniform
+        mx = wave_max(mx);
+        if (lane == 0) ymax[row] = mx;
     }
 }
 
@@ -241,14 +257,49 @@ int grid_for(int64_t n) {
 }  // namespace
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
-                               float eps, int gated, const float* gate, hipStream_t s) {
+                               float eps, int gated, const float* gate, hipStream_t s, float* ymax) {
     const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                          reinterpret_cast<uintptr_t>(y) | (gated ? reinterpret_cast<uintptr_t>(gate) : 0);
     const int wb = (rows + 3) / 4;
-    if ((al & 15) == 0 && n == 1024) klaunch(rmsnorm_rows_wave_kernel<4>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
-    else if ((al & 15) == 0 && n == 2048) klaunch(rmsnorm_rows_wave_kernel<8>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
-    else if ((al & 15) == 0 && n == 4096) klaunch(rmsnorm_rows_wave_kernel<16>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate);
-    else klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate);
+    if ((al & 15) == 0 && n == 1024)
+        klaunch(rmsnorm_rows_wave_kernel<4>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
+    else if ((al & 15) == 0 && n == 2048)
+        klaunch(rmsnorm_rows_wave_kernel<8>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
+    else if ((al & 15) == 0 && n == 4096)
+        klaunch(rmsnorm_rows_wave_kernel<16>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
+    else klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate, ymax);
+    return hipGetLastError();
+}
+
+namespace {
+__global__ __launch_bounds__(256) void bf16_absmax_kernel(const uint16_t* w, int64_t n, unsigned* out) {
+    unsigned m = 0;  // |bf16| bits compare as unsigned in magnitude order (finite values)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        m = max(m, static_cast<unsigned>(w[i] & 0x7fffu));
+    __shared__ unsigned red[4];
+    for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), o)));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicMax(out, max(max(red[0], red[1]), max(red[2], red[3])));
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t* w, uint16_t* wh, int64_t n, float scale) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const _Float16 h = static_cast<_Float16>(bf16_to_f32(w[i]) * scale);
+        wh[i] = __builtin_bit_cast(uint16_t, h);
+    }
+}
+}  // namespace
+
+hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s) {
+    klaunch(bf16_absmax_kernel, grid_for(n), 256, 0, s, w, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_bf16_to_f16(const uint16_t* w, uint16_t* wh, int64_t n, int e, hipStream_t s) {
+    klaunch(bf16_to_f16_kernel, grid_for(n), 256, 0, s, w, wh, n, ldexpf(1.0f, e));
     return hipGetLastError();
 }
 

@@ -529,13 +529,23 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);  // the 16 lanes of the row
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / kD) + a.eps);
-        if (t >= a.T) continue;
+        const int64_t tc = t < a.T ? t : a.T - 1;  // padding rows compute but store nothing
         float* out = a.out + t * (a.VH * kD) + vh * kD;
-        const float* z = a.z ? a.z + t * a.ld_z + vh * kD : nullptr;
+        const float* z = a.z ? a.z + tc * a.ld_z + vh * kD : nullptr;
+        float mx = 0.0f;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const int col = 16 * b + lr;
-            out[col] = a.norm_w ? a.norm_w[col] * (acc[b][v] * inv) * silu_f(z[col]) : acc[b][v];
+            const float y = a.norm_w ? a.norm_w[col] * (acc[b][v] * inv) * silu_f(z[col]) : acc[b][v];
+            mx = fmaxf(mx, fabsf(y));
+            if (t < a.T) out[col] = y;
+        }
+        if (a.omax) {  // uniform: the row's maximum over this v-head's 128 columns (16 lanes)
+            mx = fmaxf(mx, __shfl_xor(mx, 1));
+            mx = fmaxf(mx, __shfl_xor(mx, 2));
+            mx = fmaxf(mx, __shfl_xor(mx, 4));
+            mx = fmaxf(mx, __shfl_xor(mx, 8));
+            if (lr == 0 && t < a.T) a.omax[t * a.VH + vh] = mx;
         }
     }
 }
@@ -937,14 +947,24 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         const int t = t0 + wave * 16 + 4 * g4 + rr;
-        if (t >= a.T) continue;
+        const int tc = min(t, a.T - 1);  // rows past the block compute but store nothing
         const float inv = 1.0f / lr[rr];
-        const float* gate = a.qkv + static_cast<int64_t>(t) * a.ld_qkv + static_cast<int64_t>(h) * 2 * kHD + kHD;
+        const float* gate = a.qkv + static_cast<int64_t>(tc) * a.ld_qkv + static_cast<int64_t>(h) * 2 * kHD + kHD;
         float* out = a.out + static_cast<int64_t>(t) * (a.NQ * kHD) + static_cast<int64_t>(h) * kHD;
+        float mx = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < 16; ++tt) {
             const int dd = 16 * tt + r16;
-            out[dd] = (o[tt][rr] * inv) * sigmoid_f(gate[dd]);
+            const float y = (o[tt][rr] * inv) * sigmoid_f(gate[dd]);
+            mx = fmaxf(mx, fabsf(y));
+            if (t < a.T) out[dd] = y;
+        }
+        if (a.omax) {  // uniform: the row's maximum over this head's 256 dims (16 lanes)
+            mx = fmaxf(mx, __shfl_xor(mx, 1));
+            mx = fmaxf(mx, __shfl_xor(mx, 2));
+            mx = fmaxf(mx, __shfl_xor(mx, 4));
+            mx = fmaxf(mx, __shfl_xor(mx, 8));
+            if (r16 == 0 && t < a.T) a.omax[static_cast<int64_t>(t) * a.NQ + h] = mx;
         }
     }
 }

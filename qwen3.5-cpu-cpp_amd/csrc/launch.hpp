@@ -79,8 +79,24 @@ struct GemmArgs {
     // W rows (2i, 2i + 1) are (gate_i, up_i), the interleaved gate/up projection: store
     // Y[m][i] = silu(gate_i) * up_i instead (Y is M x N/2, row stride ldy); R unused
     int swiglu = 0;
+    // Two-part fp16 path (when Wh and xmax are set): Wh = W x 2^w_exp as fp16 (same layout),
+    // xmax[r * xmax_n + j], j < xmax_n, partial maxima of |X| row r whose maximum scales the
+    // row into [2^14, 2^15) before its split into two fp16 parts.
+    const uint16_t* Wh = nullptr;
+    int w_exp = 0;
+    const float* xmax = nullptr;
+    int xmax_n = 0;
+    // SwiGLU output: the maximum |Y| of each row over each column tile (N / 128 wide rows:
+    // ymax[r * ceil(N / 128) + tile]) for the next GEMM's two-part path (may be null)
+    float* ymax = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Column tiles of the GEMM (the ymax row width)
+inline int gemm_col_tiles(int N) { return (N + 127) / 128; }
+// max |w| over n bf16 weights, into *out (a uint zeroed beforehand: the bits of the
+// non-negative maximum); and wh = fp16(w x 2^e), round to nearest even
+hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s);
+hipError_t launch_bf16_to_f16(const uint16_t* w, uint16_t* wh, int64_t n, int e, hipStream_t s);
 
 // ---------------------------------------------------------------- GDN decode
 struct GdnDecodeArgs {
@@ -184,6 +200,7 @@ struct GdnPrefillArgs {
     // transposed ([128 dims][64 rows])
     float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Kd, *P;
     float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
+    float* omax = nullptr;  // maximum |out| of each (token, v-head): [T][VH] (may be null)
 };
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);
 void gdn_prefill_carve(GdnPrefillArgs& a, float* ws);
@@ -204,6 +221,7 @@ struct AttnPrefillArgs {
     float* Qa;                 // workspace [NQ][T][HD]
     float* out;                // [T][NQ * HD]
     const float* rope_cs;      // optional [max_ctx][ROT] cos | sin table (else computed)
+    float* omax = nullptr;     // maximum |out| of each (token, head): [T][NQ] (may be null)
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
@@ -214,8 +232,9 @@ hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidde
 // ---------------------------------------------------------------- small kernels
 // y = W x with fp32 weights [rows][n], any n
 hipError_t launch_matvec_f32(const float* W, const float* x, float* y, int rows, int n, hipStream_t s);
+// ymax (may be null): the maximum |y| of each row
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
-                               float eps, int gated, const float* gate, hipStream_t s);
+                               float eps, int gated, const float* gate, hipStream_t s, float* ymax = nullptr);
 hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s);
 hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
                             double theta, hipStream_t s);

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -76,6 +77,11 @@ struct LayerDev {
     const float* q_norm = nullptr;
     const float* k_norm = nullptr;
     int in_rows = 0;
+    // the prefill's fp16 copies of w_in, w_out, w_gu, w_down (in the prompt arena):
+    // wh[i] = w x 2^we[i], wn[i] elements
+    uint16_t* wh[4] = {nullptr, nullptr, nullptr, nullptr};
+    int we[4] = {0, 0, 0, 0};
+    int64_t wn[4] = {0, 0, 0, 0};
 };
 
 }  // namespace
@@ -642,7 +648,21 @@ q35_status alloc_context(q35_model* m, int64_t max_ctx) {
 struct PrefillPlan {
     int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
     int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
+    // row maxima of the GEMM inputs (xn, mix, hb), the weight maxima, the fp16 weights
+    int64_t xn_max = 0, mix_max = 0, hb_max = 0, wmax = 0, wh = 0;
 };
+
+// Elements of the four projection matrices of layer l (w_in, w_out, w_gu, w_down).
+void layer_matrix_sizes(const q35_dims& d, int l, int64_t (&n)[4]) {
+    const int64_t H = d.hidden_size, I = d.ffn_intermediate;
+    const int64_t KD = d.gdn_k_heads * 128LL, VD = d.gdn_v_heads * 128LL, VH = d.gdn_v_heads;
+    const int64_t NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
+    const bool attn = (l + 1) % d.attn_interval == 0;
+    n[0] = (attn ? 2 * NQ * HD + 2 * NKV * HD : 2 * KD + VD + VD + 2 * VH) * H;
+    n[1] = H * (attn ? NQ * HD : VD);
+    n[2] = 2 * I * H;
+    n[3] = H * I;
+}
 
 int64_t proj_width(const q35_dims& d) {
     const int64_t KD = d.gdn_k_heads * 128LL, VD = d.gdn_v_heads * 128LL;
@@ -671,6 +691,17 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
                          q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
     p.logits = take(static_cast<int64_t>(p.lr) * logits_width);
     p.ids = take(T);
+    p.xn_max = take(T);
+    p.mix_max = take(T * std::max(d.attn_q_heads, d.gdn_v_heads));
+    p.hb_max = take(T * q35k::gemm_col_tiles(2 * d.ffn_intermediate));
+    p.wmax = take(4LL * d.n_layers_total);
+    int64_t wh = 0;
+    for (int l = 0; l < d.n_layers_total; ++l) {
+        int64_t n[4];
+        layer_matrix_sizes(d, l, n);
+        for (const int64_t x : n) wh += (x + 127) / 128 * 128;  // 256-B aligned fp16 matrices
+    }
+    p.wh = take(wh / 2);
     p.total = cur;
     return p;
 }
@@ -679,6 +710,43 @@ int64_t logits_width(const q35_model* m) { return std::max<int64_t>(m->d.vocab_s
 
 size_t prompt_arena_bytes(const q35_model* m, int64_t tb) {
     return static_cast<size_t>(plan_prefill(m->d, static_cast<int>(tb), logits_width(m)).total) * 4;
+}
+
+// The prefill's fp16 weight copies, in the prompt arena: per matrix its maximum |w| (one
+// readback for all), then wh = fp16(w x 2^e) with e = 15 - (exponent of the maximum as in
+// frexp), so the largest weight lies in [2^14, 2^15).
+q35_status make_prefill_weights(q35_model* m, const PrefillPlan& p) {
+    const int L = m->d.n_layers_total;
+    unsigned* wmax = reinterpret_cast<unsigned*>(reinterpret_cast<float*>(m->pf_arena) + p.wmax);
+    uint16_t* wh = reinterpret_cast<uint16_t*>(reinterpret_cast<float*>(m->pf_arena) + p.wh);
+    HIPCHK(hipMemsetAsync(wmax, 0, sizeof(unsigned) * 4 * L, m->stream));
+    for (int l = 0; l < L; ++l) {
+        LayerDev& ly = m->layers[static_cast<size_t>(l)];
+        layer_matrix_sizes(m->d, l, ly.wn);
+        const uint16_t* src[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
+        for (int i = 0; i < 4; ++i) {
+            HIPCHK(q35k::launch_bf16_absmax(src[i], ly.wn[i], wmax + 4 * l + i, m->stream));
+            ly.wh[i] = wh;
+            wh += (ly.wn[i] + 127) / 128 * 128;
+        }
+    }
+    std::vector<unsigned> mx(static_cast<size_t>(4) * L);
+    HIPCHK(hipMemcpyAsync(mx.data(), wmax, mx.size() * sizeof(unsigned), hipMemcpyDeviceToHost, m->stream));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    for (int l = 0; l < L; ++l) {
+        LayerDev& ly = m->layers[static_cast<size_t>(l)];
+        const uint16_t* src[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t bits = mx[static_cast<size_t>(4 * l + i)] << 16;  // |bf16| -> fp32
+            float w = 0.0f;
+            std::memcpy(&w, &bits, 4);
+            int ex = 0;
+            (void)std::frexp(w, &ex);
+            ly.we[i] = w > 0.0f && std::isfinite(w) ? std::min(std::max(15 - ex, -100), 100) : 0;
+            HIPCHK(q35k::launch_bf16_to_f16(src[i], ly.wh[i], ly.wn[i], ly.we[i], m->stream));
+        }
+    }
+    return Q35_OK;
 }
 
 q35_status make_prompt_arena(q35_model* m, int64_t tb) {
@@ -694,7 +762,7 @@ q35_status make_prompt_arena(q35_model* m, int64_t tb) {
     m->pf_arena = static_cast<uint8_t*>(p);
     m->pf_bytes = bytes;
     m->budget.prompt_arena_bytes = bytes;
-    return Q35_OK;
+    return make_prefill_weights(m, plan_prefill(m->d, static_cast<int>(tb), logits_width(m)));
 }
 
 int prefill_block_tokens(const q35_model* m) {
@@ -951,6 +1019,21 @@ hipError_t gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, in
     return q35k::launch_gemm(g, s);
 }
 
+// The same on the two-part fp16 path: weight matrix i of layer ly, the row maxima of X
+// (xmax_n partial maxima per row), and for the SwiGLU GEMM the row maxima of its output.
+hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const float* xmax, int xmax_n, int M, int N,
+                  int K, const float* R, float* Y, int64_t ldy, hipStream_t s, float* ymax = nullptr) {
+    const uint16_t* W[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
+    q35k::GemmArgs g{X, W[i], R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
+    g.swiglu = ymax != nullptr;
+    g.Wh = ly.wh[i];
+    g.w_exp = ly.we[i];
+    g.xmax = xmax;
+    g.xmax_n = xmax_n;
+    g.ymax = ymax;
+    return q35k::launch_gemm(g, s);
+}
+
 // One block of T tokens at positions pos0 .. pos0 + T - 1 (ids already in the arena).
 // Row r of the block is prompt row base + r of logits_host / trace_host.
 q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, int64_t base, float* logits_host,
@@ -964,14 +1047,17 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
     float* F = reinterpret_cast<float*>(m->pf_arena);
     float *hidden = F + p.hidden, *xn = F + p.xn, *proj = F + p.proj, *mix = F + p.mix;
     float *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
+    float *xn_max = F + p.xn_max, *mix_max = F + p.mix_max, *hb_max = F + p.hb_max;
     const int* ids = reinterpret_cast<const int*>(F + p.ids);
     Launcher Lr{m, s, m->timing_on};
 
     Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_embed_rows(m->embed, ids, hidden, T, H, s); });
     for (int li = 0; li < L; ++li) {
         const LayerDev& ly = m->layers[static_cast<size_t>(li)];
-        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s); });
-        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_in, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s); });
+        Lr.run(Q35_KT_OTHER, [&] {
+            return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s, xn_max);
+        });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 0, xn_max, 1, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s); });
         if (!ly.attn) {
             q35k::GdnPrefillArgs g{};
             g.T = T;
@@ -993,9 +1079,10 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             g.conv_ring = m->conv_ring + static_cast<int64_t>(ly.idx) * 4 * CONV;
             g.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
             g.out = mix;
+            g.omax = mix_max;
             q35k::gdn_prefill_carve(g, ws);
             Lr.run(Q35_KT_GDN_PREFILL, [&] { return q35k::launch_gdn_prefill(g, s); });
-            Lr.run(Q35_KT_GEMM, [&] { return gemm(mix, VD, ly.w_out, T, H, VD, hidden, hidden, H, s); });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm_h(mix, VD, ly, 1, mix_max, VH, T, H, VD, hidden, hidden, H, s); });
         } else {
             q35k::AttnPrefillArgs a{};
             a.T = T;
@@ -1016,13 +1103,21 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.rope_cs = m->rope_cs;
             a.Qa = ws;
             a.out = mix;
+            a.omax = mix_max;
             Lr.run(Q35_KT_ATTN_PREFILL, [&] { return q35k::launch_attn_prefill(a, s); });
-            Lr.run(Q35_KT_GEMM, [&] { return gemm(mix, NQ * HD, ly.w_out, T, H, NQ * HD, hidden, hidden, H, s); });
+            Lr.run(Q35_KT_GEMM, [&] {
+                return gemm_h(mix, NQ * HD, ly, 1, mix_max, NQ, T, H, NQ * HD, hidden, hidden, H, s);
+            });
         }
-        Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s); });
-        // gate/up projection with silu(gate) * up in its epilogue: hb = T x I
-        Lr.run(Q35_KT_GEMM, [&] { return gemm(xn, H, ly.w_gu, T, 2 * I, H, nullptr, hb, I, s, true); });
-        Lr.run(Q35_KT_GEMM, [&] { return gemm(hb, I, ly.w_down, T, H, I, hidden, hidden, H, s); });
+        Lr.run(Q35_KT_OTHER, [&] {
+            return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s, xn_max);
+        });
+        // gate/up projection with silu(gate) * up in its epilogue: hb = T x I, with the row
+        // maxima of hb per column tile for the down projection
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 2, xn_max, 1, T, 2 * I, H, nullptr, hb, I, s, hb_max); });
+        Lr.run(Q35_KT_GEMM, [&] {
+            return gemm_h(hb, I, ly, 3, hb_max, q35k::gemm_col_tiles(2 * I), T, H, I, hidden, hidden, H, s);
+        });
         if (trace_host)
             Lr.run(Q35_KT_OTHER, [&] {
                 return hipMemcpy2DAsync(trace_host + (base * L + li) * H, static_cast<size_t>(L) * H * 4, hidden,
