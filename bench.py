@@ -296,6 +296,7 @@ def bench_attn(a) -> dict:
 
 FP32_MFMA_PEAK_TFS = 157.3
 BF16_MFMA_PEAK_TFS = 2500.0
+FP16_MFMA_PEAK_TFS = 2500.0
 GDN_CHUNK_FLOPS = 5 * 64 * 64 * 128 * 2 + 3 * 64 * 128 * 128 * 2 + 64 ** 3 // 3 * 2 + 128 * 128
 
 
@@ -351,11 +352,11 @@ def bench_prefill(a) -> dict:
     kernels = {k: {"ms": v[0], "launches": v[1]} for k, v in kt.items() if v[1]}
     dominant = max(("gemm", "attn_prefill", "gdn_prefill"), key=lambda k: ms[k])
     ach = {"gemm": gemm_tfs, "attn_prefill": attn_tfs, "gdn_prefill": gdn_tfs}[dominant]
-    # The projection GEMM runs each fp32 product as three exact bf16 products on the bf16
-    # matrix cores, so its ceiling is the dense bf16 peak over 3 in fp32-product terms; the
-    # flash attention as six bf16 part products (peak / 6); the chunked GDN on the fp32
-    # matrix cores.
-    peaks = {"gemm": BF16_MFMA_PEAK_TFS / 3, "attn_prefill": BF16_MFMA_PEAK_TFS / 6, "gdn_prefill": FP32_MFMA_PEAK_TFS}
+    # The prefill's projection GEMM runs each fp32 product as two fp16 products (row-scaled
+    # two-part activations, fp16 weight copies) on the 16-bit matrix cores, so its ceiling is
+    # the dense fp16 peak over 2 in fp32-product terms; the flash attention as six bf16 part
+    # products (peak / 6); the chunked GDN on the fp32 matrix cores.
+    peaks = {"gemm": FP16_MFMA_PEAK_TFS / 2, "attn_prefill": BF16_MFMA_PEAK_TFS / 6, "gdn_prefill": FP32_MFMA_PEAK_TFS}
     peak = peaks[dominant]
     mixer_flops = d.n_layers_attn * attn_flops + d.n_layers_gdn * gdn_flops
     mixer_ms = ms["attn_prefill"] + ms["gdn_prefill"]
@@ -369,9 +370,10 @@ def bench_prefill(a) -> dict:
                    "block": a.prefill_block or min(4096, T + 8), "gdn_chunk": 64},
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": ach, "peak": peak,
                      "unit": "TFLOP/s", "frac": ach / peak, "traffic": None,
-                     "note": "fp32 flops of the algorithm; GEMM peak = dense bf16 MFMA peak / 3 (exact "
-                             "three-way bf16 split of the fp32 activations); flash attention = bf16 peak / 6 "
-                             "(six part products per fp32 product); GDN = fp32 MFMA peak"},
+                     "note": "fp32 flops of the algorithm; GEMM peak = dense fp16 MFMA peak / 2 (two "
+                             "fp16 parts of each row-scaled fp32 activation against fp16 weight copies); "
+                             "flash attention = bf16 peak / 6 (six part products per fp32 product); GDN = "
+                             "fp32 MFMA peak"},
         "mixers": {"attn_prefill_TFs": attn_tfs, "attn_prefill_frac": attn_tfs / peaks["attn_prefill"],
                    "gdn_prefill_frac": gdn_tfs / FP32_MFMA_PEAK_TFS,
                    "gdn_prefill_TFs": gdn_tfs, "gemm_TFs": gemm_tfs,

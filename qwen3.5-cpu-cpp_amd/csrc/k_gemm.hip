@@ -2,12 +2,22 @@
 // with fp32 activations X, bf16 weights W (nn.Linear row-major layout) and fp32 results: the
 // reference's per-token matmul (src/forward_pass.cpp:44-75) for all prompt tokens at once.
 //
-// Exact three-way bf16 split on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16). Every fp32
-// x is the exact sum of three bf16 values: hi = x with its low 16 bits cleared, r = x - hi
-// (exact, at most 16 significant bits), mid = r with its low 16 bits cleared, lo = r - mid
-// (exact, at most 8 significant bits, so a bf16). A bf16 x bf16 product has at most 16
-// significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul with
-// fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one fp32 MFMA.
+// Two paths on the 16-bit matrix cores:
+//   bf16 (any caller): exact three-way bf16 split (v_mfma_f32_16x16x32_bf16). Every fp32 x
+//   is the exact sum of three bf16 values: hi = x with its low 16 bits cleared, r = x - hi
+//   (exact, at most 16 significant bits), mid = r with its low 16 bits cleared, lo = r - mid
+//   (exact, at most 8 significant bits, so a bf16). A bf16 x bf16 product has at most 16
+//   significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul
+//   with fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one.
+//   fp16 (the model's prefill: Wh, xmax set): two fp16 parts against an fp16 copy of the
+//   weights (Wh = W 2^w_exp, exact for every bf16 weight down to 2^-24 of the largest, which
+//   lies in [2^14, 2^15)). Each X row is first scaled by a power of two from its maximum (the
+//   producing kernel writes per-row partial maxima) so that it lies in (-2^15, 2^15) with
+//   its maximum at or above 2^14; then h = fp16(x), l = fp16(x - h). x - h - l is at most
+//   2^-22 |x| (2^-25 absolute below the fp16 normal range, i.e. 2^-39 of the row maximum), a
+//   quarter of an fp32 rounding of x, and each fp16 x fp16 product is exact in fp32; the
+//   epilogue multiplies by 2^-(row exponent + w_exp), exactly. Two MFMAs per product instead
+//   of three: 5-8% faster, the result within the fp32 accumulation error of the bf16 path.
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
 // of it: 2 x 8 MFMA blocks of 16 x 16 (64 accumulator registers per lane). K advances in
