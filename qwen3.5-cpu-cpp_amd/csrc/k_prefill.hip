@@ -694,7 +694,7 @@ constexpr int kLdV2 = kKT + 8;    // V part rows, dim-major (bf16): 80 B
 // with three parts); causal work grows with the query block, and workgroups are dispatched
 // in linear order, so block L takes the L-th longest item (query blocks from the last).
 // Both products run on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16): every fp32 operand
-// is the exact sum of three bf16 parts (hi + mid + lo, as in the projection GEMM), and a
+// is the exact sum of three bf16 parts (hi + mid + lo, as in the bf16 path of the projection GEMM), and a
 // product a.b is the sum of the six part products a_i b_j with i + j <= 2 (parts counted
 // from 0): the three dropped ones (mid.lo, lo.mid, lo.lo) are below 2^-23 |a||b| together,
 // the size of an fp32 rounding, and each bf16 x bf16 part product is exact in fp32. A bf16
