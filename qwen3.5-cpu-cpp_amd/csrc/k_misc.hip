@@ -294,7 +294,8 @@ __global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t* w, uin
 }  // namespace
 
 hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s) {
-    klaunch(bf16_absmax_kernel, grid_for(n), 256, 0, s, w, n, out);
+    // 256 workgroups: each ends with one atomic on the same word, so fewer is faster
+    klaunch(bf16_absmax_kernel, std::min(grid_for(n), 256), 256, 0, s, w, n, out);
     return hipGetLastError();
 }
 
