@@ -66,8 +66,9 @@ typedef struct q35_dims {
 } q35_dims;
 
 /* Bytes per arena. Mirrors MemoryBudget, include/memory_budget.h:6-19, plus the prompt arena
- * of the chunked prefill (activations of one block of prompt tokens), which the reference
- * does not have: q35_compute_budget leaves it 0, q35_model_budget reports the model's. */
+ * of the chunked prefill (activations of one block of prompt tokens and the fp16 copies of
+ * the projection weights its GEMMs multiply), which the reference does not have:
+ * q35_compute_budget leaves it 0, q35_model_budget reports the model's. */
 typedef struct q35_budget {
     uint64_t weight_bytes;
     uint64_t gdn_state_bytes;
