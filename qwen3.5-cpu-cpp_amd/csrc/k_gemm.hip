@@ -9,7 +9,8 @@
 //   (exact, at most 8 significant bits, so a bf16). A bf16 x bf16 product has at most 16
 //   significant bits and is exact in fp32, so W.x = W.hi + W.mid + W.lo is the fp32 matmul
 //   with fp32 accumulation -- three bf16 MFMAs at 16x the fp32-MFMA rate instead of one.
-//   fp16 (the model's prefill: Wh, xmax set): two fp16 parts against an fp16 copy of the
+//   fp16 (the model's prefill: Wh, xmax set, X in the tiled layout of xt_off so that each
+//   wave-wide 16-byte load reads one contiguous KB): two fp16 parts against an fp16 copy of the
 //   weights (Wh = W 2^w_exp, exact for every bf16 weight down to 2^-24 of the largest, which
 //   lies in [2^14, 2^15)). Each X row is first scaled by a power of two from its maximum (the
 //   producing kernel writes per-row partial maxima) so that it lies in (-2^15, 2^15) with
@@ -102,7 +103,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
     for (int r = 0; r < 2; ++r) {
         const int row = m0 + wave * 32 + 16 * r + l16;
         arow_i[r] = row < a.M ? row : 0;
-        arow[r] = a.X + static_cast<int64_t>(arow_i[r]) * a.ldx;
+        // F16 (tiled X): the lane's 16 bytes in the first k block of its row block
+        arow[r] = F16 ? a.X + static_cast<int64_t>((m0 >> 4) + 2 * wave + r) * (a.K >> 5) * 512 + (l16 << 4) +
+                            ((lane >> 4) << 2)
+                      : a.X + static_cast<int64_t>(arow_i[r]) * a.ldx;
     }
     // F16: each row's scale 2^xe, xe = 15 - (exponent of its maximum |x| as in frexp), so
     // the row lies in (-2^15, 2^15) with its maximum at or above 2^14; exact in fp32
@@ -131,8 +135,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                xa[r][i] = *reinterpret_cast<const uint4*>(arow[r] + min(k0 + kq + 4 * i, a.K - 4));
+            for (int i = 0; i < 2; ++i) {
+                if constexpr (F16)  // one 1 KB contiguous block per wave-wide load
+                    xa[r][i] = *reinterpret_cast<const uint4*>(arow[r] + (min(k0, a.K - 32) >> 5) * 512 + 256 * i);
+                else
+                    xa[r][i] = *reinterpret_cast<const uint4*>(arow[r] + min(k0 + kq + 4 * i, a.K - 4));
+            }
     };
     auto load_w = [&](uint4 (&wb)[2], int k0) {
 #pragma unroll
@@ -269,7 +277,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
                     const float h = silu_f(acc[r][j][v]) * up;
                     if (!(lane & 1) && col + 1 < a.N) {
                         ym[r][v] = fmaxf(ym[r][v], fabsf(h));
-                        if (row < a.M) a.Y[static_cast<int64_t>(row) * a.ldy + (col >> 1)] = h;
+                        if (row < a.M)
+                            a.Y[a.y_tiled ? xt_off(row, col >> 1, a.N >> 1)
+                                          : static_cast<int64_t>(row) * a.ldy + (col >> 1)] = h;
                     }
                 }
         }
@@ -333,7 +343,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     dim3 grid(gemm_col_tiles(a.N), (a.M + kBM - 1) / kBM);
-    const bool f16 = a.Wh && a.xmax && a.xmax_n > 0;
+    const bool f16 = a.Wh && a.xmax && a.xmax_n > 0 && a.x_tiled && a.K % 32 == 0;
+    // the tiled layouts exist on the two-part path only (Y: its SwiGLU output)
+    if ((a.x_tiled && !f16) || (a.y_tiled && !(f16 && a.swiglu && (a.N / 2) % 32 == 0))) return hipErrorInvalidValue;
     if (f16) {
         if (a.swiglu) klaunch(gemm_kernel<2, true>, grid, 256, 0, s, a);
         else if (a.R) klaunch(gemm_kernel<1, true>, grid, 256, 0, s, a);

@@ -16,7 +16,8 @@ namespace {
 // y = w * (x * rsqrt(mean(x^2) + eps)) * silu(gate).
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const float* w,
                                                            float* y, int n, float eps,
-                                                           int gated, const float* gate, float* ymax) {
+                                                           int gated, const float* gate, float* ymax,
+                                                           int y_tiled) {
     __shared__ double red[4];
     __shared__ float mred[4];
     const int64_t off = static_cast<int64_t>(blockIdx.x) * n;
@@ -31,7 +32,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
     for (int i = threadIdx.x; i < n; i += 256) {
         const float v = x[off + i];
         const float o = gated ? w[i] * (v * inv) * silu_f(gate[off + i]) : v * inv * (1.0f + w[i]);
-        y[off + i] = o;
+        y[y_tiled ? xt_off(blockIdx.x, i, n) : off + i] = o;
         mx = fmaxf(mx, fabsf(o));
     }
     if (ymax) {  // uniform
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
 template <int NV4>
 __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const float* w, float* y,
                                                                 int rows, float eps, int gated,
-                                                                const float* gate, float* ymax) {
+                                                                const float* gate, float* ymax, int y_tiled) {
     constexpr int n = NV4 * 256;
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;  // whole waves
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
             o = make_float4(v[i].x * inv * (1.0f + w4.x), v[i].y * inv * (1.0f + w4.y), v[i].z * inv * (1.0f + w4.z),
                             v[i].w * inv * (1.0f + w4.w));
         }
-        *reinterpret_cast<float4*>(y + off + c) = o;
+        *reinterpret_cast<float4*>(y + (y_tiled ? xt_off(row, c, n) : off + c)) = o;
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
     }
     if (ymax) {  // uniform
@@ -257,17 +258,18 @@ int grid_for(int64_t n) {
 }  // namespace
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
-                               float eps, int gated, const float* gate, hipStream_t s, float* ymax) {
+                               float eps, int gated, const float* gate, hipStream_t s, float* ymax, int y_tiled) {
+    if (y_tiled && n % 32 != 0) return hipErrorInvalidValue;
     const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                          reinterpret_cast<uintptr_t>(y) | (gated ? reinterpret_cast<uintptr_t>(gate) : 0);
     const int wb = (rows + 3) / 4;
     if ((al & 15) == 0 && n == 1024)
-        klaunch(rmsnorm_rows_wave_kernel<4>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
+        klaunch(rmsnorm_rows_wave_kernel<4>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax, y_tiled);
     else if ((al & 15) == 0 && n == 2048)
-        klaunch(rmsnorm_rows_wave_kernel<8>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
+        klaunch(rmsnorm_rows_wave_kernel<8>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax, y_tiled);
     else if ((al & 15) == 0 && n == 4096)
-        klaunch(rmsnorm_rows_wave_kernel<16>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax);
-    else klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate, ymax);
+        klaunch(rmsnorm_rows_wave_kernel<16>, wb, 256, 0, s, x, w, y, rows, eps, gated, gate, ymax, y_tiled);
+    else klaunch(rmsnorm_rows_kernel, rows, 256, 0, s, x, w, y, n, eps, gated, gate, ymax, y_tiled);
     return hipGetLastError();
 }
 

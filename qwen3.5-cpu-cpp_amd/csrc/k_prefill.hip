@@ -538,7 +538,10 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
             const int col = 16 * b + lr;
             const float y = a.norm_w ? a.norm_w[col] * (acc[b][v] * inv) * silu_f(z[col]) : acc[b][v];
             mx = fmaxf(mx, fabsf(y));
-            if (t < a.T) out[col] = y;
+            if (t < a.T) {
+                if (a.out_tiled) a.out[xt_off(t, vh * kD + col, a.VH * kD)] = y;
+                else out[col] = y;
+            }
         }
         if (a.omax) {  // uniform: the row's maximum over this v-head's 128 columns (16 lanes)
             mx = fmaxf(mx, __shfl_xor(mx, 1));
@@ -957,7 +960,10 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
             const int dd = 16 * tt + r16;
             const float y = (o[tt][rr] * inv) * sigmoid_f(gate[dd]);
             mx = fmaxf(mx, fabsf(y));
-            if (t < a.T) out[dd] = y;
+            if (t < a.T) {
+                if (a.out_tiled) a.out[xt_off(t, h * kHD + dd, a.NQ * kHD)] = y;
+                else out[dd] = y;
+            }
         }
         if (a.omax) {  // uniform: the row's maximum over this head's 256 dims (16 lanes)
             mx = fmaxf(mx, __shfl_xor(mx, 1));

@@ -89,8 +89,20 @@ struct GemmArgs {
     // SwiGLU output: the maximum |Y| of each row over each column tile (N / 128 wide rows:
     // ymax[r * ceil(N / 128) + tile]) for the next GEMM's two-part path (may be null)
     float* ymax = nullptr;
+    // X (two-part path) and, for SwiGLU, Y in the tiled layout of xt_off (ldx / ldy unused;
+    // rows padded to a multiple of 128, K to a multiple of 32)
+    int x_tiled = 0, y_tiled = 0;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Tiled activation layout of the two-part GEMM's X operand: blocks of 16 rows x 32 k
+// (512 floats), row block after row block and within one the k blocks in order; inside a
+// block [h][r][g][e] for k = 8 g + 4 h + e of row r: the 16 bytes a lane of the matrix-core
+// operand loads per instruction are contiguous, 1 KB per wave-wide load. K % 32 == 0.
+__host__ __device__ inline int64_t xt_off(int64_t row, int k, int K) {
+    return ((row >> 4) * (K >> 5) + (k >> 5)) * 512 + (((k & 7) >> 2) << 8) + ((row & 15) << 4) +
+           (((k & 31) >> 3) << 2) + (k & 3);
+}
+inline int64_t rows_tiled(int64_t rows) { return (rows + 127) / 128 * 128; }
 // Column tiles of the GEMM (the ymax row width)
 inline int gemm_col_tiles(int N) { return (N + 127) / 128; }
 // max |w| over n bf16 weights, into *out (a uint zeroed beforehand: the bits of the
@@ -201,6 +213,7 @@ struct GdnPrefillArgs {
     float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Kd, *P;
     float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
     float* omax = nullptr;  // maximum |out| of each (token, v-head): [T][VH] (may be null)
+    int out_tiled = 0;      // out in the xt_off layout (K = VH * 128)
 };
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T);
 void gdn_prefill_carve(GdnPrefillArgs& a, float* ws);
@@ -222,6 +235,7 @@ struct AttnPrefillArgs {
     float* out;                // [T][NQ * HD]
     const float* rope_cs;      // optional [max_ctx][ROT] cos | sin table (else computed)
     float* omax = nullptr;     // maximum |out| of each (token, head): [T][NQ] (may be null)
+    int out_tiled = 0;         // out in the xt_off layout (K = NQ * HD)
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
@@ -234,7 +248,8 @@ hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidde
 hipError_t launch_matvec_f32(const float* W, const float* x, float* y, int rows, int n, hipStream_t s);
 // ymax (may be null): the maximum |y| of each row
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
-                               float eps, int gated, const float* gate, hipStream_t s, float* ymax = nullptr);
+                               float eps, int gated, const float* gate, hipStream_t s, float* ymax = nullptr,
+                               int y_tiled = 0);
 hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s);
 hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
                             double theta, hipStream_t s);

@@ -647,6 +647,7 @@ q35_status alloc_context(q35_model* m, int64_t max_ctx) {
 // The logits rows are wide enough for either output head (vocab_size or the embedding's rows).
 struct PrefillPlan {
     int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
+    int tiled = 0;       // xn, mix, hb in the tiled layout of the two-part GEMM (H, I % 32 == 0)
     int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
     // row maxima of the GEMM inputs (xn, mix, hb), the weight maxima, the fp16 weights
     int64_t xn_max = 0, mix_max = 0, hb_max = 0, wmax = 0, wh = 0;
@@ -674,6 +675,7 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
     PrefillPlan p;
     p.tb = tb;
     p.lr = std::min(tb, 256);
+    p.tiled = d.hidden_size % 32 == 0 && d.ffn_intermediate % 32 == 0;
     const int64_t H = d.hidden_size, I = d.ffn_intermediate, T = tb;
     const int64_t VD = d.gdn_v_heads * 128LL, QD = static_cast<int64_t>(d.attn_q_heads) * d.attn_head_dim;
     int64_t cur = 0;
@@ -682,11 +684,13 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
         cur += (n + 63) / 64 * 64;
         return o;
     };
+    // xn, mix and hb feed the two-part GEMM in its tiled layout: rows padded to 128
+    const int64_t TP = q35k::rows_tiled(T);
     p.hidden = take(T * H);
-    p.xn = take(T * H);
+    p.xn = take(TP * H);
     p.proj = take(T * proj_width(d));
-    p.mix = take(T * std::max(VD, QD));
-    p.hb = take(T * I);
+    p.mix = take(TP * std::max(VD, QD));
+    p.hb = take(TP * I);
     p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
                          q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
     p.logits = take(static_cast<int64_t>(p.lr) * logits_width);
@@ -1022,7 +1026,7 @@ hipError_t gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, in
 // The same on the two-part fp16 path: weight matrix i of layer ly, the row maxima of X
 // (xmax_n partial maxima per row), and for the SwiGLU GEMM the row maxima of its output.
 hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const float* xmax, int xmax_n, int M, int N,
-                  int K, const float* R, float* Y, int64_t ldy, hipStream_t s, float* ymax = nullptr) {
+                  int K, const float* R, float* Y, int64_t ldy, hipStream_t s, int tiled, float* ymax = nullptr) {
     const uint16_t* W[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
     q35k::GemmArgs g{X, W[i], R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
     g.swiglu = ymax != nullptr;
@@ -1031,6 +1035,8 @@ hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const 
     g.xmax = xmax;
     g.xmax_n = xmax_n;
     g.ymax = ymax;
+    g.x_tiled = tiled;
+    g.y_tiled = tiled && ymax != nullptr;
     return q35k::launch_gemm(g, s);
 }
 
@@ -1055,9 +1061,9 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
     for (int li = 0; li < L; ++li) {
         const LayerDev& ly = m->layers[static_cast<size_t>(li)];
         Lr.run(Q35_KT_OTHER, [&] {
-            return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s, xn_max);
+            return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s, xn_max, p.tiled);
         });
-        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 0, xn_max, 1, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 0, xn_max, 1, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s, p.tiled); });
         if (!ly.attn) {
             q35k::GdnPrefillArgs g{};
             g.T = T;
@@ -1080,9 +1086,10 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             g.state = m->gdn_state + static_cast<int64_t>(ly.idx) * VH * 128 * 128;
             g.out = mix;
             g.omax = mix_max;
+            g.out_tiled = p.tiled;
             q35k::gdn_prefill_carve(g, ws);
             Lr.run(Q35_KT_GDN_PREFILL, [&] { return q35k::launch_gdn_prefill(g, s); });
-            Lr.run(Q35_KT_GEMM, [&] { return gemm_h(mix, VD, ly, 1, mix_max, VH, T, H, VD, hidden, hidden, H, s); });
+            Lr.run(Q35_KT_GEMM, [&] { return gemm_h(mix, VD, ly, 1, mix_max, VH, T, H, VD, hidden, hidden, H, s, p.tiled); });
         } else {
             q35k::AttnPrefillArgs a{};
             a.T = T;
@@ -1104,19 +1111,20 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.Qa = ws;
             a.out = mix;
             a.omax = mix_max;
+            a.out_tiled = p.tiled;
             Lr.run(Q35_KT_ATTN_PREFILL, [&] { return q35k::launch_attn_prefill(a, s); });
             Lr.run(Q35_KT_GEMM, [&] {
-                return gemm_h(mix, NQ * HD, ly, 1, mix_max, NQ, T, H, NQ * HD, hidden, hidden, H, s);
+                return gemm_h(mix, NQ * HD, ly, 1, mix_max, NQ, T, H, NQ * HD, hidden, hidden, H, s, p.tiled);
             });
         }
         Lr.run(Q35_KT_OTHER, [&] {
-            return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s, xn_max);
+            return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s, xn_max, p.tiled);
         });
         // gate/up projection with silu(gate) * up in its epilogue: hb = T x I, with the row
         // maxima of hb per column tile for the down projection
-        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 2, xn_max, 1, T, 2 * I, H, nullptr, hb, I, s, hb_max); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 2, xn_max, 1, T, 2 * I, H, nullptr, hb, I, s, p.tiled, hb_max); });
         Lr.run(Q35_KT_GEMM, [&] {
-            return gemm_h(hb, I, ly, 3, hb_max, q35k::gemm_col_tiles(2 * I), T, H, I, hidden, hidden, H, s);
+            return gemm_h(hb, I, ly, 3, hb_max, q35k::gemm_col_tiles(2 * I), T, H, I, hidden, hidden, H, s, p.tiled);
         });
         if (trace_host)
             Lr.run(Q35_KT_OTHER, [&] {
