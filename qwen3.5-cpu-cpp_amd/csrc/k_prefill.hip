@@ -688,8 +688,6 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 constexpr int kFW = 8;            // waves per workgroup
 constexpr int kQT = 16 * kFW;     // query rows per workgroup (16 per wave)
 constexpr int kKT = 32;           // keys per tile
-constexpr int kLdK2 = kHD + 8;    // K part rows (bf16): 528 B, the 16 rows of a read on distinct banks
-constexpr int kLdV2 = kKT + 8;    // V part rows, dim-major (bf16): 80 B
 
 // 128 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
 // the cache, 32-key tiles staged through LDS (the next tile's rows are loaded into registers
@@ -736,8 +734,13 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
     const int grp = a.NQ / a.NKV, kh = h / grp;
     const int t0 = qt * kQT;
     const int r16 = lane & 15, g4 = lane >> 4;
-    __shared__ __align__(16) uint16_t Kp[NP][kKT][kLdK2];
-    __shared__ __align__(16) uint16_t Vt[NP][kHD][kLdV2];
+    // LDS in 16-byte chunks (8 bf16) so that the 16 lanes of a lane group read one whole
+    // 256-byte row of 16 chunks (any order within the row runs at full rate; rows of padded
+    // or scattered chunks at 0.6 of it): K chunk (key, dims 8 dc ..) at Kc[p][key / 16][dc]
+    // [key % 16], V chunk (dim, key slots 8 g ..) at Vc[p][dim / 16][g][(dim % 16) ^ 4 g]
+    // (the XOR puts the 8 lanes of each staging store on distinct banks).
+    __shared__ __align__(16) uint4 Kc[NP][2][kHD / 8][16];
+    __shared__ __align__(16) uint4 Vc[NP][kHD / 16][4][16];
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
     // this lane's query row, dims 32c + 8 g4 .. + 7, as three bf16 parts (the B operand)
@@ -768,69 +771,81 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
 
     const int kv_end = a.pos0 + min(a.T, t0 + kQT);
     const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;
-    // staging of one tile, in registers while the previous tile is multiplied: K rows
-    // tid / 16, dims 16 (tid % 16) .. + 15 (four float4); V keys 4 (tid / 64) .. + 3, dims
-    // 4 (tid % 64) .. + 3 (one float4 per key); split (or widened) when stored to LDS
-    const int ks_row = tid >> 4, ks_d = (tid & 15) * 16;
-    const int vs_k = (tid >> 6) * 4, vs_d = (tid & 63) * 4;
-    float4 kst[4], vst[4];
+    // staging of one tile, in registers while the previous tile is multiplied: K key
+    // 8 (wave % 4) + lane % 8, dim chunks 8 c + lane / 8 for c = 2 (wave / 4) + i, i < 2 (two
+    // float4 each); V dims 2 (tid / 4), + 1 of the eight keys of slot chunk g = tid % 4 (keys
+    // 4 g .. + 3 and 16 + 4 g .. + 3, one float2 each); split (or widened) when stored to LDS
+    const int ks_row = 8 * (wave & 3) + (lane & 7), ks_c0 = 16 * (wave >> 2) + (lane >> 3);
+    const int vs_g = tid & 3, vs_d = (tid >> 2) * 2;
+    float4 kst[4];
+    float2 vst[8];
+    auto vkey = [&](int j) { return (j < 4 ? 0 : 12) + 4 * vs_g + j; };  // key of slot 8 g + j
     auto load_tile = [&](int kv0) {
         const bool live = kv0 < kv_end;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int pk = min(kv0 + ks_row, kv_end - 1), pv = min(kv0 + vs_k + j, kv_end - 1);
-            const int64_t ok = live ? static_cast<int64_t>(pk) * kHD + ks_d + 4 * j : 0;
-            const int64_t ov = live ? static_cast<int64_t>(pv) * kHD + vs_d : 0;
+            const int pk = min(kv0 + ks_row, kv_end - 1);
+            const int64_t ok = live ? static_cast<int64_t>(pk) * kHD + 8 * (ks_c0 + 8 * (j >> 1)) + 4 * (j & 1) : 0;
             if constexpr (KVB) {
                 const uint2 kb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff + ok);
-                const uint2 vb = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff + ov);
                 kst[j] = make_float4(bf16_lo(kb.x), bf16_hi(kb.x), bf16_lo(kb.y), bf16_hi(kb.y));
-                vst[j] = make_float4(bf16_lo(vb.x), bf16_hi(vb.x), bf16_lo(vb.y), bf16_hi(vb.y));
             } else {
                 kst[j] = *reinterpret_cast<const float4*>(a.k_cache + hoff + ok);
-                vst[j] = *reinterpret_cast<const float4*>(a.v_cache + hoff + ov);
             }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int pv = min(kv0 + vkey(j), kv_end - 1);
+            const int64_t ov = live ? static_cast<int64_t>(pv) * kHD + vs_d : 0;
+            if constexpr (KVB) {
+                const uint32_t vb = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff + ov);
+                vst[j] = make_float2(bf16_lo(vb), bf16_hi(vb));
+            } else {
+                vst[j] = *reinterpret_cast<const float2*>(a.v_cache + hoff + ov);
+            }
+        }
+    };
+    // eight floats as NP 16-byte chunks: three exact bf16 parts, or (a bf16 cache) the values
+    auto parts8 = [&](const float (&x)[8], uint4 (&c)[NP]) {
+        if constexpr (KVB) {
+            c[0] = make_uint4(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
+                              __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u),
+                              __float_as_uint(x[4]) >> 16 | (__float_as_uint(x[5]) & 0xffff0000u),
+                              __float_as_uint(x[6]) >> 16 | (__float_as_uint(x[7]) & 0xffff0000u));
+        } else {
+            const float lo[4] = {x[0], x[1], x[2], x[3]}, hi[4] = {x[4], x[5], x[6], x[7]};
+            uint2 p0[3], p1[3];
+            split3_4(lo, p0);
+            split3_4(hi, p1);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) c[p] = make_uint4(p0[p].x, p0[p].y, p1[p].x, p1[p].y);
         }
     };
     auto store_tile = [&](int kv0) {
         // K: rows past the end are zero (their scores are masked anyway)
         const bool kok = kv0 + ks_row < kv_end;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float x[4] = {kok ? kst[j].x : 0.f, kok ? kst[j].y : 0.f, kok ? kst[j].z : 0.f, kok ? kst[j].w : 0.f};
-            if constexpr (KVB) {
-                *reinterpret_cast<uint2*>(&Kp[0][ks_row][ks_d + 4 * j]) =
-                    make_uint2(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
-                               __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u));
-            } else {
-                uint2 pt[3];
-                split3_4(x, pt);
+        for (int i = 0; i < 2; ++i) {
+            const float4 u = kst[2 * i], w = kst[2 * i + 1];
+            const float x[8] = {kok ? u.x : 0.f, kok ? u.y : 0.f, kok ? u.z : 0.f, kok ? u.w : 0.f,
+                                kok ? w.x : 0.f, kok ? w.y : 0.f, kok ? w.z : 0.f, kok ? w.w : 0.f};
+            uint4 c[NP];
+            parts8(x, c);
 #pragma unroll
-                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Kp[p][ks_row][ks_d + 4 * j]) = pt[p];
-            }
+            for (int p = 0; p < NP; ++p) Kc[p][ks_row >> 4][ks_c0 + 8 * i][ks_row & 15] = c[p];
         }
-        // V, transposed: dim vs_d + e gets the four keys vs_k .. + 3 at their slots (zero past
+        // V, dim-major: dims vs_d, vs_d + 1 get the eight keys of slot chunk vs_g (zero past
         // the end: 0 * V must stay 0, and P is 0 there)
-        const int slot = vslot(vs_k);  // the four keys take four consecutive slots
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float x[4];
+        for (int e = 0; e < 2; ++e) {
+            float x[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 v = vst[j];
-                const float ve = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-                x[j] = kv0 + vs_k + j < kv_end ? ve : 0.0f;
-            }
-            if constexpr (KVB) {
-                *reinterpret_cast<uint2*>(&Vt[0][vs_d + e][slot]) =
-                    make_uint2(__float_as_uint(x[0]) >> 16 | (__float_as_uint(x[1]) & 0xffff0000u),
-                               __float_as_uint(x[2]) >> 16 | (__float_as_uint(x[3]) & 0xffff0000u));
-            } else {
-                uint2 pt[3];
-                split3_4(x, pt);
+            for (int j = 0; j < 8; ++j) x[j] = kv0 + vkey(j) < kv_end ? (e ? vst[j].y : vst[j].x) : 0.0f;
+            uint4 c[NP];
+            parts8(x, c);
+            const int d = vs_d + e;
 #pragma unroll
-                for (int p = 0; p < NP; ++p) *reinterpret_cast<uint2*>(&Vt[p][vs_d + e][slot]) = pt[p];
-            }
+            for (int p = 0; p < NP; ++p) Vc[p][d >> 4][vs_g][(d & 15) ^ (4 * vs_g)] = c[p];
         }
     };
     load_tile(0);
@@ -852,7 +867,7 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
                     bf16x8 kop[NP];
 #pragma unroll
                     for (int p = 0; p < NP; ++p)
-                        kop[p] = *reinterpret_cast<const bf16x8*>(&Kp[p][16 * hf + r16][32 * c + 8 * g4]);
+                        kop[p] = __builtin_bit_cast(bf16x8, Kc[p][hf][4 * c + g4][r16]);
                     floatx4& b = sb[c & 1];
                     if constexpr (KVB) {
                         b = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[0], qp[2][c], b, 0, 0, 0);
@@ -923,7 +938,7 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
             for (int t = 0; t < 16; ++t) {
                 bf16x8 vb[NP];
 #pragma unroll
-                for (int q = 0; q < NP; ++q) vb[q] = *reinterpret_cast<const bf16x8*>(&Vt[q][16 * t + r16][8 * g4]);
+                for (int q = 0; q < NP; ++q) vb[q] = __builtin_bit_cast(bf16x8, Vc[q][t][g4][r16 ^ (4 * g4)]);
                 floatx4 ob = floatx4{0.f, 0.f, 0.f, 0.f};
                 if constexpr (KVB) {
                     ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], ob, 0, 0, 0);
