@@ -274,11 +274,23 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int row
 }
 
 namespace {
+// max |w| of n bf16 values as the bits of the largest |bf16| (|bf16| bits compare as unsigned
+// in magnitude order for finite values); VEC: 16-byte loads (w 16-byte aligned, n % 8 == 0)
+template <bool VEC>
 __global__ __launch_bounds__(256) void bf16_absmax_kernel(const uint16_t* w, int64_t n, unsigned* out) {
-    unsigned m = 0;  // |bf16| bits compare as unsigned in magnitude order (finite values)
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256)
-        m = max(m, static_cast<unsigned>(w[i] & 0x7fffu));
+    unsigned m = 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    if constexpr (VEC) {
+        const uint4* w8 = reinterpret_cast<const uint4*>(w);
+        auto m2 = [](unsigned x) { return max(x & 0x7fffu, (x >> 16) & 0x7fffu); };
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n / 8; i += stride) {
+            const uint4 v = w8[i];
+            m = max(m, max(max(m2(v.x), m2(v.y)), max(m2(v.z), m2(v.w))));
+        }
+    } else {
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+            m = max(m, static_cast<unsigned>(w[i] & 0x7fffu));
+    }
     __shared__ unsigned red[4];
     for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), o)));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
@@ -286,23 +298,42 @@ __global__ __launch_bounds__(256) void bf16_absmax_kernel(const uint16_t* w, int
     if (threadIdx.x == 0) atomicMax(out, max(max(red[0], red[1]), max(red[2], red[3])));
 }
 
+// wh = fp16(w * scale); VEC: eight values per thread with 16-byte loads and stores
+template <bool VEC>
 __global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t* w, uint16_t* wh, int64_t n, float scale) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        const _Float16 h = static_cast<_Float16>(bf16_to_f32(w[i]) * scale);
-        wh[i] = __builtin_bit_cast(uint16_t, h);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    if constexpr (VEC) {
+        auto cv = [&](unsigned x) {
+            const _Float16 lo = static_cast<_Float16>(__uint_as_float(x << 16) * scale);
+            const _Float16 hi = static_cast<_Float16>(__uint_as_float(x & 0xffff0000u) * scale);
+            return static_cast<unsigned>(__builtin_bit_cast(uint16_t, lo)) |
+                   (static_cast<unsigned>(__builtin_bit_cast(uint16_t, hi)) << 16);
+        };
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n / 8; i += stride) {
+            const uint4 v = reinterpret_cast<const uint4*>(w)[i];
+            reinterpret_cast<uint4*>(wh)[i] = make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
+        }
+    } else {
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+            const _Float16 h = static_cast<_Float16>(bf16_to_f32(w[i]) * scale);
+            wh[i] = __builtin_bit_cast(uint16_t, h);
+        }
     }
 }
 }  // namespace
 
 hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s) {
-    // 256 workgroups: each ends with one atomic on the same word, so fewer is faster
-    klaunch(bf16_absmax_kernel, std::min(grid_for(n), 256), 256, 0, s, w, n, out);
+    // at most 1024 workgroups: each ends with one atomic on the same word
+    if ((reinterpret_cast<uintptr_t>(w) & 15) == 0 && n % 8 == 0)
+        klaunch(bf16_absmax_kernel<true>, std::min(grid_for(n / 8), 1024), 256, 0, s, w, n, out);
+    else klaunch(bf16_absmax_kernel<false>, std::min(grid_for(n), 1024), 256, 0, s, w, n, out);
     return hipGetLastError();
 }
 
 hipError_t launch_bf16_to_f16(const uint16_t* w, uint16_t* wh, int64_t n, int e, hipStream_t s) {
-    klaunch(bf16_to_f16_kernel, grid_for(n), 256, 0, s, w, wh, n, ldexpf(1.0f, e));
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(wh)) & 15) == 0 && n % 8 == 0)
+        klaunch(bf16_to_f16_kernel<true>, grid_for(n / 8), 256, 0, s, w, wh, n, ldexpf(1.0f, e));
+    else klaunch(bf16_to_f16_kernel<false>, grid_for(n), 256, 0, s, w, wh, n, ldexpf(1.0f, e));
     return hipGetLastError();
 }
 
