@@ -688,6 +688,7 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(AttnPrefillArgs 
 constexpr int kFW = 8;            // waves per workgroup
 constexpr int kQT = 16 * kFW;     // query rows per workgroup (16 per wave)
 constexpr int kKT = 32;           // keys per tile
+constexpr float kLog2e = 1.44269504088896341f;
 
 // 128 query rows of one head per workgroup (16 per wave), causal, keys of earlier blocks from
 // the cache, 32-key tiles staged through LDS (the next tile's rows are loaded into registers
@@ -821,26 +822,24 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
             for (int p = 0; p < NP; ++p) c[p] = make_uint4(p0[p].x, p0[p].y, p1[p].x, p1[p].y);
         }
     };
+    // Rows past the end of the keys are copies of the last one (finite): their scores are
+    // masked to -inf, so their weights are exactly 0 and 0 * V adds nothing.
     auto store_tile = [&](int kv0) {
-        // K: rows past the end are zero (their scores are masked anyway)
-        const bool kok = kv0 + ks_row < kv_end;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const float4 u = kst[2 * i], w = kst[2 * i + 1];
-            const float x[8] = {kok ? u.x : 0.f, kok ? u.y : 0.f, kok ? u.z : 0.f, kok ? u.w : 0.f,
-                                kok ? w.x : 0.f, kok ? w.y : 0.f, kok ? w.z : 0.f, kok ? w.w : 0.f};
+            const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
             uint4 c[NP];
             parts8(x, c);
 #pragma unroll
             for (int p = 0; p < NP; ++p) Kc[p][ks_row >> 4][ks_c0 + 8 * i][ks_row & 15] = c[p];
         }
-        // V, dim-major: dims vs_d, vs_d + 1 get the eight keys of slot chunk vs_g (zero past
-        // the end: 0 * V must stay 0, and P is 0 there)
+        // V, dim-major: dims vs_d, vs_d + 1 get the eight keys of slot chunk vs_g
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             float x[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = kv0 + vkey(j) < kv_end ? (e ? vst[j].y : vst[j].x) : 0.0f;
+            for (int j = 0; j < 8; ++j) x[j] = e ? vst[j].y : vst[j].x;
             uint4 c[NP];
             parts8(x, c);
             const int d = vs_d + e;
@@ -900,11 +899,14 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
             // no key yet keeps -inf and weight 0
             const float m_new = tm > m_run + 8.0f ? tm : m_run;
             const bool live = m_new != -INFINITY;
-            const float f = live ? expf(m_run - m_new) : 1.0f;
+            // e^y as the native 2^(y log2 e): y = score - max is formed exactly as before, so
+            // the product's rounding moves a weight by |y| 2^-24 relative (1 ulp of v_exp_f32
+            // besides), negligible where the weights are large
+            const float f = live ? __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e) : 1.0f;
             float p[8], ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                p[i] = live ? expf(sv[i] - m_new) : 0.0f;
+                p[i] = live ? __builtin_amdgcn_exp2f((sv[i] - m_new) * kLog2e) : 0.0f;
                 ps += p[i];
             }
             ps += __shfl_xor(ps, 16);
@@ -939,18 +941,18 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
                 bf16x8 vb[NP];
 #pragma unroll
                 for (int q = 0; q < NP; ++q) vb[q] = __builtin_bit_cast(bf16x8, Vc[q][t][g4][r16 ^ (4 * g4)]);
-                floatx4 ob = floatx4{0.f, 0.f, 0.f, 0.f};
+                // the part products straight into the running output, smallest first
                 if constexpr (KVB) {
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], ob, 0, 0, 0);
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], ob, 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], o[t], 0, 0, 0);
                 } else {
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], ob, 0, 0, 0);
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[1 % NP], ob, 0, 0, 0);
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[2 % NP], ob, 0, 0, 0);
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], ob, 0, 0, 0);
-                    ob = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[1 % NP], ob, 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[2], vb[0], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[1 % NP], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[2 % NP], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vb[0], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[1 % NP], o[t], 0, 0, 0);
                 }
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[0], o[t] + ob, 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vb[0], o[t], 0, 0, 0);
             }
         }
         lds_barrier();  // every wave is done with this tile
