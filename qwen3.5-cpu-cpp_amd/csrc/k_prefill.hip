@@ -824,7 +824,7 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
     };
     // Rows past the end of the keys are copies of the last one (finite): their scores are
     // masked to -inf, so their weights are exactly 0 and 0 * V adds nothing.
-    auto store_tile = [&](int kv0) {
+    auto store_tile = [&]() {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const float4 u = kst[2 * i], w = kst[2 * i + 1];
@@ -848,7 +848,7 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
         }
     };
     load_tile(0);
-    store_tile(0);
+    store_tile();
     lds_barrier();
     for (int kv0 = 0; kv0 < kv_end; kv0 += kKT) {
         load_tile(kv0 + kKT);  // in flight during this tile's products
@@ -957,7 +957,7 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
         }
         lds_barrier();  // every wave is done with this tile
         if (kv0 + kKT < kv_end) {
-            store_tile(kv0 + kKT);
+            store_tile();
             lds_barrier();
         }
     }

@@ -289,3 +289,22 @@ def test_ffn_wider_than_64kb_of_lds(tmp_path):
     pf = m.prefill(prompt)
     m.close()
     assert rel_l2(pf, lg) < REL_L2
+
+
+def test_prefill_widths_not_multiple_of_32(tmp_path):
+    """Hidden 264 and FFN 520 (multiples of 8, not of 32): the prefill keeps its activations
+    row-major and the projections take the three-part bf16 GEMM; the prefill logits equal the
+    oracle's step logits token by token."""
+    d = pyq35.default_dims(hidden_size=264, n_layers_total=4, gdn_k_heads=2, gdn_v_heads=2,
+                           attn_q_heads=2, attn_kv_heads=1, ffn_intermediate=520,
+                           vocab_size=1024, native_max_context=4096)
+    path = str(tmp_path / "odd")
+    pyq35.synth_write_model(path, d, seed=7, std=0.02)
+    prompt = pyq35.synth_token_ids(7, d.vocab_size, 40)
+    m = pyq35.Model(path, 64)
+    pf = m.prefill(prompt)
+    m.close()
+    o = op.Oracle(path, 64)
+    ref = np.stack([o.step(int(t)) for t in prompt])
+    o.close()
+    assert rel_l2(pf, ref) < REL_L2
