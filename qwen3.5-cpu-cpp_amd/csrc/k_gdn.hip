@@ -37,11 +37,12 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     constexpr int NRG = 256 / CS;
     constexpr int RPT = kD / NRG;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // workgroups are dispatched to the 8 XCDs in turn: with VH a multiple of 8, the NSPLIT
-    // slices of a head get ids of one residue mod 8, so they run on one XCD and its L2
-    // fetches the head's shared q / k rows once
+    // workgroups are dispatched to the 8 XCDs in turn: in a launch of 32-column slices (one
+    // layer, the decode step) with VH a multiple of 8, the slices of a head get ids of one
+    // residue mod 8, so they run on one XCD and its L2 fetches the head's shared q / k rows
+    // once (the 64-column launches of many layers run 6% faster without it)
     int vh, split;
-    if (NSPLIT > 1 && (a.VH & 7) == 0) {
+    if (NSPLIT == 4 && (a.VH & 7) == 0) {
         const int xcd = blockIdx.x & 7, rest = blockIdx.x >> 3;
         split = rest % NSPLIT;
         vh = xcd + 8 * (rest / NSPLIT);
