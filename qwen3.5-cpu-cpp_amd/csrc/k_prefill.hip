@@ -712,9 +712,6 @@ constexpr float kLog2e = 1.44269504088896341f;
 //         which the gfx950 matrix cores run at half the 32-deep one's rate.)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// position of a tile's key in the V rows (and k slot of the P operand)
-__device__ __forceinline__ int vslot(int key) { return 8 * ((key & 15) >> 2) + 4 * (key >> 4) + (key & 3); }
-
 // the three bf16 parts of four floats, each part as four packed bf16 (element 0 low)
 __device__ __forceinline__ void split3_4(const float (&x)[4], uint2 (&part)[3]) {
     uint32_t h[4], m[4], l[4];
