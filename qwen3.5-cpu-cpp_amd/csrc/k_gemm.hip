@@ -241,8 +241,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
             load_a(xa[f & 1], k0 + 2 * kBK);
             // keep the loads ahead of the products (the scheduler would sink them)
             __builtin_amdgcn_sched_barrier(0);
+            // the products at raised wave priority: the issue arbiter then prefers the wave
+            // that feeds the matrix core over its SIMD partner's loads and splits
+            __builtin_amdgcn_s_setprio(1);
             if (f == 0) products(aop, f & 1, std::true_type{});
             else products(aop, f & 1, std::false_type{});
+            __builtin_amdgcn_s_setprio(0);
             lds_barrier();  // LDS only: the loads stay in flight
         }
 #pragma unroll
