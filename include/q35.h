@@ -377,7 +377,11 @@ q35_status q35_gdn_prefill(const q35_gdn_prefill_args *args, q35_stream s);
  * to the caches at pos0 + t, softmax over positions [0, pos0 + t], times sigmoid(gate).
  *   qkv [n][ld_qkv]: NQ x [q | gate] (2 HD each), then NKV x k, then NKV x v
  *   k_cache, v_cache [NKV][max_context][HD]; out [n][NQ * HD]
- * workspace: q35_attn_prefill_workspace_bytes() bytes. Requires HD == 256. */
+ * workspace (16-byte aligned): q35_attn_prefill_workspace_bytes() bytes. With an fp32 cache
+ * that size includes the keys and values of positions [0, pos0 + n) pre-split into the
+ * attention kernel's tile layout (3 KB per position and kv head); a workspace of at least
+ * NQ * n * HD * 4 + 256 bytes but smaller than that is accepted, and the kernel then splits
+ * every tile itself (slower, same results). Requires HD == 256. */
 typedef struct q35_attn_prefill_args {
     int32_t n_tokens, pos0, q_heads, kv_heads, head_dim, rotary_dim;
     int32_t kv_dtype;      /* cache elements: 0 = fp32, 1 = bf16 (as q35_attn_decode_args) */

@@ -293,9 +293,19 @@ q35_status q35_gdn_prefill(const q35_gdn_prefill_args* args, q35_stream s) {
     return launched(q35k::launch_gdn_prefill(a, as_stream(s)), "q35_gdn_prefill");
 }
 
+namespace {
+// without the pre-split key / value tiles (the least q35_attn_prefill accepts)
+uint64_t attn_prefill_min_bytes(const q35_attn_prefill_args& g) {
+    return static_cast<uint64_t>(q35k::attn_prefill_workspace_floats(g.q_heads, g.n_tokens)) * 4;
+}
+}  // namespace
+
 uint64_t q35_attn_prefill_workspace_bytes(const q35_attn_prefill_args* args) {
     if (!args || args->q_heads <= 0 || args->n_tokens <= 0) return 0;
-    return static_cast<uint64_t>(q35k::attn_prefill_workspace_floats(args->q_heads, args->n_tokens)) * 4;
+    uint64_t n = attn_prefill_min_bytes(*args);
+    if (args->kv_dtype == 0 && args->kv_heads > 0 && args->pos0 >= 0)
+        n += static_cast<uint64_t>(q35k::attn_prefill_image_floats(args->kv_heads, args->pos0, args->n_tokens)) * 4;
+    return n;
 }
 
 q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
@@ -314,10 +324,12 @@ q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
     if (g.kv_dtype != 0 && g.kv_dtype != 1) return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: kv_dtype %d", g.kv_dtype);
     if (g.ld_qkv < 2LL * g.q_heads * 256 + 2LL * g.kv_heads * 256)
         return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: leading dimension too small");
-    if (g.workspace_bytes < q35_attn_prefill_workspace_bytes(args))
+    if (g.workspace_bytes < attn_prefill_min_bytes(g))
         return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: workspace of %llu bytes, needs %llu",
                          static_cast<unsigned long long>(g.workspace_bytes),
-                         static_cast<unsigned long long>(q35_attn_prefill_workspace_bytes(args)));
+                         static_cast<unsigned long long>(attn_prefill_min_bytes(g)));
+    if ((reinterpret_cast<uintptr_t>(g.workspace) & 15) != 0)
+        return q35::fail(Q35_ERR_ARG, "q35_attn_prefill: workspace not 16-byte aligned");
     q35k::AttnPrefillArgs a{};
     a.T = g.n_tokens;
     a.NQ = g.q_heads;
@@ -335,6 +347,8 @@ q35_status q35_attn_prefill(const q35_attn_prefill_args* args, q35_stream s) {
     a.v_cache = g.v_cache;
     a.kv_bf16 = g.kv_dtype == 1;
     a.Qa = static_cast<float*>(g.workspace);
+    if (!a.kv_bf16 && g.workspace_bytes >= q35_attn_prefill_workspace_bytes(args))
+        a.kv_img = a.Qa + q35k::attn_prefill_workspace_floats(a.NQ, a.T);
     a.out = g.out;
     return launched(q35k::launch_attn_prefill(a, as_stream(s)), "q35_attn_prefill");
 }

@@ -722,8 +722,61 @@ __device__ __forceinline__ void split3_4(const float (&x)[4], uint2 (&part)[3]) 
     part[2] = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
 }
 
-template <bool KVB>
+// eight floats as three 16-byte chunks, the exact bf16 parts of each (elements 0..7 in order)
+__device__ __forceinline__ void split3_8(const float (&x)[8], uint4 (&c)[3]) {
+    const float lo[4] = {x[0], x[1], x[2], x[3]}, hi[4] = {x[4], x[5], x[6], x[7]};
+    uint2 p0[3], p1[3];
+    split3_4(lo, p0);
+    split3_4(hi, p1);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) c[p] = make_uint4(p0[p].x, p0[p].y, p1[p].x, p1[p].y);
+}
+
+// The flash kernel's LDS image of one 32-key tile of an fp32 cache: K chunks Kc[3][2][32][16]
+// then V chunks Vc[3][16][4][16] (the layouts described at that kernel), 16-byte chunks.
+constexpr int kImgK = 3 * 2 * (kHD / 8) * 16;
+constexpr int kImgTile = 2 * kImgK;
+// key of slot 8 g + j of a V chunk: keys 4 g .. + 3 of the tile's first half, then the same
+// four of its second half
+__device__ __forceinline__ int vslot_key(int g, int j) { return (j < 4 ? 0 : 12) + 4 * g + j; }
+
+// grid (tiles, NKV), 256 threads: writes the LDS image of every tile of keys [0, pos0 + T) of
+// one kv head (rows past the last key are copies of it), so that the flash kernel stages a
+// tile by a plain copy instead of splitting it again in every query-block workgroup.
+__global__ __launch_bounds__(256) void attn_kv_image_kernel(AttnPrefillArgs a) {
+    const int ti = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int last = a.pos0 + a.T - 1;
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;
+    uint4* img = static_cast<uint4*>(a.kv_img) + (static_cast<int64_t>(kh) * gridDim.x + ti) * kImgTile;
+    // K chunk (key, dims 8 dc ..): lanes walk the dim chunks of one key
+    for (int e = tid; e < kKT * (kHD / 8); e += 256) {
+        const int key = e >> 5, dc = e & 31;
+        const float* src = a.k_cache + hoff + static_cast<int64_t>(min(ti * kKT + key, last)) * kHD + 8 * dc;
+        const float4 u = *reinterpret_cast<const float4*>(src), w = *reinterpret_cast<const float4*>(src + 4);
+        const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+        uint4 c[3];
+        split3_8(x, c);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) img[((p * 2 + (key >> 4)) * (kHD / 8) + dc) * 16 + (key & 15)] = c[p];
+    }
+    // V chunk (dim d, slot chunk g): lanes walk the dims of the same eight keys
+    for (int e = tid; e < kHD * 4; e += 256) {
+        const int d = e & (kHD - 1), g = e >> 8;
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            x[j] = a.v_cache[hoff + static_cast<int64_t>(min(ti * kKT + vslot_key(g, j), last)) * kHD + d];
+        uint4 c[3];
+        split3_8(x, c);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) img[kImgK + ((p * (kHD / 16) + (d >> 4)) * 4 + g) * 16 + ((d & 15) ^ (4 * g))] = c[p];
+    }
+}
+
+// IMG (fp32 cache only): tiles are copied from the image attn_kv_image_kernel wrote.
+template <bool KVB, bool IMG>
 __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs a) {
+    static_assert(!(KVB && IMG), "the tile image holds the parts of an fp32 cache");
     constexpr int NP = KVB ? 1 : 3;  // parts of K and V
     const int nqt = gridDim.x;
     const int rank = blockIdx.x + blockIdx.y * nqt;
@@ -775,10 +828,20 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
     // 4 g .. + 3 and 16 + 4 g .. + 3, one float2 each); split (or widened) when stored to LDS
     const int ks_row = 8 * (wave & 3) + (lane & 7), ks_c0 = 16 * (wave >> 2) + (lane >> 3);
     const int vs_g = tid & 3, vs_d = (tid >> 2) * 2;
-    float4 kst[4];
-    float2 vst[8];
-    auto vkey = [&](int j) { return (j < 4 ? 0 : 12) + 4 * vs_g + j; };  // key of slot 8 g + j
+    float4 kst[IMG ? 1 : 4];
+    float2 vst[IMG ? 1 : 8];
+    // (vector-typed: an array of uint4 structs here was placed in scratch memory)
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 ist[IMG ? kImgTile / (kFW * 64) : 1];
+    auto vkey = [&](int j) { return vslot_key(vs_g, j); };
     auto load_tile = [&](int kv0) {
+        if constexpr (IMG) {  // tiles past the block's keys: the last one again (in the image)
+            const u32x4* src = static_cast<const u32x4*>(a.kv_img) +
+                               (static_cast<int64_t>(kh) * a.img_tiles + min(kv0, kv_end - 1) / kKT) * kImgTile;
+#pragma unroll
+            for (int j = 0; j < kImgTile / (kFW * 64); ++j) ist[j] = src[tid + kFW * 64 * j];
+            return;
+        }
         const bool live = kv0 < kv_end;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -811,17 +874,20 @@ __global__ __launch_bounds__(kFW * 64, 1) void flash_attn_kernel(AttnPrefillArgs
                               __float_as_uint(x[4]) >> 16 | (__float_as_uint(x[5]) & 0xffff0000u),
                               __float_as_uint(x[6]) >> 16 | (__float_as_uint(x[7]) & 0xffff0000u));
         } else {
-            const float lo[4] = {x[0], x[1], x[2], x[3]}, hi[4] = {x[4], x[5], x[6], x[7]};
-            uint2 p0[3], p1[3];
-            split3_4(lo, p0);
-            split3_4(hi, p1);
-#pragma unroll
-            for (int p = 0; p < NP; ++p) c[p] = make_uint4(p0[p].x, p0[p].y, p1[p].x, p1[p].y);
+            split3_8(x, c);
         }
     };
     // Rows past the end of the keys are copies of the last one (finite): their scores are
     // masked to -inf, so their weights are exactly 0 and 0 * V adds nothing.
     auto store_tile = [&]() {
+        if constexpr (IMG) {  // the image is the two arrays' contents, chunk for chunk
+            constexpr int NJ = kImgTile / (kFW * 64);
+#pragma unroll
+            for (int j = 0; j < NJ / 2; ++j) reinterpret_cast<u32x4*>(&Kc[0][0][0][0])[tid + kFW * 64 * j] = ist[j];
+#pragma unroll
+            for (int j = 0; j < NJ / 2; ++j) reinterpret_cast<u32x4*>(&Vc[0][0][0][0])[tid + kFW * 64 * j] = ist[NJ / 2 + j];
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const float4 u = kst[2 * i], w = kst[2 * i + 1];
@@ -1047,14 +1113,25 @@ hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
 }
 
 int64_t attn_prefill_workspace_floats(int NQ, int T) { return static_cast<int64_t>(NQ) * T * kHD + 64; }
+int attn_prefill_image_tiles(int pos0, int T) { return (pos0 + T + kKT - 1) / kKT; }
+int64_t attn_prefill_image_floats(int NKV, int pos0, int T) {
+    return static_cast<int64_t>(NKV) * attn_prefill_image_tiles(pos0, T) * kImgTile * 4;
+}
 
 hipError_t launch_attn_prefill(const AttnPrefillArgs& in, hipStream_t s) {
     AttnPrefillArgs a = in;
     if (a.ROT % 8 == 0) klaunch(attn_prefill_prep_kernel, a.T, 256, 0, s, a);
     else klaunch(attn_prefill_prep_any_kernel, dim3(a.T, a.NQ + a.NKV), 256, 0, s, a);
     const dim3 grid((a.T + kQT - 1) / kQT, a.NQ);
-    if (a.kv_bf16) klaunch(flash_attn_kernel<true>, grid, kFW * 64, 0, s, a);
-    else klaunch(flash_attn_kernel<false>, grid, kFW * 64, 0, s, a);
+    if (a.kv_bf16) {
+        klaunch(flash_attn_kernel<true, false>, grid, kFW * 64, 0, s, a);
+    } else if (a.kv_img) {
+        a.img_tiles = attn_prefill_image_tiles(a.pos0, a.T);
+        klaunch(attn_kv_image_kernel, dim3(a.img_tiles, a.NKV), 256, 0, s, a);
+        klaunch(flash_attn_kernel<false, true>, grid, kFW * 64, 0, s, a);
+    } else {
+        klaunch(flash_attn_kernel<false, false>, grid, kFW * 64, 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -236,8 +236,14 @@ struct AttnPrefillArgs {
     const float* rope_cs;      // optional [max_ctx][ROT] cos | sin table (else computed)
     float* omax = nullptr;     // maximum |out| of each (token, head): [T][NQ] (may be null)
     int out_tiled = 0;         // out in the xt_off layout (K = NQ * HD)
+    // optional (fp32 cache): attn_prefill_image_floats(NKV, pos0, T) floats, 16-byte aligned,
+    // for the keys and values pre-split into the attention kernel's tile layout
+    void* kv_img = nullptr;
+    int img_tiles = 0;  // set by the launch
 };
 int64_t attn_prefill_workspace_floats(int NQ, int T);
+int attn_prefill_image_tiles(int pos0, int T);
+int64_t attn_prefill_image_floats(int NKV, int pos0, int T);
 hipError_t launch_attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
 // h[t][i] = silu(gu[t][2i]) * gu[t][2i + 1] (gate / up columns interleaved)
 // hidden[t][:] = bf16 embed[ids[t]][:]

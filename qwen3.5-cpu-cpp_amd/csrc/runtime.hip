@@ -649,6 +649,7 @@ struct PrefillPlan {
     int tb = 0, lr = 0;  // tokens per block, logits rows per output-head pass
     int tiled = 0;       // xn, mix, hb in the tiled layout of the two-part GEMM (H, I % 32 == 0)
     int64_t hidden = 0, xn = 0, proj = 0, mix = 0, hb = 0, ws = 0, logits = 0, ids = 0, total = 0;
+    int64_t ws_n = 0;  // floats at ws
     // row maxima of the GEMM inputs (xn, mix, hb), the weight maxima, the fp16 weights
     int64_t xn_max = 0, mix_max = 0, hb_max = 0, wmax = 0, wh = 0;
 };
@@ -691,8 +692,9 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
     p.proj = take(T * proj_width(d));
     p.mix = take(TP * std::max(VD, QD));
     p.hb = take(TP * I);
-    p.ws = take(std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
-                         q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb)));
+    p.ws_n = std::max(q35k::gdn_prefill_workspace_floats(d.gdn_k_heads, d.gdn_v_heads, tb),
+                      q35k::attn_prefill_workspace_floats(d.attn_q_heads, tb));
+    p.ws = take(p.ws_n);
     p.logits = take(static_cast<int64_t>(p.lr) * logits_width);
     p.ids = take(T);
     p.xn_max = take(T);
@@ -1109,6 +1111,10 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             a.kv_bf16 = m->kv_elem == 2;
             a.rope_cs = m->rope_cs;
             a.Qa = ws;
+            // the pre-split key / value tiles where they fit in the rest of the workspace
+            // (the GDN layers' share is the larger one at 2B shapes: up to ~35k keys)
+            const int64_t qa_n = q35k::attn_prefill_workspace_floats(NQ, T);
+            if (!a.kv_bf16 && qa_n + q35k::attn_prefill_image_floats(NKV, pos0, T) <= p.ws_n) a.kv_img = ws + qa_n;
             a.out = mix;
             a.omax = mix_max;
             a.out_tiled = p.tiled;

@@ -169,7 +169,7 @@ def test_gdn_prefill_512_tokens_state(hip):
 
 
 # ----------------------------------------------------------------------------- attention
-def run_attn_prefill(hip, nq, nkv, T, pos0, seed, rot=64):
+def run_attn_prefill(hip, nq, nkv, T, pos0, seed, rot=64, ws_min=False):
     rng = np.random.default_rng(seed)
     d = pyq35.default_dims(attn_q_heads=nq, attn_kv_heads=nkv)
     d.partial_rotary_factor = rot / 256.0
@@ -189,6 +189,8 @@ def run_attn_prefill(hip, nq, nkv, T, pos0, seed, rot=64):
                                      rotary_dim=rot, max_context=maxc, rope_theta=d.rope_theta,
                                      eps=d.rms_norm_eps, ld_qkv=ld)
         ws = pyq35.lib.q35_attn_prefill_workspace_bytes(args)
+        if ws_min:  # no room for the pre-split tiles: the kernel splits them itself
+            ws = nq * T * HD * 4 + 256
         args.qkv = B.up("rows", rows)
         args.q_norm, args.k_norm = B.up("qn", qnw), B.up("kn", knw)
         args.k_cache, args.v_cache = B.up("K", Kd), B.up("V", Vd)
@@ -225,6 +227,18 @@ def test_attn_prefill_vs_oracle(hip, nq, nkv, T, pos0):
     for kh in range(nkv):
         np.testing.assert_allclose(Kdev[kh, :pos0 + T], Ko[:pos0 + T, kh], rtol=2e-6, atol=2e-6)
         np.testing.assert_array_equal(Vdev[kh, :pos0 + T], Vo[:pos0 + T, kh])
+
+
+@pytest.mark.parametrize("nq,nkv,T,pos0", [(2, 1, 70, 0), (8, 2, 65, 37), (16, 2, 300, 1000)])
+def test_attn_prefill_split_tiles_match_presplit(hip, nq, nkv, T, pos0):
+    """A workspace without room for the pre-split key / value tiles runs the kernel that splits
+    each tile itself: the same parts and products, so the same output bit for bit, and both
+    within the bar against the oracle."""
+    seed = 7 * T + pos0
+    out_img, ref, _, _, _, _ = run_attn_prefill(hip, nq, nkv, T, pos0, seed=seed)
+    out_own, _, _, _, _, _ = run_attn_prefill(hip, nq, nkv, T, pos0, seed=seed, ws_min=True)
+    np.testing.assert_array_equal(out_img, out_own)
+    assert max(rel_l2(out_img[t], ref[t]) for t in range(T)) < REL_L2
 
 
 @pytest.mark.parametrize("rot", [0, 18, 32, 256])
