@@ -239,6 +239,19 @@ def test_kernel_entry_points_validate_before_launch():
                                qkv=1 << 20)
     assert pyq35.lib.q35_attn_prefill(C.byref(ap), None) == -1
     assert b"kv_dtype" in pyq35.lib.q35_last_error()
+    # workspace: the full size holds the pre-split K / V tiles of an fp32 cache (3 KB per
+    # position and kv head, 32-position tiles); below the Q parts alone, or misaligned: refused
+    ap.kv_dtype, ap.n_tokens, ap.pos0, ap.max_context = 0, 40, 30, 128
+    q_only = 8 * 40 * 256 * 4 + 256
+    assert pyq35.lib.q35_attn_prefill_workspace_bytes(C.byref(ap)) == q_only + 2 * 3 * 96 * 1024
+    ap.kv_dtype = 1
+    assert pyq35.lib.q35_attn_prefill_workspace_bytes(C.byref(ap)) == q_only
+    ap.workspace_bytes = q_only - 4
+    assert pyq35.lib.q35_attn_prefill(C.byref(ap), None) == -1
+    assert b"workspace of" in pyq35.lib.q35_last_error()
+    ap.workspace_bytes, ap.workspace = q_only, (1 << 20) + 8
+    assert pyq35.lib.q35_attn_prefill(C.byref(ap), None) == -1
+    assert b"aligned" in pyq35.lib.q35_last_error()
     assert pyq35.lib.q35_matmul_bf16(None, None, None, 4, 8, None) == -1
     assert pyq35.lib.q35_matmul_bf16(1 << 20, 1 << 20, 1 << 20, 4, 12, None) == -7
 
