@@ -357,7 +357,9 @@ q35_status q35_attn_decode_static(const q35_attn_decode_args *args, q35_stream s
  *   qkv [n][ld_qkv] (CONV pre-conv channels), z [n][ld_z] (VD), b, a [n][ld_ba] (VH each)
  *   conv_w, A_log, dt_bias, norm_w, conv_ring, state as for q35_gdn_decode
  *   out [n][VD]: gated-rmsnorm output (raw readout when norm_w is NULL)
- * workspace: q35_gdn_prefill_workspace_bytes() bytes. Requires DK == DV == 128, KER == 4. */
+ * workspace: q35_gdn_prefill_workspace_bytes() bytes. Requires DK == DV == 128, KER == 4;
+ * qkv, conv_ring, conv_w and workspace 16-byte aligned and ld_qkv a multiple of 4 (read 16
+ * bytes at a time), else Q35_ERR_ARG. */
 typedef struct q35_gdn_prefill_args {
     int32_t n_tokens, pos0, k_heads, v_heads, head_dim_k, head_dim_v, conv_kernel;
     float eps;

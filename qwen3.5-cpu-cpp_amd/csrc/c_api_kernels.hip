@@ -265,6 +265,12 @@ q35_status q35_gdn_prefill(const q35_gdn_prefill_args* args, q35_stream s) {
     const int64_t CONV = 2LL * g.k_heads * 128 + g.v_heads * 128;
     if (g.ld_qkv < CONV || (g.z && g.ld_z < g.v_heads * 128LL) || g.ld_ba < g.v_heads)
         return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: leading dimension too small");
+    // the conv pass reads qkv rows, the ring and the taps 16 bytes at a time, and carves the
+    // workspace into float4-aligned arrays
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (g.ld_qkv % 4 != 0 || !a16(g.qkv) || !a16(g.conv_ring) || !a16(g.conv_w) || !a16(g.workspace))
+        return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: qkv, conv_ring, conv_w and workspace must be 16-byte aligned "
+                                      "and ld_qkv a multiple of 4");
     if (g.workspace_bytes < q35_gdn_prefill_workspace_bytes(args))
         return q35::fail(Q35_ERR_ARG, "q35_gdn_prefill: workspace of %llu bytes, needs %llu",
                          static_cast<unsigned long long>(g.workspace_bytes),

@@ -15,10 +15,12 @@
 //   lies in [2^14, 2^15)). Each X row is first scaled by a power of two from its maximum (the
 //   producing kernel writes per-row partial maxima) so that it lies in (-2^15, 2^15) with
 //   its maximum at or above 2^14; then h = fp16(x), l = fp16(x - h). x - h - l is at most
-//   2^-22 |x| (2^-25 absolute below the fp16 normal range, i.e. 2^-39 of the row maximum), a
-//   quarter of an fp32 rounding of x, and each fp16 x fp16 product is exact in fp32; the
+//   2^-22 |x| (2^-25 absolute below the fp16 normal range, i.e. 2^-39 of the row maximum):
+//   four times fp32's unit roundoff 2^-24, so h + l carries about 22 significant bits of x
+//   where the three bf16 parts carry all 24. Each fp16 x fp16 product is exact in fp32; the
 //   epilogue multiplies by 2^-(row exponent + w_exp), exactly. Two MFMAs per product instead
-//   of three: 5-8% faster, the result within the fp32 accumulation error of the bf16 path.
+//   of three: 5-8% faster; against float64 the outputs stay within the fp32 accumulation
+//   error (the dropped 2^-22 |x| averages out over K like the accumulator's own roundings).
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
 // of it: 2 x 8 MFMA blocks of 16 x 16 (64 accumulator registers per lane). K advances in

@@ -597,25 +597,88 @@ ScratchPlan scratch_plan(const q35_dims& d, int64_t max_ctx) {
     return p;
 }
 
-// (Re)makes the KV and scratch arenas for max_ctx positions (one hipMalloc each), zeroed,
-// with the RoPE table filled; the model is at position 0 afterwards.
-q35_status alloc_context(q35_model* m, int64_t max_ctx) {
+size_t kv_arena_bytes(const q35_model* m, int64_t max_ctx) {
     const q35_dims& d = m->d;
-    if (m->kv_arena) HIPCHK(hipFree(m->kv_arena));
-    if (m->scratch) HIPCHK(hipFree(m->scratch));
+    return static_cast<size_t>(d.n_layers_attn) * 2 * d.attn_kv_heads * static_cast<size_t>(max_ctx) *
+           d.attn_head_dim * m->kv_elem;
+}
+
+// The KV and scratch arenas for max_ctx positions, both or neither (a failed second
+// allocation frees the first).
+hipError_t alloc_context_pair(const q35_model* m, int64_t max_ctx, void** kv, void** sc) {
+    *kv = *sc = nullptr;
+    hipError_t e = dev_alloc(kv, std::max<size_t>(kv_arena_bytes(m, max_ctx), 256));
+    if (e == hipSuccess) e = dev_alloc(sc, scratch_plan(m->d, max_ctx).bytes);
+    if (e != hipSuccess) {
+        if (*kv) (void)hipFree(*kv);
+        *kv = *sc = nullptr;
+        (void)hipGetLastError();  // the failed allocation is reported by the caller
+    }
+    return e;
+}
+
+void release_context(q35_model* m) {
+    if (m->kv_arena) (void)hipFree(m->kv_arena);
+    if (m->scratch) (void)hipFree(m->scratch);
     m->kv_arena = nullptr;
     m->scratch = nullptr;
+    m->max_ctx = 0;
+    m->kv_bytes = 0;
+    m->scratch_bytes = 0;
+    m->pos = 0;
+}
+
+// The KV cache and scratch arenas exist (a failed q35_model_reserve_context that could not
+// make any context arenas again leaves a model without them).
+q35_status need_context(const q35_model* m) {
+    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    if (!m->scratch || !m->kv_arena)
+        return q35::fail(Q35_ERR_RANGE, "the model has no context arenas (a context reservation failed)");
+    return Q35_OK;
+}
+
+q35_status install_context(q35_model* m, int64_t max_ctx, void* kv, void* sc);
+
+// (Re)makes the KV and scratch arenas for max_ctx positions (one hipMalloc each), zeroed,
+// with the RoPE table filled; the model is at position 0 afterwards. The new arenas are
+// made while the old ones still exist and replace them only when both were made; when they
+// do not fit beside the old ones, the old ones are freed and the new size tried again, then
+// the old size. Should even that fail, the model keeps no context arenas (max_context 0)
+// and every call that needs them refuses with Q35_ERR_RANGE instead of touching them.
+q35_status alloc_context(q35_model* m, int64_t max_ctx) {
+    const int64_t old_ctx = m->scratch ? m->max_ctx : 0;
+    void *kv = nullptr, *sc = nullptr;
+    hipError_t e = alloc_context_pair(m, max_ctx, &kv, &sc);
+    if (e != hipSuccess && old_ctx > 0) {
+        release_context(m);
+        e = alloc_context_pair(m, max_ctx, &kv, &sc);
+        if (e != hipSuccess) {
+            const hipError_t e_old = alloc_context_pair(m, old_ctx, &kv, &sc);
+            if (e_old == hipSuccess) {
+                const q35_status st = install_context(m, old_ctx, kv, sc);
+                if (st != Q35_OK) return st;
+                return q35::fail(Q35_ERR_HIP, "context arenas for %lld positions: %s (the %lld-position arenas were made again)",
+                                 static_cast<long long>(max_ctx), hipGetErrorString(e), static_cast<long long>(old_ctx));
+            }
+        }
+    }
+    if (e != hipSuccess)
+        return q35::fail(Q35_ERR_HIP, "context arenas for %lld positions: %s", static_cast<long long>(max_ctx),
+                         hipGetErrorString(e));
+    release_context(m);
+    return install_context(m, max_ctx, kv, sc);
+}
+
+// Takes over kv / sc (made by alloc_context_pair for max_ctx) as the model's context arenas.
+q35_status install_context(q35_model* m, int64_t max_ctx, void* kv, void* sc) {
+    const q35_dims& d = m->d;
+    m->kv_arena = static_cast<float*>(kv);
+    m->scratch = static_cast<uint8_t*>(sc);
     m->max_ctx = max_ctx;
-    m->kv_bytes = static_cast<size_t>(d.n_layers_attn) * 2 * d.attn_kv_heads * static_cast<size_t>(max_ctx) *
-                  d.attn_head_dim * m->kv_elem;
+    m->kv_bytes = kv_arena_bytes(m, max_ctx);
     m->n_splits = q35k::attn_default_splits(max_ctx, d.attn_kv_heads, m->n_cu);
     const ScratchPlan sp = scratch_plan(d, max_ctx);
     m->scratch_bytes = sp.bytes;
-    void* p = nullptr;
-    HIPCHK(dev_alloc(&p, std::max<size_t>(m->kv_bytes, 256)));
-    m->kv_arena = static_cast<float*>(p);
-    HIPCHK(dev_alloc(&p, m->scratch_bytes));
-    m->scratch = static_cast<uint8_t*>(p);
     auto S32 = [&](size_t off) { return reinterpret_cast<float*>(m->scratch + off); };
     const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
     m->hidden = S32(sp.hidden);
@@ -1006,7 +1069,10 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     st = alloc_context(m.get(), max_ctx);
     if (st != Q35_OK) return st;
     if (prefill_block > 0) {
-        st = make_prompt_arena(m.get(), std::min<int64_t>(prefill_block, max_ctx));
+        // the block size the arena is made for: a block beyond max_context is never run, and
+        // a later q35_model_reserve_context keeps blocks within this arena
+        m->pf_planned = static_cast<int>(std::min<int64_t>(prefill_block, max_ctx));
+        st = make_prompt_arena(m.get(), m->pf_planned);
         if (st != Q35_OK) return st;
     }
     std::cerr << "[q35] device arenas (max_context=" << max_ctx << "): weights " << (m->w_bytes >> 20)
@@ -1167,6 +1233,7 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
 // logits of the last token, its argmax in token_dev and ids_dev[pos + n - 1].
 q35_status extend(q35_model* m, const int32_t* ids, int32_t n, float* logits_host, float* trace_host) {
     if (!m || !ids || n <= 0) return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     if (m->pos + n > m->max_ctx)
         return q35::fail(Q35_ERR_RANGE, "position %lld + %d tokens exceeds max_context %lld", (long long)m->pos, n,
                          (long long)m->max_ctx);
@@ -1274,7 +1341,8 @@ q35_status q35_model_synchronize(q35_model* m) {
 }
 
 q35_status q35_model_reset(q35_model* m) {
-    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    const q35_status nc = need_context(m);
+    if (nc != Q35_OK) return nc;
     HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
     HIPCHK(q35k::launch_fill_f32(m->kv_arena, static_cast<int64_t>(m->kv_bytes / 4), 0.0f, m->stream));
     HIPCHK(q35k::launch_set_int(m->pos_dev, 0, m->stream));
@@ -1283,7 +1351,8 @@ q35_status q35_model_reset(q35_model* m) {
 }
 
 q35_status q35_model_step(q35_model* m, int32_t token, float* logits_host, int32_t* argmax) {
-    if (!m) return q35::fail(Q35_ERR_ARG, "null model");
+    const q35_status nc = need_context(m);
+    if (nc != Q35_OK) return nc;
     if (token < 0 || token >= m->embed_rows || token >= m->d.vocab_size)
         return q35::fail(Q35_ERR_RANGE, "token %d outside [0, %d)", token, m->d.vocab_size);
     if (m->pos >= m->max_ctx)
@@ -1309,6 +1378,8 @@ namespace {
 // the argmax the previous step left in token_dev. ids_dev[p] receives the argmax after
 // the step at position p.
 q35_status run_greedy(q35_model* m, int32_t token, int32_t n_steps) {
+    const q35_status nc = need_context(m);
+    if (nc != Q35_OK) return nc;
     if (token < 0 || token >= m->d.vocab_size)
         return q35::fail(Q35_ERR_RANGE, "token %d outside [0, %d)", token, m->d.vocab_size);
     if (m->pos + n_steps > m->max_ctx)
@@ -1351,6 +1422,7 @@ q35_status q35_model_generate_greedy(q35_model* m, const int32_t* prompt, int32_
                                      int32_t n_new, int32_t* out) {
     if (!m || (n_prompt > 0 && !prompt) || n_prompt < 0 || n_new < 0 || (n_new > 0 && !out))
         return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     if (n_prompt + static_cast<int64_t>(n_new) > m->max_ctx)
         return q35::fail(Q35_ERR_RANGE, "prompt + new tokens (%d + %d) exceed max_context %lld", n_prompt, n_new,
                          (long long)m->max_ctx);
@@ -1395,6 +1467,7 @@ q35_status q35_model_set_layer_trace(q35_model* m, int32_t enable) {
 
 q35_status q35_model_read_layer_trace(q35_model* m, float* host) {
     if (!m || !host) return q35::fail(Q35_ERR_ARG, "null argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     HIPCHK(hipMemcpyAsync(host, m->trace, static_cast<size_t>(m->d.n_layers_total) * m->d.hidden_size * 4,
                           hipMemcpyDeviceToHost, m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
@@ -1403,6 +1476,7 @@ q35_status q35_model_read_layer_trace(q35_model* m, float* host) {
 
 q35_status q35_model_read_hidden(q35_model* m, float* host) {
     if (!m || !host) return q35::fail(Q35_ERR_ARG, "null argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     HIPCHK(hipMemcpyAsync(host, m->hidden, static_cast<size_t>(m->d.hidden_size) * 4, hipMemcpyDeviceToHost,
                           m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
@@ -1473,6 +1547,7 @@ q35_status q35_model_read_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t 
                              float* v_host) {
     if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
         return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim, E = m->kv_elem;
     std::vector<uint16_t> tmp(m->kv_elem == 2 ? static_cast<size_t>(n) * NKV * HD : 0);
     for (int which = 0; which < 2; ++which) {
@@ -1498,6 +1573,7 @@ q35_status q35_model_write_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t
                               const float* v_host) {
     if (!m || layer < 0 || layer >= m->d.n_layers_attn || pos0 < 0 || n < 0 || pos0 + n > m->max_ctx)
         return q35::fail(Q35_ERR_ARG, "bad argument");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim, E = m->kv_elem;
     std::vector<uint16_t> tmp(m->kv_elem == 2 ? static_cast<size_t>(n) * NKV * HD : 0);
     for (int which = 0; which < 2; ++which) {
@@ -1520,6 +1596,7 @@ q35_status q35_model_write_kv(q35_model* m, int32_t layer, int64_t pos0, int64_t
 
 q35_status q35_model_set_position(q35_model* m, int64_t pos) {
     if (!m || pos < 0 || pos > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "bad position");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     HIPCHK(q35k::launch_set_int(m->pos_dev, static_cast<int>(pos), m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
     m->pos = pos;
@@ -1528,6 +1605,7 @@ q35_status q35_model_set_position(q35_model* m, int64_t pos) {
 
 q35_status q35_model_fill_synthetic(q35_model* m, int64_t pos, uint64_t seed, float state_std) {
     if (!m || pos < 0 || pos > m->max_ctx) return q35::fail(Q35_ERR_RANGE, "bad position");
+    if (need_context(m) != Q35_OK) return Q35_ERR_RANGE;
     const int NKV = m->d.attn_kv_heads, HD = m->d.attn_head_dim;
     for (int l = 0; l < m->d.n_layers_attn; ++l)
         for (int which = 0; which < 2; ++which)
@@ -1588,12 +1666,13 @@ q35_status q35_model_reserve_context(q35_model* m, int64_t max_context) {
     if (max_context <= m->max_ctx) return Q35_OK;
     HIPCHK(hipStreamSynchronize(m->stream));
     drop_graph(m);
-    q35_status st = alloc_context(m, max_context);
-    if (st != Q35_OK) return st;
-    // the recurrent state goes back to zero with the cache: the model is reset
+    const q35_status st = alloc_context(m, max_context);
+    if (!m->scratch) return st;  // no context arenas: every call that needs them refuses
+    // the recurrent state goes back to zero with the cache (also when a failed reservation
+    // made the old arenas again): the model is reset
     HIPCHK(q35k::launch_fill_f32(m->state_arena, static_cast<int64_t>(m->state_bytes / 4), 0.0f, m->stream));
     HIPCHK(hipStreamSynchronize(m->stream));
-    return Q35_OK;
+    return st;
 }
 
 }  // extern "C"

@@ -29,10 +29,14 @@ bool QwenForward::prefill(const std::vector<int>& ids, std::vector<float>& logit
             return false;
         }
     }
-    if (seq > q35_model_max_context(m_) &&
-        q35_model_reserve_context(m_, std::max<int64_t>(seq, 2 * q35_model_max_context(m_))) != Q35_OK) {
-        std::cerr << "[qwen] prefill: " << q35_last_error() << "\n";
-        return false;
+    if (seq > q35_model_max_context(m_)) {
+        // room for prompts up to twice as long first; if that does not fit, exactly this one
+        const int64_t want = std::max<int64_t>(seq, 2 * q35_model_max_context(m_));
+        if (q35_model_reserve_context(m_, want) != Q35_OK &&
+            (want == seq || q35_model_reserve_context(m_, seq) != Q35_OK)) {
+            std::cerr << "[qwen] prefill: " << q35_last_error() << "\n";
+            return false;
+        }
     }
     logits_out.assign(static_cast<size_t>(seq) * static_cast<size_t>(q35_model_prefill_logits_width(m_)), 0.0f);
     std::vector<int32_t> v(ids.begin(), ids.end());

@@ -235,6 +235,14 @@ bool SafeTensors::parse_shard(const std::string& path) {
             e.abs_offset = data0 + static_cast<size_t>(span[0]);
             e.nbytes = static_cast<size_t>(span[1] - span[0]);
             const size_t es = dtype_size(e.dtype);
+            // the element count in checked arithmetic: a shape whose product (or its byte size)
+            // wraps around could otherwise equal the span and pass the check below
+            int64_t count = 1, bytes = 0;
+            bool wraps = false;
+            for (const int64_t d : e.shape) wraps = wraps || __builtin_mul_overflow(count, d, &count);
+            wraps = wraps || __builtin_mul_overflow(count, static_cast<int64_t>(es), &bytes);
+            if (wraps)
+                return complain(path, "tensor '" + name + "' has a shape whose size overflows 64 bits");
             if (es && static_cast<size_t>(e.numel()) * es != e.nbytes && !e.shape.empty())
                 return complain(path, "tensor '" + name + "' holds " + std::to_string(e.nbytes) + " bytes, not " +
                                           std::to_string(e.numel()) + " x " + std::to_string(es));

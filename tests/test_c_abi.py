@@ -2,6 +2,7 @@
 host-only parts (config reader, memory equation, synthetic writer, argument checks and
 error reporting) behave like the reference's. No GPU work is started here."""
 import ctypes as C
+import json
 import os
 import re
 import shutil
@@ -215,6 +216,12 @@ def test_model_open_reports_bad_files(tmp_path, model_dirs):
     # header length beyond the file
     p.write_bytes((10**12).to_bytes(8, "little") + data[8:64])
     assert pyq35.lib.q35_model_open(str(bad).encode(), 64, C.byref(h)) == -3
+    # a shape whose element count wraps around 64 bits to the span's size:
+    # (2^62 + 1) x 4 = 2^64 + 4 -> 4 elements of 2 bytes = the 8-byte span
+    hdr = json.dumps({"w": {"dtype": "BF16", "shape": [2**62 + 1, 4], "data_offsets": [0, 8]}}).encode()
+    p.write_bytes(len(hdr).to_bytes(8, "little") + hdr + bytes(8))
+    assert pyq35.lib.q35_model_open(str(bad).encode(), 64, C.byref(h)) == -3
+    assert not h.value
 
 
 def test_kernel_entry_points_validate_before_launch():
@@ -254,6 +261,23 @@ def test_kernel_entry_points_validate_before_launch():
     assert b"aligned" in pyq35.lib.q35_last_error()
     assert pyq35.lib.q35_matmul_bf16(None, None, None, 4, 8, None) == -1
     assert pyq35.lib.q35_matmul_bf16(1 << 20, 1 << 20, 1 << 20, 4, 12, None) == -7
+    # GDN prefill: the conv pass reads qkv rows, the ring and the taps 16 bytes at a time
+    gfake = {k: 1 << 20 for k in ("qkv", "z", "b", "a", "conv_w", "A_log", "dt_bias", "norm_w",
+                                  "conv_ring", "state", "out", "workspace")}
+    gp = pyq35.GdnPrefillArgs(n_tokens=8, k_heads=2, v_heads=2, head_dim_k=128, head_dim_v=128, conv_kernel=4,
+                              ld_qkv=768, ld_z=256, ld_ba=2, **gfake)
+    gp.workspace_bytes = pyq35.lib.q35_gdn_prefill_workspace_bytes(C.byref(gp))
+    assert gp.workspace_bytes > 0
+    for field, bad_value in (("ld_qkv", 770), ("qkv", (1 << 20) + 4), ("conv_ring", (1 << 20) + 8),
+                             ("conv_w", (1 << 20) + 12), ("workspace", (1 << 20) + 4)):
+        good = getattr(gp, field)
+        setattr(gp, field, bad_value)
+        assert pyq35.lib.q35_gdn_prefill(C.byref(gp), None) == -1, field
+        assert b"16-byte aligned" in pyq35.lib.q35_last_error()
+        setattr(gp, field, good)
+    gp.workspace_bytes -= 4
+    assert pyq35.lib.q35_gdn_prefill(C.byref(gp), None) == -1
+    assert b"workspace of" in pyq35.lib.q35_last_error()
 
 
 def test_attn_decode_static_refuses_oversized_partials():

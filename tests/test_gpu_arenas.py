@@ -94,6 +94,47 @@ def test_reserve_context_keeps_the_weights(model_dirs):
     assert rows_close(lg, ref) < REL_L2
 
 
+def test_failed_reserve_context_leaves_a_usable_model(model_dirs):
+    """A context too large for the device (2^30 positions: terabytes of KV) is refused with
+    the HIP status; the model keeps arenas of its old size (made again, zeroed, position 0)
+    and decodes exactly as a fresh model of that size."""
+    g = golden("tiny")
+    ids = np.asarray(g["long_ids"][:40], np.int32)
+    m = pyq35.Model(model_dirs["tiny"], 64)
+    m.prefill(ids, want_logits=False)
+    with pytest.raises(pyq35.Q35Error) as e:
+        m.reserve_context(2**30)
+    assert e.value.status == -2
+    assert m.max_context == 64 and m.position == 0
+    assert m.budget()["kv_cache_bytes"] == 1 * 64 * 2 * 1 * 256 * 4
+    lg = m.prefill(ids)
+    got = m.decode_greedy(int(np.argmax(lg[-1])), 8)
+    m.close()
+    fresh = pyq35.Model(model_dirs["tiny"], 64)
+    ref = fresh.prefill(ids)
+    np.testing.assert_array_equal(fresh.decode_greedy(int(np.argmax(ref[-1])), 8), got)
+    fresh.close()
+    assert rows_close(lg, ref) < REL_L2
+
+
+def test_planned_block_beyond_max_context_then_reserve(model_dirs):
+    """A block planned beyond max_context gets an arena for max_context tokens; after the
+    context grows, prompts run in blocks of that size (no refusal, no new arena)."""
+    g = golden("tiny")
+    ids = np.asarray(g["long_ids"][:200], np.int32)
+    m = pyq35.Model(model_dirs["tiny"], 48, prefill_block=256)
+    m.reserve_context(256)
+    n0 = allocs()
+    out = m.prefill(ids)
+    assert allocs() == n0
+    m.close()
+    lazy = pyq35.Model(model_dirs["tiny"], 256)
+    lazy.set_prefill_block(48)
+    ref = lazy.prefill(ids)
+    lazy.close()
+    assert rows_close(out, ref) < REL_L2
+
+
 def test_max_context_planned_by_the_memory_equation(tmp_path):
     """max_context 0: the KV capacity comes from solve_max_context against the device's
     memory, capped at the native context (here 131072, the long-decode workload's cap: the
