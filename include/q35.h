@@ -274,6 +274,20 @@ q35_status q35_matmul_f32(const float *W, const float *x, float *y, int32_t out_
 q35_status q35_gemm_bf16(const float *X, int64_t ldx, const uint16_t *W, int32_t M, int32_t N,
                          int32_t K, const float *R, int64_t ldr, float *Y, int64_t ldy,
                          q35_stream s);
+/* The same product on the model prefill's two-part fp16 path, from plain row-major inputs
+ * (replaces forward_pass.cpp:65-75 for M rows at once, as q35_gemm_bf16): W is copied to fp16
+ * scaled by 2^e so that its largest |w| lies in [2^14, 2^15) (exact for every bf16 weight
+ * down to 2^-24 of the largest); each row of X is scaled by a power of two from its maximum
+ * into (-2^15, 2^15) and split into h = fp16(x), l = fp16(x - h), |x - h - l| <= 2^-22 |x|
+ * (about 22 significant bits of x); each fp16 x fp16 product is exact, accumulation is fp32
+ * and both scales are undone exactly. Requires K % 32 == 0, a 16-byte aligned W and a
+ * 256-byte aligned workspace of q35_gemm_f16x2_workspace_bytes(M, N, K) bytes (fp16 copy of
+ * W, X in the GEMM's tiled layout, the maxima). Synchronizes the stream once (the weights'
+ * maximum is read back to choose their scale). */
+uint64_t q35_gemm_f16x2_workspace_bytes(int32_t M, int32_t N, int32_t K);
+q35_status q35_gemm_f16x2(const float *X, int64_t ldx, const uint16_t *W, int32_t M, int32_t N,
+                          int32_t K, const float *R, int64_t ldr, float *Y, int64_t ldy,
+                          void *workspace, uint64_t workspace_bytes, q35_stream s);
 /* Row-wise y = x * rsqrt(mean(x^2) + eps) * (1 + w) over rows of n (forward_pass.cpp:77-84). */
 q35_status q35_rmsnorm(const float *x, const float *w, float *y, int32_t rows, int32_t n,
                        float eps, q35_stream s);

@@ -3,6 +3,9 @@
 // that no kernel is launched with an extent it does not support.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
+#include <cstring>
 #include <mutex>
 
 #include "../host/q35_internal.h"
@@ -147,6 +150,72 @@ q35_status q35_gemm_bf16(const float* X, int64_t ldx, const uint16_t* W, int32_t
         return q35::fail(Q35_ERR_UNSUPPORTED, "q35_gemm_bf16: needs K %% 8 == 0, ldx %% 4 == 0, 16-byte aligned X/W");
     q35k::GemmArgs a{X, W, R, Y, M, N, K, ldx, R ? ldr : 0, ldy};
     return launched(q35k::launch_gemm(a, as_stream(s)), "q35_gemm_bf16");
+}
+
+namespace {
+// workspace of q35_gemm_f16x2 (byte offsets, 256-B aligned): weight maximum, row maxima,
+// the fp16 weight copy, the tiled activations
+struct F16x2Plan {
+    uint64_t xmax, wh, xt, bytes;
+};
+F16x2Plan f16x2_plan(int64_t M, int64_t N, int64_t K) {
+    auto al = [](uint64_t x) { return (x + 255) / 256 * 256; };
+    F16x2Plan p{};
+    p.xmax = 256;
+    p.wh = p.xmax + al(static_cast<uint64_t>(M) * 4);
+    p.xt = p.wh + al(static_cast<uint64_t>(N) * K * 2);
+    p.bytes = p.xt + al(static_cast<uint64_t>(q35k::rows_tiled(M)) * K * 4);
+    return p;
+}
+}  // namespace
+
+uint64_t q35_gemm_f16x2_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return f16x2_plan(M, N, K).bytes;
+}
+
+q35_status q35_gemm_f16x2(const float* X, int64_t ldx, const uint16_t* W, int32_t M, int32_t N, int32_t K,
+                          const float* R, int64_t ldr, float* Y, int64_t ldy, void* workspace, uint64_t workspace_bytes,
+                          q35_stream s) {
+    if (!X || !W || !Y || !workspace || M <= 0 || N <= 0 || K <= 0 || ldx < K || ldy < N || (R && ldr < N))
+        return q35::fail(Q35_ERR_ARG, "q35_gemm_f16x2: bad argument");
+    if (K % 32 != 0 || (reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(workspace) & 255))
+        return q35::fail(Q35_ERR_UNSUPPORTED, "q35_gemm_f16x2: needs K %% 32 == 0, 16-byte aligned W, 256-byte aligned workspace");
+    const F16x2Plan p = f16x2_plan(M, N, K);
+    if (workspace_bytes < p.bytes)
+        return q35::fail(Q35_ERR_ARG, "q35_gemm_f16x2: workspace of %llu bytes, needs %llu",
+                         static_cast<unsigned long long>(workspace_bytes), static_cast<unsigned long long>(p.bytes));
+    const hipStream_t st = as_stream(s);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    unsigned* wmax = reinterpret_cast<unsigned*>(ws);
+    float* xmax = reinterpret_cast<float*>(ws + p.xmax);
+    uint16_t* wh = reinterpret_cast<uint16_t*>(ws + p.wh);
+    float* xt = reinterpret_cast<float*>(ws + p.xt);
+    const int64_t nw = static_cast<int64_t>(N) * K;
+    // the weights' scale: 2^e with e = 15 - (exponent of max |w| as in frexp), as the model's
+    // prefill makes its fp16 copies
+    unsigned mx = 0;
+    q35_status r = launched(q35k::launch_fill_f32(reinterpret_cast<float*>(wmax), 1, 0.0f, st), "q35_gemm_f16x2");
+    if (r == Q35_OK) r = launched(q35k::launch_bf16_absmax(W, nw, wmax, st), "q35_gemm_f16x2");
+    if (r == Q35_OK) r = launched(hipMemcpyAsync(&mx, wmax, 4, hipMemcpyDeviceToHost, st), "q35_gemm_f16x2");
+    if (r == Q35_OK) r = launched(hipStreamSynchronize(st), "q35_gemm_f16x2");
+    if (r != Q35_OK) return r;
+    const uint32_t bits = mx << 16;
+    float wm = 0.0f;
+    std::memcpy(&wm, &bits, 4);
+    int ex = 0;
+    (void)std::frexp(wm, &ex);
+    const int we = wm > 0.0f && std::isfinite(wm) ? std::min(std::max(15 - ex, -100), 100) : 0;
+    r = launched(q35k::launch_bf16_to_f16(W, wh, nw, we, st), "q35_gemm_f16x2");
+    if (r == Q35_OK) r = launched(q35k::launch_rows_to_tiled(X, ldx, M, K, xt, xmax, st), "q35_gemm_f16x2");
+    if (r != Q35_OK) return r;
+    q35k::GemmArgs g{xt, W, R, Y, M, N, K, K, R ? ldr : 0, ldy};
+    g.Wh = wh;
+    g.w_exp = we;
+    g.xmax = xmax;
+    g.xmax_n = 1;
+    g.x_tiled = 1;
+    return launched(q35k::launch_gemm(g, st), "q35_gemm_f16x2");
 }
 
 q35_status q35_rmsnorm(const float* x, const float* w, float* y, int32_t rows, int32_t n, float eps,

@@ -320,7 +320,30 @@ __global__ __launch_bounds__(256) void bf16_to_f16_kernel(const uint16_t* w, uin
         }
     }
 }
+
+// Row-major X [M][ldx] -> the tiled layout of the two-part GEMM (rows padded to a multiple
+// of 128 with zeros), and each row's max |x|. One workgroup per (padded) row.
+__global__ __launch_bounds__(256) void rows_to_tiled_kernel(const float* X, int64_t ldx, int M, int K, float* Xt,
+                                                            float* xmax) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    float m = 0.0f;
+    for (int k = tid; k < K; k += 256) {
+        const float v = row < M ? X[static_cast<int64_t>(row) * ldx + k] : 0.0f;
+        Xt[xt_off(row, k, K)] = v;
+        m = fmaxf(m, fabsf(v));
+    }
+    __shared__ float red[4];
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0 && row < M) xmax[row] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
 }  // namespace
+
+hipError_t launch_rows_to_tiled(const float* X, int64_t ldx, int M, int K, float* Xt, float* xmax, hipStream_t s) {
+    klaunch(rows_to_tiled_kernel, static_cast<int>(rows_tiled(M)), 256, 0, s, X, ldx, M, K, Xt, xmax);
+    return hipGetLastError();
+}
 
 hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s) {
     // at most 1024 workgroups: each ends with one atomic on the same word

@@ -109,6 +109,8 @@ inline int gemm_col_tiles(int N) { return (N + 127) / 128; }
 // non-negative maximum); and wh = fp16(w x 2^e), round to nearest even
 hipError_t launch_bf16_absmax(const uint16_t* w, int64_t n, unsigned* out, hipStream_t s);
 hipError_t launch_bf16_to_f16(const uint16_t* w, uint16_t* wh, int64_t n, int e, hipStream_t s);
+// row-major X -> tiled Xt (rows_tiled(M) rows, zero padding) and xmax[r] = max |X[r][:]|
+hipError_t launch_rows_to_tiled(const float* X, int64_t ldx, int M, int K, float* Xt, float* xmax, hipStream_t s);
 
 // ---------------------------------------------------------------- GDN decode
 struct GdnDecodeArgs {

@@ -164,6 +164,8 @@ def _load():
         "q35_attn_decode": (S, [C.POINTER(AttnDecodeArgs), P]),
         "q35_attn_decode_static": (S, [C.POINTER(AttnDecodeArgs), P]),
         "q35_gemm_bf16": (S, [P, I64, P, I32, I32, I32, P, I64, P, I64, P]),
+        "q35_gemm_f16x2_workspace_bytes": (U64, [I32, I32, I32]),
+        "q35_gemm_f16x2": (S, [P, I64, P, I32, I32, I32, P, I64, P, I64, P, U64, P]),
         "q35_gdn_prefill_workspace_bytes": (U64, [C.POINTER(GdnPrefillArgs)]),
         "q35_gdn_prefill": (S, [C.POINTER(GdnPrefillArgs), P]),
         "q35_attn_prefill_workspace_bytes": (U64, [C.POINTER(AttnPrefillArgs)]),

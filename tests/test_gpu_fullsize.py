@@ -77,50 +77,90 @@ def inject_state(m, o, d, P, kv_bf16, seed):
 def test_decode_2b_after_8k_positions_through_graph(m2b4, kv):
     path, d = m2b4
     bf16 = kv == "bf16"
-    tol = REL_L2 if not bf16 else 2e-4
     max_ctx = P_8K + 16
     m = pyq35.Model(path, max_ctx, kv_bytes_per_elem=2 if bf16 else 4)
     o = op.Oracle(path, max_ctx, kv_bf16=bf16)
     try:
-        inject_state(m, o, d, P_8K, bf16, seed=11)
-        ids = pyq35.synth_token_ids(5, d.vocab_size, 6)
-        worst = 0.0
-        # graph-replayed steps (layer trace and timing off): logits, argmax, residual
-        for t in ids:
-            lg, am = m.step(int(t))
-            ref = o.step(int(t))
-            e = rel_l2(lg, ref)
-            worst = max(worst, e)
-            assert e < tol, f"logits at position {o.position - 1}: {e}"
-            assert am == int(np.argmax(ref))
-            assert rel_l2(m.hidden(), o.hidden()) < tol
-        # greedy decoding with no host round trip between the steps
-        first = int(np.argmax(ref))
-        got = m.decode_greedy(first, 4)
-        want, tok = [], first
-        for _ in range(4):
-            tok = int(np.argmax(o.step(tok)))
-            want.append(tok)
-        np.testing.assert_array_equal(got, want)
-        # one more step with the per-layer trace (eager launches) against the oracle's trace
-        rtr = o.enable_trace(rows=1)
-        m.set_layer_trace(True)
-        lg, _ = m.step(int(want[-1]))
-        ref = o.step(int(want[-1]))
-        tr = m.layer_trace()
-        errs = rel_rows(tr, rtr[0])
-        print(f"{kv}: worst logits rel_l2 {worst:.3g}, per-layer {errs.max():.3g}")
-        assert errs.max() < tol
-        assert rel_l2(lg, ref) < tol
-        # the cache rows the steps appended
-        n_new = len(ids) + 4 + 1
-        for l in range(d.n_layers_total // d.attn_interval):
-            K, V = m.kv(l, P_8K, n_new)
-            assert rel_l2(K, o.kcache(l)[P_8K:P_8K + n_new]) < tol
-            assert rel_l2(V, o.vcache(l)[P_8K:P_8K + n_new]) < tol
+        decode_parity(m, o, d, P_8K, kv)
     finally:
         m.close()
         o.close()
+
+
+@pytest.fixture(scope="module")
+def m2b4_131k(tmp_path_factory):
+    """The 4-layer 2B-shaped model with a native context of 131072 (the long-decode cap)."""
+    d = pyq35.dims_for("2b")
+    d.n_layers_total = 4
+    d.vocab_size = 4096
+    d.native_max_context = 131072
+    path = str(tmp_path_factory.mktemp("m2b4_131k") / "model")
+    pyq35.synth_write_model(path, d, seed=4, std=0.02)
+    return path, d
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("kv", ["fp32", "bf16"])
+def test_decode_2b_at_131k_context_planned_by_memory_equation(m2b4_131k, kv):
+    """The long-context decode as the long-decode workload runs it: max_context 0, so the KV
+    arena is planned by solve_max_context (src/memory_budget.cpp:56-81) and capped at 131072;
+    the default split count for that arena, the RoPE table rows past 131000 (angles in double,
+    src/forward_pass.cpp:102-112), the captured step graph and the greedy run, against the
+    oracle holding the same state with 131060 cached positions (src/qwen_model.cpp:106-152)."""
+    path, d = m2b4_131k
+    bf16 = kv == "bf16"
+    m = pyq35.Model(path, 0, kv_bytes_per_elem=2 if bf16 else 4)
+    assert m.max_context == 131072
+    o = op.Oracle(path, 131072, kv_bf16=bf16)
+    try:
+        decode_parity(m, o, d, 131060, kv)
+    finally:
+        m.close()
+        o.close()
+
+
+def decode_parity(m, o, d, P, kv):
+    """Inject the same state with P cached positions into the device model and the oracle,
+    then compare graph-replayed steps, a greedy run, one layer-traced step and the appended
+    cache rows."""
+    bf16 = kv == "bf16"
+    tol = REL_L2 if not bf16 else 2e-4
+    inject_state(m, o, d, P, bf16, seed=11)
+    ids = pyq35.synth_token_ids(5, d.vocab_size, 6)
+    worst = 0.0
+    # graph-replayed steps (layer trace and timing off): logits, argmax, residual
+    for t in ids:
+        lg, am = m.step(int(t))
+        ref = o.step(int(t))
+        e = rel_l2(lg, ref)
+        worst = max(worst, e)
+        assert e < tol, f"logits at position {o.position - 1}: {e}"
+        assert am == int(np.argmax(ref))
+        assert rel_l2(m.hidden(), o.hidden()) < tol
+    # greedy decoding with no host round trip between the steps
+    first = int(np.argmax(ref))
+    got = m.decode_greedy(first, 4)
+    want, tok = [], first
+    for _ in range(4):
+        tok = int(np.argmax(o.step(tok)))
+        want.append(tok)
+    np.testing.assert_array_equal(got, want)
+    # one more step with the per-layer trace (eager launches) against the oracle's trace
+    rtr = o.enable_trace(rows=1)
+    m.set_layer_trace(True)
+    lg, _ = m.step(int(want[-1]))
+    ref = o.step(int(want[-1]))
+    tr = m.layer_trace()
+    errs = rel_rows(tr, rtr[0])
+    print(f"{kv} at {P} positions: worst logits rel_l2 {worst:.3g}, per-layer {errs.max():.3g}")
+    assert errs.max() < tol
+    assert rel_l2(lg, ref) < tol
+    # the cache rows the steps appended
+    n_new = len(ids) + 4 + 1
+    for l in range(d.n_layers_total // d.attn_interval):
+        K, V = m.kv(l, P, n_new)
+        assert rel_l2(K, o.kcache(l)[P:P + n_new]) < tol
+        assert rel_l2(V, o.vcache(l)[P:P + n_new]) < tol
 
 
 @pytest.mark.timeout(900)

@@ -91,6 +91,73 @@ def test_gemm_rejects_bad_shapes(hip):
     unsupported, bad_arg = -7, -1
     assert pyq35.lib.q35_gemm_bf16(256, 12, 256, 4, 4, 12, None, 4, 512, 4, None) == unsupported  # K % 8
     assert pyq35.lib.q35_gemm_bf16(None, 32, 256, 4, 4, 32, None, 4, 512, 4, None) == bad_arg
+    ws = pyq35.lib.q35_gemm_f16x2_workspace_bytes(4, 4, 32)
+    assert ws > 0 and pyq35.lib.q35_gemm_f16x2_workspace_bytes(4, 4, 0) == 0
+    assert pyq35.lib.q35_gemm_f16x2(256, 40, 256, 4, 4, 40, None, 4, 512, 4, 1 << 20, 1 << 20, None) == unsupported
+    assert pyq35.lib.q35_gemm_f16x2(256, 32, 256, 4, 4, 32, None, 4, 512, 4, (1 << 20) + 16, ws, None) == unsupported
+    assert pyq35.lib.q35_gemm_f16x2(256, 32, 256, 4, 4, 32, None, 4, 512, 4, 1 << 20, ws - 4, None) == bad_arg
+
+
+def _f16x2_inputs(M, N, K, seed):
+    """Activations with the rows the two-part split has to survive -- all zeros, one channel
+    10^4 times the rest, magnitudes near 1e-20 and 1e20 -- and bf16 weights whose
+    magnitudes spread log-uniformly down to 2^-30 of the largest."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    X[0] = 0.0
+    X[1] = 1e-4 * X[1]
+    X[1, K // 3] = 1.0
+    X[2] *= np.float32(1e-20)
+    X[3] *= np.float32(1e20)
+    X[4, : K // 2] = 0.0
+    w = 0.02 * rng.standard_normal((N, K)) * np.exp2(-rng.uniform(0, 30, (N, K)))
+    w[0, 0] = 0.08  # the largest
+    return X, bf16_bits(w.astype(np.float32))
+
+
+@pytest.mark.parametrize("N,K,resid", [(8224, 2048, False), (2048, 2048, True), (12288, 2048, False),
+                                       (2048, 6144, True), (9216, 2048, False), (2048, 4096, True)])
+def test_gemm_f16x2_vs_float64(hip, N, K, resid):
+    """The model prefill's projection GEMM (two fp16 parts per activation against the scaled
+    fp16 weight copy) at the 2B projection shapes against float64, elementwise within
+    2^-17 of sum |x||w| (the split's 2^-22 |x| plus fp32 accumulation over K, with headroom)
+    and within 1e-6 rel_l2 per ordinary row; zero rows give exact zeros; the three-part
+    bf16 path agrees to the same 1e-6."""
+    M = 203
+    X, W = _f16x2_inputs(M, N, K, N + K)
+    R = np.random.default_rng(K).standard_normal((M, N)).astype(np.float32) if resid else None
+    ws = pyq35.lib.q35_gemm_f16x2_workspace_bytes(M, N, K)
+    B = Bufs(hip)
+    try:
+        dX, dW, dws = B.up("X", X), B.up("W", W), B.alloc("ws", ws)
+        dY = B.up("Y", R) if resid else B.alloc("Y", M * N * 4)
+        pyq35.check(pyq35.lib.q35_gemm_f16x2(dX, K, dW, M, N, K, dY if resid else None, N, dY, N, dws, ws, None))
+        hip.sync()
+        Y = hip.download(dY, (M, N))
+        dY3 = B.up("Y3", R) if resid else B.alloc("Y3", M * N * 4)
+        pyq35.check(pyq35.lib.q35_gemm_bf16(dX, K, dW, M, N, K, dY3 if resid else None, N, dY3, N, None))
+        hip.sync()
+        Y3 = hip.download(dY3, (M, N))
+    finally:
+        B.free()
+    Wf = bf16_to_f32(W).astype(np.float64)
+    ref = X.astype(np.float64) @ Wf.T
+    scale = np.abs(X.astype(np.float64)) @ np.abs(Wf).T
+    if resid:
+        ref += R
+        scale += np.abs(R)
+    bound = 2.0**-17 * scale
+    worst = float(np.max(np.abs(Y - ref) / np.where(scale > 0, scale, 1.0)))
+    print(f"N={N} K={K}: worst |dy| / sum|x||w| = {worst:.3g} (2^{np.log2(max(worst, 1e-300)):.1f})")
+    assert np.all(np.abs(Y - ref) <= bound)
+    if not resid:
+        assert np.all(Y[0] == 0.0)
+    for r in range(M):
+        if np.abs(ref[r]).max() > 0:
+            assert rel_l2(Y[r], ref[r]) < 1e-6, r
+            assert rel_l2(Y[r], Y3[r]) < 1e-6, r
+    print(f"  rel_l2 vs float64: rows 1-3 {[f'{rel_l2(Y[r], ref[r]):.2g}' for r in (1, 2, 3)]}, "
+          f"all {rel_l2(Y, ref):.3g}; vs three-part {rel_l2(Y, Y3):.3g}")
 
 
 # ----------------------------------------------------------------------------- GDN
