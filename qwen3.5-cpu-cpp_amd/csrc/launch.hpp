@@ -147,10 +147,6 @@ struct AttnDecodeArgs {
     // its natural stride, the caches with stride ls_cache (0 = NKV * max_ctx * HD)
     int n_layers;
     int64_t ls_cache;
-    // how the partial kernel assigned the cache to the splits (set by the launches): 0, equal
-    // position ranges of ceil((pos + 1) / n_splits); 1, whole 16-position tiles of [0, pos)
-    // (attn_tile_splits), the appended position pos on the last active split
-    int split_mode;
 };
 // Advances the per-layer pointers of `a` to layer l (device side).
 __device__ __forceinline__ void attn_select_layer(AttnDecodeArgs& a, int l) {
