@@ -214,7 +214,10 @@ def bench_gdn(a) -> dict:
 def bench_attn(a) -> dict:
     """Isolated gated-attention decode at the 2B shape: 6 layers with their own fp32 KV
     caches (N(0,1)) at each context of --ctx-list, one new token per step across the 6 layers
-    (q/k norm + RoPE + append + split-K softmax + gate). --kv bf16: bf16 caches."""
+    (q/k norm + RoPE + append + split-K softmax + gate). --kv bf16: bf16 caches. With
+    --rotate R, up to R independent sets of the 6 caches are visited round-robin (as many as
+    keep the working set near 1 GiB), so that the caches are read from HBM rather than from
+    the 256 MB Infinity Cache."""
     import pyq35
 
     hip = pyq35.Hip()
@@ -231,14 +234,16 @@ def bench_attn(a) -> dict:
     for ctx in a.ctx_list:
         maxc = ctx + 2 * (a.warmup + a.steps) + 1
         n = NKV * maxc * HD  # one layer's K (or V) cache
-        K = cache(L * n, 0)
-        V = cache(L * n, 1)
+        set_bytes = 2 * L * n * E
+        R = max(1, min(a.rotate, -(-(1 << 30) // set_bytes)))
+        Ks = [cache(L * n, 2 * r) for r in range(R)]
+        Vs = [cache(L * n, 2 * r + 1) for r in range(R)]
         qg = hip.upload(pyq35.synth_normal(L * 2 * NQ * HD, 12, 0))
         kn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 1))
         vn = hip.upload(pyq35.synth_normal(L * NKV * HD, 12, 2))
         w = hip.upload(np.zeros(L * HD, np.float32))
         out = hip.malloc(L * NQ * HD * 4)
-        row = {"kv_working_set_MiB": 2 * L * n * E / 2**20}
+        row = {"kv_working_set_MiB": R * set_bytes / 2**20, "kv_sets": R}
         p = ctx
         for mode in ("batched", "per_layer"):
             args = pyq35.AttnDecodeArgs(q_heads=NQ, kv_heads=NKV, head_dim=HD, rotary_dim=64, pos=ctx,
@@ -250,6 +255,7 @@ def bench_attn(a) -> dict:
 
             def step(pos):
                 args.pos = pos
+                K, V = Ks[pos % R], Vs[pos % R]
                 if mode == "batched":
                     args.qg, args.k_new, args.v_new, args.q_norm, args.k_norm = qg, kn, vn, w, w
                     args.k_cache, args.v_cache = K, V
@@ -278,7 +284,7 @@ def bench_attn(a) -> dict:
                          "frac": nbytes / (per / 1e3) / 1e9 / HBM_PEAK_GBS}
             hip.free(wsp)
         res[str(ctx)] = row
-        for q in (K, V, qg, kn, vn, w, out):
+        for q in Ks + Vs + [qg, kn, vn, w, out]:
             hip.free(q)
     key = str(8192) if "8192" in res else list(res)[0]
     r = res[key]["batched"]
@@ -287,7 +293,8 @@ def bench_attn(a) -> dict:
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
             "data": "synthetic N(0,1) KV cache and inputs",
             "config": {"workload": "isolated attention decode", "context": int(key), "layers": L,
-                       "heads": f"{NQ}q/{NKV}kv x {HD}", "kv_cache": a.kv},
+                       "heads": f"{NQ}q/{NKV}kv x {HD}", "kv_cache": a.kv,
+                       "kv_sets": res[key]["kv_sets"], "kv_working_set_MiB": res[key]["kv_working_set_MiB"]},
             "roofline": {"bound": "hbm", "kernel": "attention decode (split-K + combine), 6 layers",
                          "achieved": r["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac"],
                          "traffic": None},
@@ -443,7 +450,8 @@ def main() -> None:
     ap.add_argument("--prompt", type=int, default=4096, help="prefill: prompt tokens")
     ap.add_argument("--prefill-block", type=int, default=0, help="prefill: tokens per block (0 = auto)")
     ap.add_argument("--cpu-prompt", type=int, default=32, help="prefill: prompt tokens of the CPU sample")
-    ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets, round-robin")
+    ap.add_argument("--rotate", type=int, default=1, help="gdn: independent state sets; attn: independent sets of the 6 KV caches "
+                         "(as many as fit about 1 GiB), visited round-robin")
     ap.add_argument("--ctx-list", type=lambda s: [int(x) for x in s.split(",")], default=[2048, 8192, 32768])
     ap.add_argument("--attn-splits", type=int, default=0,
                     help="attention split-K count (0 = the library default)")
