@@ -227,7 +227,17 @@ __global__ __launch_bounds__(64) void gdn_wave_kernel(GdnDecodeArgs a) {
     constexpr int CW = 32, RR = 16;
     const int lane = threadIdx.x;
     const int rg = lane >> 3, cq = lane & 7;
-    const int vh = blockIdx.x >> 2, split = blockIdx.x & 3;
+    // workgroups go to the 8 XCDs in turn: with VH a multiple of 8 the four slices of a head
+    // get ids of one residue mod 8, so one L2 fetches the head's q / k rows for all four
+    int vh, split;
+    if ((a.VH & 7) == 0) {
+        const int xcd = blockIdx.x & 7, rest = blockIdx.x >> 3;
+        split = rest & 3;
+        vh = xcd + 8 * (rest >> 2);
+    } else {
+        vh = blockIdx.x >> 2;
+        split = blockIdx.x & 3;
+    }
     const int layer = blockIdx.y;
     const int rep = a.VH / a.KH, kh = vh / rep;
     const int KD = a.KH * kD;
