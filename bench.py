@@ -328,7 +328,7 @@ def bench_prefill(a) -> dict:
     ensure_model(a.model_dir, d, pyq35)
     T = a.prompt
     ids = pyq35.synth_token_ids(2, d.vocab_size, T)
-    m = pyq35.Model(a.model_dir, T + 8)
+    m = pyq35.Model(a.model_dir, T + 8, prefill_exact=a.prefill_exact)
     if a.prefill_block:
         m.set_prefill_block(a.prefill_block)
     for _ in range(max(1, a.warmup)):
@@ -363,7 +363,9 @@ def bench_prefill(a) -> dict:
     # two-part activations, fp16 weight copies) on the 16-bit matrix cores, so its ceiling is
     # the dense fp16 peak over 2 in fp32-product terms; the flash attention as six bf16 part
     # products (peak / 6); the chunked GDN on the fp32 matrix cores.
-    peaks = {"gemm": FP16_MFMA_PEAK_TFS / 2, "attn_prefill": BF16_MFMA_PEAK_TFS / 6, "gdn_prefill": FP32_MFMA_PEAK_TFS}
+    # (--prefill-exact: three exact bf16 parts, bf16 peak / 3)
+    gemm_peak = BF16_MFMA_PEAK_TFS / 3 if a.prefill_exact else FP16_MFMA_PEAK_TFS / 2
+    peaks = {"gemm": gemm_peak, "attn_prefill": BF16_MFMA_PEAK_TFS / 6, "gdn_prefill": FP32_MFMA_PEAK_TFS}
     peak = peaks[dominant]
     mixer_flops = d.n_layers_attn * attn_flops + d.n_layers_gdn * gdn_flops
     mixer_ms = ms["attn_prefill"] + ms["gdn_prefill"]
@@ -374,11 +376,14 @@ def bench_prefill(a) -> dict:
         "dtype": "fp32", "data": "synthetic: random-init bf16 weights N(0,0.02) seed 0, ids uniform seed 2",
         "config": {"workload": f"2B-shaped Qwen3.5 prefill of {T} tokens", "hidden": d.hidden_size,
                    "layers": "24 = 18 GDN + 6 gated attention", "prompt": T,
-                   "block": a.prefill_block or min(4096, T + 8), "gdn_chunk": 64},
+                   "block": a.prefill_block or min(4096, T + 8), "gdn_chunk": 64,
+                   "gemm": ("three exact bf16 parts per fp32 activation" if a.prefill_exact else
+                            "two row-scaled fp16 parts per fp32 activation, fp16 weight copies")},
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": ach, "peak": peak,
                      "unit": "TFLOP/s", "frac": ach / peak, "traffic": None,
                      "note": "fp32 flops of the algorithm; GEMM peak = dense fp16 MFMA peak / 2 (two "
-                             "fp16 parts of each row-scaled fp32 activation against fp16 weight copies); "
+                             "fp16 parts of each row-scaled fp32 activation against fp16 weight copies; "
+                             "with --prefill-exact bf16 peak / 3, three exact bf16 parts); "
                              "flash attention = bf16 peak / 6 (six part products per fp32 product); GDN = "
                              "fp32 MFMA peak"},
         "mixers": {"attn_prefill_TFs": attn_tfs, "attn_prefill_frac": attn_tfs / peaks["attn_prefill"],
@@ -457,6 +462,8 @@ def main() -> None:
                     help="attention split-K count (0 = the library default)")
     ap.add_argument("--kv", choices=["fp32", "bf16"], default="fp32",
                     help="KV cache element type (decode, attn): fp32 is the reference's cache")
+    ap.add_argument("--prefill-exact", action="store_true",
+                    help="prefill: projection GEMMs on three exact bf16 parts (no fp16 weight copies)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()

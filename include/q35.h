@@ -148,11 +148,16 @@ q35_status q35_model_create(const q35_dims *d, const q35_tensor *tensors, int32_
  * cache (rows rounded to nearest even when appended; half the KV bytes and bandwidth).
  * prefill_block > 0 plans the prompt arena at creation, for prefill blocks of up to that
  * many tokens (a fifth hipMalloc, reported in q35_budget.prompt_arena_bytes; larger blocks
- * are refused); 0 leaves it to the first prefill. */
+ * are refused); 0 leaves it to the first prefill. prefill_exact = 1 runs the prefill's
+ * projection GEMMs on three exact bf16 parts of each fp32 activation (full fp32 precision;
+ * no fp16 weight copies, so the prompt arena is smaller by the projection weights' size in
+ * fp16, 2.7 GiB at the 2B shape); 0 (default) on two row-scaled fp16 parts (about 22
+ * significant bits of each activation) against fp16 copies of the weights, which is faster. */
 typedef struct q35_model_options {
     int32_t kv_bytes_per_elem;
     int32_t prefill_block;
-    int32_t reserved[6];
+    int32_t prefill_exact;
+    int32_t reserved[5];
 } q35_model_options;
 q35_status q35_model_create_opts(const q35_dims *d, const q35_tensor *tensors, int32_t n_tensors,
                                  int64_t max_context, const q35_model_options *opt, q35_model **out);

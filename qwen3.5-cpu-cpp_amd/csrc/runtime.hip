@@ -127,6 +127,7 @@ struct q35_model {
     size_t pf_bytes = 0;
     int pf_block = 0;    // requested block size (0 = automatic)
     int pf_planned = 0;  // block size planned at creation (0: none)
+    int pf_exact = 0;    // prefill GEMMs on three exact bf16 parts (no fp16 weight copies)
     int prefill_head = 0;  // prefill logits: 0 = the step's output head, 1 = the embedding
 
     bool use_graph = true;
@@ -735,11 +736,11 @@ int64_t proj_width(const q35_dims& d) {
                              2LL * d.attn_q_heads * d.attn_head_dim + 2LL * d.attn_kv_heads * d.attn_head_dim);
 }
 
-PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
+PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width, bool exact) {
     PrefillPlan p;
     p.tb = tb;
     p.lr = std::min(tb, 256);
-    p.tiled = d.hidden_size % 32 == 0 && d.ffn_intermediate % 32 == 0;
+    p.tiled = !exact && d.hidden_size % 32 == 0 && d.ffn_intermediate % 32 == 0;
     const int64_t H = d.hidden_size, I = d.ffn_intermediate, T = tb;
     const int64_t VD = d.gdn_v_heads * 128LL, QD = static_cast<int64_t>(d.attn_q_heads) * d.attn_head_dim;
     int64_t cur = 0;
@@ -764,13 +765,15 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
     p.mix_max = take(T * std::max(d.attn_q_heads, d.gdn_v_heads));
     p.hb_max = take(T * q35k::gemm_col_tiles(2 * d.ffn_intermediate));
     p.wmax = take(4LL * d.n_layers_total);
-    int64_t wh = 0;
-    for (int l = 0; l < d.n_layers_total; ++l) {
-        int64_t n[4];
-        layer_matrix_sizes(d, l, n);
-        for (const int64_t x : n) wh += (x + 127) / 128 * 128;  // 256-B aligned fp16 matrices
+    if (p.tiled) {  // the fp16 weight copies of the two-part path
+        int64_t wh = 0;
+        for (int l = 0; l < d.n_layers_total; ++l) {
+            int64_t n[4];
+            layer_matrix_sizes(d, l, n);
+            for (const int64_t x : n) wh += (x + 127) / 128 * 128;  // 256-B aligned fp16 matrices
+        }
+        p.wh = take(wh / 2);
     }
-    p.wh = take(wh / 2);
     p.total = cur;
     return p;
 }
@@ -778,7 +781,7 @@ PrefillPlan plan_prefill(const q35_dims& d, int tb, int64_t logits_width) {
 int64_t logits_width(const q35_model* m) { return std::max<int64_t>(m->d.vocab_size, m->embed_rows); }
 
 size_t prompt_arena_bytes(const q35_model* m, int64_t tb) {
-    return static_cast<size_t>(plan_prefill(m->d, static_cast<int>(tb), logits_width(m)).total) * 4;
+    return static_cast<size_t>(plan_prefill(m->d, static_cast<int>(tb), logits_width(m), m->pf_exact).total) * 4;
 }
 
 // The prefill's fp16 weight copies, in the prompt arena: per matrix its maximum |w| (one
@@ -831,7 +834,8 @@ q35_status make_prompt_arena(q35_model* m, int64_t tb) {
     m->pf_arena = static_cast<uint8_t*>(p);
     m->pf_bytes = bytes;
     m->budget.prompt_arena_bytes = bytes;
-    return make_prefill_weights(m, plan_prefill(m->d, static_cast<int>(tb), logits_width(m)));
+    const PrefillPlan plan = plan_prefill(m->d, static_cast<int>(tb), logits_width(m), m->pf_exact);
+    return plan.tiled ? make_prefill_weights(m, plan) : Q35_OK;
 }
 
 int prefill_block_tokens(const q35_model* m) {
@@ -843,7 +847,7 @@ int prefill_block_tokens(const q35_model* m) {
 // last prefill made when it is large enough, else a new one (lazy mode only).
 q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
     const int tb = prefill_block_tokens(m);
-    *plan = plan_prefill(m->d, tb, logits_width(m));
+    *plan = plan_prefill(m->d, tb, logits_width(m), m->pf_exact);
     if (m->pf_arena && static_cast<size_t>(plan->total) * 4 <= m->pf_bytes) return Q35_OK;
     if (m->pf_planned > 0)
         return q35::fail(Q35_ERR_RANGE, "a prefill block of %d tokens exceeds the prompt arena planned for %d", tb,
@@ -855,7 +859,7 @@ q35_status ensure_prefill_arena(q35_model* m, PrefillPlan* plan) {
 }
 
 q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int64_t max_ctx, int kv_elem,
-                        int prefill_block, q35_model** out) {
+                        int prefill_block, int prefill_exact, q35_model** out) {
     if (!dims || !ts || !out || nt <= 0) return q35::fail(Q35_ERR_ARG, "q35_model_create: null argument");
     *out = nullptr;
     if (max_ctx < 0 || max_ctx > (int64_t{1} << 30))
@@ -864,6 +868,8 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
         return q35::fail(Q35_ERR_RANGE, "prefill block %d out of range", prefill_block);
     if (kv_elem != 4 && kv_elem != 2)
         return q35::fail(Q35_ERR_UNSUPPORTED, "KV cache element of %d bytes (4 = fp32 or 2 = bf16)", kv_elem);
+    if (prefill_exact != 0 && prefill_exact != 1)
+        return q35::fail(Q35_ERR_ARG, "prefill_exact %d (0 or 1)", prefill_exact);
     q35_dims d = *dims;
     d.n_layers_attn = d.n_layers_total / d.attn_interval;
     d.n_layers_gdn = d.n_layers_total - d.n_layers_attn;
@@ -969,6 +975,7 @@ q35_status create_model(const q35_dims* dims, const q35_tensor* ts, int nt, int6
     m->w_bytes = plan.bytes();
     m->embed_rows = emb_rows;
     m->pf_planned = prefill_block;
+    m->pf_exact = prefill_exact;
     const size_t pf_bytes = prefill_block > 0 ? prompt_arena_bytes(m.get(), max_ctx > 0 ? std::min<int64_t>(prefill_block, max_ctx) : prefill_block) : 0;
 
     if (max_ctx == 0) {
@@ -1098,7 +1105,7 @@ hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const 
     const uint16_t* W[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
     q35k::GemmArgs g{X, W[i], R, Y, M, N, K, ldx, R ? ldy : 0, ldy};
     g.swiglu = ymax != nullptr;
-    g.Wh = ly.wh[i];
+    g.Wh = tiled ? ly.wh[i] : nullptr;  // row-major X: the three exact bf16 parts
     g.w_exp = ly.we[i];
     g.xmax = xmax;
     g.xmax_n = xmax_n;
@@ -1288,13 +1295,13 @@ int64_t q35_device_alloc_count(void) { return g_dev_allocs.load(); }
 
 q35_status q35_model_create(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
                             int64_t max_context, q35_model** out) {
-    return create_model(d, tensors, n_tensors, max_context, 4, 0, out);
+    return create_model(d, tensors, n_tensors, max_context, 4, 0, 0, out);
 }
 
 q35_status q35_model_create_opts(const q35_dims* d, const q35_tensor* tensors, int32_t n_tensors,
                                  int64_t max_context, const q35_model_options* opt, q35_model** out) {
     return create_model(d, tensors, n_tensors, max_context, opt ? opt->kv_bytes_per_elem : 4,
-                        opt ? opt->prefill_block : 0, out);
+                        opt ? opt->prefill_block : 0, opt ? opt->prefill_exact : 0, out);
 }
 
 q35_status q35_model_open(const char* model_dir, int64_t max_context, q35_model** out) {
@@ -1313,7 +1320,8 @@ q35_status q35_model_open_opts(const char* model_dir, int64_t max_context, const
     q35_dims d;
     q35::dims_from_config(cfg, &d);
     return create_model(&d, table.data(), static_cast<int32_t>(table.size()), max_context,
-                        opt ? opt->kv_bytes_per_elem : 4, opt ? opt->prefill_block : 0, out);
+                        opt ? opt->kv_bytes_per_elem : 4, opt ? opt->prefill_block : 0, opt ? opt->prefill_exact : 0,
+                        out);
 }
 
 void q35_model_destroy(q35_model* m) { destroy(m); }

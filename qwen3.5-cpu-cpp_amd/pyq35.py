@@ -75,7 +75,8 @@ class AttnDecodeArgs(C.Structure):
 
 
 class ModelOptions(C.Structure):
-    _fields_ = [("kv_bytes_per_elem", C.c_int32), ("prefill_block", C.c_int32), ("reserved", C.c_int32 * 6)]
+    _fields_ = [("kv_bytes_per_elem", C.c_int32), ("prefill_block", C.c_int32), ("prefill_exact", C.c_int32),
+                ("reserved", C.c_int32 * 5)]
 
 
 class GdnPrefillArgs(C.Structure):
@@ -228,11 +229,14 @@ def synth_normal(n: int, seed: int, stream: int, std: float = 1.0) -> np.ndarray
 class Model:
     """The device-resident decoder (QwenModel on the GPU)."""
 
-    def __init__(self, model_dir: str, max_context: int, kv_bytes_per_elem: int = 4, prefill_block: int = 0):
+    def __init__(self, model_dir: str, max_context: int, kv_bytes_per_elem: int = 4, prefill_block: int = 0,
+                 prefill_exact: bool = False):
         """max_context 0: planned by the memory equation against the device's memory;
-        prefill_block > 0: the prompt arena is planned at creation for blocks of that size."""
+        prefill_block > 0: the prompt arena is planned at creation for blocks of that size;
+        prefill_exact: the prefill GEMMs on three exact bf16 parts (no fp16 weight copies)."""
         h = C.c_void_p()
-        opt = ModelOptions(kv_bytes_per_elem=kv_bytes_per_elem, prefill_block=prefill_block)
+        opt = ModelOptions(kv_bytes_per_elem=kv_bytes_per_elem, prefill_block=prefill_block,
+                           prefill_exact=int(prefill_exact))
         check(lib.q35_model_open_opts(model_dir.encode(), max_context, C.byref(opt), C.byref(h)))
         self.h = h
         d = Dims()

@@ -389,18 +389,32 @@ def test_prefill_block_invariance(model_dirs):
     m.close()
 
 
-def test_prefill_2b_mixers_vs_oracle(tmp_path):
+@pytest.mark.parametrize("exact", [False, True])
+def test_prefill_2b_mixers_vs_oracle(tmp_path, exact):
     """2B mixer shapes (16 GDN heads, 16 q / 2 kv heads, H 2048) in a 4-layer model with a
     small vocabulary: 300 prompt tokens (ragged chunks, two blocks of 256) vs the oracle's
-    sequential prefill, per layer and for the logits."""
+    sequential prefill, per layer and for the logits; on the default two-part fp16 GEMMs
+    and with prefill_exact (three exact bf16 parts, no fp16 weight copies: a smaller prompt
+    arena)."""
     d = pyq35.dims_for("2b")
     d.n_layers_total = 4
     d.vocab_size = 4096
     path = str(tmp_path / "m2b4")
     pyq35.synth_write_model(path, d, seed=3, std=0.02)
     ids = pyq35.synth_token_ids(2, d.vocab_size, 300)
-    m = pyq35.Model(path, 512)
-    m.set_prefill_block(256)
+    m = pyq35.Model(path, 512, prefill_block=256, prefill_exact=exact)
+    arena = m.budget()["prompt_arena_bytes"]
+    # the fp16 copies of the four projection matrices of the 4 layers (3 GDN + 1 attention)
+    n16 = 0
+    for l in range(4):
+        attn = (l + 1) % 4 == 0
+        n_in = (2 * 16 * 256 + 2 * 2 * 256 if attn else 2 * 2048 + 2048 + 2048 + 32) * 2048
+        for n in (n_in, 2048 * (16 * 256 if attn else 2048), 2 * 6144 * 2048, 2048 * 6144):
+            n16 += (n + 127) // 128 * 128 * 2
+    if exact:
+        ref_m = pyq35.Model(path, 512, prefill_block=256)
+        assert ref_m.budget()["prompt_arena_bytes"] - arena >= n16
+        ref_m.close()
     lg, tr = m.extend(ids, want_logits=True, want_trace=True)
     m.close()
     o = op.Oracle(path, 512)
@@ -408,6 +422,6 @@ def test_prefill_2b_mixers_vs_oracle(tmp_path):
     ref = o.prefill(ids)
     o.close()
     worst = max(rel_l2(tr[t, l], rtr[t, l]) for t in range(len(ids)) for l in range(4))
-    print(f"2B-shaped: worst per-layer rel_l2 {worst:.3g}")
+    print(f"2B-shaped ({'exact' if exact else 'two-part'}): worst per-layer rel_l2 {worst:.3g}")
     assert worst < REL_L2
     assert max(rel_l2(lg[t], ref[t]) for t in range(len(ids))) < REL_L2
