@@ -86,6 +86,41 @@ def test_config_reader(tmp_path):
         assert th.value == d.rope_theta and eps.value == d.rms_norm_eps
 
 
+QUIRKY_CONFIGS = [
+    # flat file (no text_config), integers rounded as (int)(v + 0.5), exponents
+    '{"hidden_size": 2047.6, "num_hidden_layers": 8.4, "vocab_size": 1e3, "rms_norm_eps": 1E-5}',
+    # "true" after the flag's comma does not count; the first occurrence of a key wins,
+    # nested objects included; a key quoted as a string value is still the key's first match
+    '{"text_config": {"tie_word_embeddings": false, "x": true, "rope_parameters": {"rope_theta": 25e4},'
+    ' "rope_theta": 1, "model_type": "head_dim", "head_dim": 128}}',
+    # out-of-range and malformed numbers keep the defaults; blanks before the value
+    '{"text_config": {"hidden_size": 1e999, "intermediate_size": -, "vocab_size":\n\t 512,'
+    ' "partial_rotary_factor": 5e-400, "tie_word_embeddings": true}}',
+    # an unterminated text_config object: the whole file is the scope
+    '{"hidden_size": 64, "text_config": {"hidden_size": 32',
+]
+
+
+@pytest.mark.skipif(not op.ref_available(), reason="reference build absent")
+@pytest.mark.parametrize("text", QUIRKY_CONFIGS)
+def test_config_reader_quirks_match_reference(tmp_path, text):
+    """The reader's textual lookup rules on unusual files, side by side with the compiled
+    reference loader (src/config_loader.cpp:13-108)."""
+    cfg = tmp_path / "config.json"
+    cfg.write_text(text)
+    d = pyq35.load_config(str(cfg))
+    v = np.zeros(16, np.int64)
+    th, eps, pf = C.c_double(), C.c_float(), C.c_float()
+    op.Ref.lib().ref_config(str(cfg).encode(), v.ctypes.data, C.byref(th), C.byref(eps), C.byref(pf))
+    mine = [d.hidden_size, d.n_layers_total, d.n_layers_gdn, d.n_layers_attn, d.gdn_k_heads,
+            d.gdn_v_heads, d.gdn_k_head_dim, d.gdn_v_head_dim, d.gdn_conv_kernel, d.attn_q_heads,
+            d.attn_kv_heads, d.attn_head_dim, d.ffn_intermediate, d.vocab_size,
+            d.native_max_context, d.n_params]
+    assert v.tolist() == mine
+    assert th.value == d.rope_theta and eps.value == pytest.approx(d.rms_norm_eps, rel=1e-7)
+    assert pf.value == pytest.approx(d.partial_rotary_factor, rel=1e-7)
+
+
 def _budget(d, bpw, ctx, kvb):
     b = pyq35.Budget()
     pyq35.check(pyq35.lib.q35_compute_budget(C.byref(d), bpw, ctx, kvb, 4, 1024, C.byref(b)))
