@@ -3,20 +3,22 @@
 // at position pos0 and continues from the model's state (so prefill and decode hand over).
 //
 // Gated DeltaNet, chunked (chunk C = 64, the WY form of the gated delta rule):
-//   prep     conv window + SiLU per channel (inputs before the block come from the conv
-//            ring), l2norm of q and k per head, q scaled by DK^-1/2, beta = sigmoid(b),
-//            g = -exp(A_log) softplus(a + dt_bias); head-major outputs padded to whole chunks
-//            (padding rows have q = k = v = 0, beta = g = 0 and change nothing).
-//   ring     the last three raw inputs of the block go to their ring slots.
-//   chunk    per (v-head, chunk): gamma = cumsum(g) in double (every decay factor below is
-//            e^(a difference of gammas) rounded once: an fp32 running sum would lose ~1e-6 of
-//            each exponent to cancellation, gamma reaching -40 within a chunk); the chunk's
-//            e^gamma and e^(gamma_last - gamma) go to the workspace for the later passes;
-//            Q K^T and K K^T on the fp32 matrix cores;
+//   chunk    per (v-head, chunk), from the raw projection rows: conv window + SiLU per
+//            channel (the three inputs before the block come from the conv ring), l2norm of
+//            q and k per token, q scaled by DK^-1/2, beta = sigmoid(b),
+//            g = -exp(A_log) softplus(a + dt_bias); rows past the block (padding to whole
+//            chunks) have q = k = v = 0, beta = g = 0 and change nothing. q goes head-major to
+//            the workspace for the output pass. gamma = cumsum(g) in double (every decay factor
+//            below is e^(a difference of gammas) rounded once: an fp32 running sum would lose
+//            ~1e-6 of each exponent to cancellation, gamma reaching -40 within a chunk); the
+//            chunk's e^gamma and e^(gamma_last - gamma) go to the workspace for the later passes;
+//            Q K^T and K K^T on the fp32 matrix cores (the 10 lower-triangle 16 x 16 blocks);
 //              P[i][j] = q_i.k_j e^(gamma_i - gamma_j)      (j <= i)
 //              A[i][j] = beta_i k_i.k_j e^(gamma_i - gamma_j)  (j < i)
 //              [U | W] = (I + A)^-1 [beta v | beta e^gamma k]  (forward substitution, one
 //                                                               column per thread, in registers)
+//   ring     the last three raw inputs of the block go to their ring slots (after the chunk
+//            pass, which reads the old ones).
 //   state    per (v-head, 16-column slice of the state), sequential over the chunks, on the
 //            fp32 matrix cores: store the chunk-start state S_c, v_new = U - W S,
 //              S <- e^(gamma_last) S + K^T (e^(gamma_last - gamma) v_new)
@@ -43,124 +45,6 @@ constexpr int kD = 128;   // GDN head dim
 constexpr int kC = 64;    // chunk length
 constexpr int kHD = 256;  // attention head dim
 
-// ------------------------------------------------------------------ GDN prep
-// grid (T / 16, KH), 384 threads: conv + SiLU of the k-head's q, k and its rep v-heads' v
-// channels for 16 tokens, l2norm of q and k, beta / g of the rep v-heads. Threads
-// 128 g .. 128 g + 127 take channel group g (q, k, v: two waves each); within a group, thread
-// t handles four consecutive tokens (group (t / 32) % 4) and four consecutive channels
-// (quad t % 32), so every load and store is 16 bytes and each 32-lane half-wave holds one
-// head's 128 channels of a token; its seven input rows (the four tokens and the three
-// before them) are read once.
-constexpr int kPT = 16;   // tokens per workgroup
-constexpr int kPTT = 4;   // tokens per thread
-
-__global__ __launch_bounds__(384) void gdn_prep_kernel(GdnPrefillArgs a) {
-    const int kh = blockIdx.y, tid = threadIdx.x;
-    const int grp = tid >> 7;                       // 0 q, 1 k, 2 v (uniform per wave)
-    const int tg = (tid >> 5) & 3, c4 = (tid & 31) * 4;  // token group; first channel in the head
-    const int t0 = blockIdx.x * kPT + kPTT * tg;
-    const int rep = a.VH / a.KH;
-    const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
-    const int nt = min(kPTT, a.T - t0);  // may be <= 0 for the last block's groups
-    // raw inputs of tokens t0 - 3 + j (the conv ring before the block), channels ch .. ch + 3
-    auto xin = [&](int s, int ch) -> float4 {
-        if (s >= 0) return *reinterpret_cast<const float4*>(a.qkv + static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch);
-        return *reinterpret_cast<const float4*>(a.conv_ring + static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch);
-    };
-    // causal conv + SiLU of four channels for the thread's tokens (the reference's 4-tap
-    // window, src/qwen_forward.cpp:109-118)
-    auto conv = [&](int ch, float (&y)[kPTT][4]) {
-        float4 x[kPTT + 3];
-#pragma unroll
-        for (int j = 0; j < kPTT + 3; ++j) x[j] = xin(t0 - 3 + j, ch);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float4 w4 = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(ch + e) * 4);
-            float xs[kPTT + 3];
-#pragma unroll
-            for (int j = 0; j < kPTT + 3; ++j) xs[j] = e == 0 ? x[j].x : e == 1 ? x[j].y : e == 2 ? x[j].z : x[j].w;
-#pragma unroll
-            for (int j = 0; j < kPTT; ++j) {
-                float acc = 0.0f;
-                acc += w4.x * xs[j];
-                acc += w4.y * xs[j + 1];
-                acc += w4.z * xs[j + 2];
-                acc += w4.w * xs[j + 3];
-                y[j][e] = silu_f(acc);
-            }
-        }
-    };
-    float y[kPTT][4];
-    if (grp < 2) {
-        conv(grp * KD + kh * kD + c4, y);
-        // l2norm per token over the head's 128 channels (this half-wave): sums in double
-#pragma unroll
-        for (int j = 0; j < kPTT; ++j) {
-            double ss = 0.0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ss += static_cast<double>(y[j][e]) * y[j][e];
-            ss = half_wave_sum(ss);
-            if (j >= nt) continue;
-            const float inv = 1.0f / sqrtf(static_cast<float>(ss) + 1e-6f);
-            const int64_t row = static_cast<int64_t>(kh) * a.Tp + t0 + j;
-            float4 o;
-            if (grp == 0) {
-                const float qs = 1.0f / sqrtf(static_cast<float>(kD));
-                o = make_float4((y[j][0] * inv) * qs, (y[j][1] * inv) * qs, (y[j][2] * inv) * qs, (y[j][3] * inv) * qs);
-                *reinterpret_cast<float4*>(a.Qg + row * kD + c4) = o;
-            } else {
-                o = make_float4(y[j][0] * inv, y[j][1] * inv, y[j][2] * inv, y[j][3] * inv);
-                *reinterpret_cast<float4*>(a.Kg + row * kD + c4) = o;
-            }
-        }
-        return;
-    }
-    // v channels of the v-heads served by this k-head
-    for (int r = 0; r < rep; ++r) {
-        const int vh = kh * rep + r;
-        conv(2 * KD + vh * kD + c4, y);
-#pragma unroll
-        for (int j = 0; j < kPTT; ++j)
-            if (j < nt)
-                *reinterpret_cast<float4*>(a.Vg + (static_cast<int64_t>(vh) * a.Tp + t0 + j) * kD + c4) =
-                    make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
-    }
-    // beta / g of (v-head, token) pairs: the v threads of token group 0
-    if (tg != 0) return;
-    for (int i = tid & 31; i < rep * kPT; i += 32) {
-        const int r = i / kPT, j = i - r * kPT, t = blockIdx.x * kPT + j;
-        if (t >= a.T) continue;
-        const int vh = kh * rep + r;
-        const float bb = a.b[static_cast<int64_t>(t) * a.ld_ba + vh];
-        const float aa = a.a[static_cast<int64_t>(t) * a.ld_ba + vh];
-        a.Bg[static_cast<int64_t>(vh) * a.Tp + t] = sigmoid_f(bb);
-        a.Gg[static_cast<int64_t>(vh) * a.Tp + t] = -expf(a.A_log[vh]) * softplus_f(aa + a.dt_bias[vh]);
-    }
-}
-
-// zero the padding rows [T, Tp) of the head-major prep outputs
-__global__ __launch_bounds__(256) void gdn_pad_kernel(GdnPrefillArgs a) {
-    const int pad = a.Tp - a.T;
-    const int64_t n_qk = static_cast<int64_t>(a.KH) * pad * kD, n_v = static_cast<int64_t>(a.VH) * pad * kD;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_qk + n_v + 2 * a.VH * pad;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        if (i < n_qk) {
-            const int64_t h = i / (pad * kD), rest = i % (pad * kD);
-            const int64_t off = (h * a.Tp + a.T) * kD + rest;
-            a.Qg[off] = 0.0f;
-            a.Kg[off] = 0.0f;
-        } else if (i < n_qk + n_v) {
-            const int64_t j = i - n_qk, h = j / (pad * kD), rest = j % (pad * kD);
-            a.Vg[(h * a.Tp + a.T) * kD + rest] = 0.0f;
-        } else {
-            const int64_t j = i - n_qk - n_v;
-            const int64_t h = (j % (a.VH * pad)) / pad, r = j % pad;
-            float* dst = j < a.VH * pad ? a.Bg : a.Gg;
-            dst[h * a.Tp + a.T + r] = 0.0f;
-        }
-    }
-}
-
 // ring slots of the block's last three raw inputs
 __global__ __launch_bounds__(256) void gdn_ring_kernel(GdnPrefillArgs a) {
     const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
@@ -180,32 +64,135 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
 }
 
 // ------------------------------------------------------------------ GDN chunk
-// grid (VH, Tp / 64), 256 threads. P and A on the fp32 matrix cores (K and Q rows padded to
-// 132 floats: the 16 rows x 4 dims of an operand read fall in 64 distinct banks). A takes
-// the place of Q in LDS once the products are done (68 KB in all: two workgroups per CU).
+// grid (VH, Tp / 64), 256 threads: the whole chunk pass of one (v-head, chunk of 64 tokens).
+//   inputs   thread (run, quad) convolves channels 4 quad .. + 3 of the head's q and k over
+//            tokens 8 run .. + 7 of the chunk (eleven raw rows, 16 bytes per load), and each
+//            32-lane half-wave (one run) sums a token's squares for the l2norm (in double);
+//            threads 0..127 convolve v channel tid over the 64 tokens (the column they solve
+//            for below); wave 0 forms beta and g, thread 0 the cumulative sum.
+//   products P and A on the fp32 matrix cores over the lower triangle of 16 x 16 blocks
+//            (three block pairs per wave, the last wave one), K and Q rows padded to 132
+//            floats so the 16 rows x 4 dims of an operand read fall in 64 distinct banks; A
+//            takes the place of Q in LDS once the products are done (68 KB in all: two
+//            workgroups per CU).
+//   solve    threads 0..127 the columns of beta v, 128..255 those of beta e^gamma k; step i
+//            requests row i + 1 of A before it computes, so it waits once per row.
 constexpr int kLdC = kD + 4;
 constexpr int kLdA = kC + 4;  // A rows: 16-byte aligned, read four entries at a time
+constexpr int kRun = 8;       // tokens per q / k conv run
 __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-    const int kh = vh / (a.VH / a.KH);
-    const int64_t row0 = static_cast<int64_t>(c) * kC;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int rep = a.VH / a.KH, kh = vh / rep;
+    const int KD = a.KH * kD, VD = a.VH * kD, CONV = 2 * KD + VD;
+    const int t0 = c * kC;
+    const int64_t row0 = t0;
     __shared__ __align__(16) float Ks[kC][kLdC];
     __shared__ __align__(16) float QA[kC * kLdC];
     float (*Qs)[kLdC] = reinterpret_cast<float (*)[kLdC]>(QA);
     float (*As)[kLdA] = reinterpret_cast<float (*)[kLdA]>(QA);
     __shared__ double gam[kC];
-    __shared__ float beta[kC], edl[kC];
-    const float* K = a.Kg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-    const float* Q = a.Qg + (static_cast<int64_t>(kh) * a.Tp + row0) * kD;
-    for (int f = tid; f < kC * kD / 4; f += 256) {
-        *reinterpret_cast<float4*>(&Ks[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(K + f * 4);
-        *reinterpret_cast<float4*>(&Qs[f >> 5][(f & 31) * 4]) = *reinterpret_cast<const float4*>(Q + f * 4);
+    __shared__ float beta[kC], gsh[kC], edl[kC];
+    // raw input of block token s (s < 0: the conv ring; s >= T: a padding row, zeroed below)
+    auto xin4 = [&](int s, int ch) -> float4 {
+        if (s >= 0) return *reinterpret_cast<const float4*>(a.qkv + static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch);
+        return *reinterpret_cast<const float4*>(a.conv_ring + static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch);
+    };
+    auto xin1 = [&](int s, int ch) -> float {
+        if (s >= 0) return a.qkv[static_cast<int64_t>(min(s, a.T - 1)) * a.ld_qkv + ch];
+        return a.conv_ring[static_cast<int64_t>((a.pos0 + s) & 3) * CONV + ch];
+    };
+    // every input requested up front: q / k runs, their taps, the v column and its taps
+    const int run = tid >> 5, c4 = 4 * (tid & 31);
+    const int ts0 = t0 + kRun * run;
+    float4 xq[kRun + 3], xk[kRun + 3];
+#pragma unroll
+    for (int j = 0; j < kRun + 3; ++j) {
+        xq[j] = xin4(ts0 - 3 + j, kh * kD + c4);
+        xk[j] = xin4(ts0 - 3 + j, KD + kh * kD + c4);
     }
-    if (tid < kC) beta[tid] = a.Bg[static_cast<int64_t>(vh) * a.Tp + row0 + tid];
+    float4 wq[4], wk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        wq[e] = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(kh * kD + c4 + e) * 4);
+        wk[e] = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(KD + kh * kD + c4 + e) * 4);
+    }
+    float xv[kC + 3];
+    float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < kD) {
+        const int ch = 2 * KD + vh * kD + tid;
+#pragma unroll
+        for (int j = 0; j < kC + 3; ++j) xv[j] = xin1(t0 - 3 + j, ch);
+        wv = *reinterpret_cast<const float4*>(a.conv_w + static_cast<int64_t>(ch) * 4);
+    }
+    if (tid < kC) {
+        const int t = t0 + tid;
+        float bb = 0.0f, gg = 0.0f;
+        if (t < a.T) {
+            bb = sigmoid_f(a.b[static_cast<int64_t>(t) * a.ld_ba + vh]);
+            gg = -expf(a.A_log[vh]) * softplus_f(a.a[static_cast<int64_t>(t) * a.ld_ba + vh] + a.dt_bias[vh]);
+        }
+        beta[tid] = bb;
+        gsh[tid] = gg;
+    }
+    // causal conv + SiLU of four channels over a run (the reference's 4-tap window,
+    // src/qwen_forward.cpp:109-118)
+    auto conv_run = [&](const float4 (&x)[kRun + 3], const float4 (&w)[4], float (&y)[kRun][4]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float xs[kRun + 3];
+#pragma unroll
+            for (int j = 0; j < kRun + 3; ++j) xs[j] = e == 0 ? x[j].x : e == 1 ? x[j].y : e == 2 ? x[j].z : x[j].w;
+#pragma unroll
+            for (int j = 0; j < kRun; ++j) {
+                float acc = 0.0f;
+                acc += w[e].x * xs[j];
+                acc += w[e].y * xs[j + 1];
+                acc += w[e].z * xs[j + 2];
+                acc += w[e].w * xs[j + 3];
+                y[j][e] = silu_f(acc);
+            }
+        }
+    };
+    {
+        // q: l2norm, scaled by DK^-1/2; to LDS and (once per k-head) to the workspace
+        const bool write_q = vh % rep == 0;
+        const float qs = 1.0f / sqrtf(static_cast<float>(kD));
+        float y[kRun][4];
+        conv_run(xq, wq, y);
+#pragma unroll
+        for (int j = 0; j < kRun; ++j) {
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss += static_cast<double>(y[j][e]) * y[j][e];
+            ss = half_wave_sum(ss);
+            const float inv = 1.0f / sqrtf(static_cast<float>(ss) + 1e-6f);
+            float4 o = make_float4((y[j][0] * inv) * qs, (y[j][1] * inv) * qs, (y[j][2] * inv) * qs, (y[j][3] * inv) * qs);
+            if (ts0 + j >= a.T) o = make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&Qs[kRun * run + j][c4]) = o;
+            if (write_q) *reinterpret_cast<float4*>(a.Qg + (static_cast<int64_t>(kh) * a.Tp + ts0 + j) * kD + c4) = o;
+        }
+    }
+    {
+        float y[kRun][4];
+        conv_run(xk, wk, y);
+#pragma unroll
+        for (int j = 0; j < kRun; ++j) {
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss += static_cast<double>(y[j][e]) * y[j][e];
+            ss = half_wave_sum(ss);
+            const float inv = 1.0f / sqrtf(static_cast<float>(ss) + 1e-6f);
+            float4 o = make_float4(y[j][0] * inv, y[j][1] * inv, y[j][2] * inv, y[j][3] * inv);
+            if (ts0 + j >= a.T) o = make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&Ks[kRun * run + j][c4]) = o;
+        }
+    }
+    __syncthreads();  // Q, K, beta, g in LDS
     if (tid == 0) {
         double s = 0.0;
         for (int i = 0; i < kC; ++i) {
-            s += static_cast<double>(a.Gg[static_cast<int64_t>(vh) * a.Tp + row0 + i]);
+            s += static_cast<double>(gsh[i]);
             gam[i] = s;
         }
     }
@@ -215,35 +202,42 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
         a.Eg[r] = expf(static_cast<float>(gam[tid]));
         edl[tid] = expf(static_cast<float>(gam[kC - 1] - gam[tid]));
     }
-    // P (j <= i) and A (j < i): S = Q K^T and KK = K K^T over the 128 dims; wave w owns rows
-    // [16 w, 16 w + 16) and the 4 blocks of 16 columns; lane (lr, lg) ends with rows
-    // 16 w + 4 lg + v of column 16 b + lr
+    // P (j <= i) and A (j < i): Q K^T and K K^T over the 128 dims for the block pairs
+    // (row block r, column block b <= r) of this wave: (3,0) (3,1) (3,2) | (3,3) (2,0) (2,1) |
+    // (2,2) (1,0) (1,1) | (0,0); lane (lr, lg) ends with rows 16 r + 4 lg + v of column 16 b + lr
     {
-        const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
-        floatx4 sq[4], sk[4];
+        const int pr[3] = {wave < 2 ? 3 : wave == 2 ? 2 : 0, wave == 0 ? 3 : wave == 1 ? 2 : 1,
+                           wave == 0 ? 3 : wave == 1 ? 2 : 1};
+        const int pb[3] = {wave == 0 ? 0 : wave == 1 ? 3 : wave == 2 ? 2 : 0, wave == 0 ? 1 : 0,
+                           wave == 0 ? 2 : 1};
+        const bool three = wave < 3;
+        floatx4 sq[3], sk[3];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) sq[b] = sk[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < 3; ++p) sq[p] = sk[p] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
         for (int k = 0; k < kD; k += 4) {
-            const float aq = Qs[16 * wave + lr][k + lg], ak = Ks[16 * wave + lr][k + lg];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const float bk = Ks[16 * b + lr][k + lg];
-                sq[b] = mfma4(aq, bk, sq[b]);
-                sk[b] = mfma4(ak, bk, sk[b]);
+            for (int p = 0; p < 3; ++p) {
+                if (p > 0 && !three) break;
+                const float aq = Qs[16 * pr[p] + lr][k + lg], ak = Ks[16 * pr[p] + lr][k + lg];
+                const float bk = Ks[16 * pb[p] + lr][k + lg];
+                sq[p] = mfma4(aq, bk, sq[p]);
+                sk[p] = mfma4(ak, bk, sk[p]);
             }
         }
         lds_barrier();  // every wave is done reading Q: A takes its place
+        // (P blocks above the diagonal are never read and are left unwritten)
         float* P = a.P + (static_cast<int64_t>(vh) * (a.Tp / kC) + c) * kC * kC;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int i = 16 * wave + 4 * lg + v;
+        for (int p = 0; p < 3; ++p) {
+            if (p > 0 && !three) break;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int j = 16 * b + lr;
+            for (int v = 0; v < 4; ++v) {
+                const int i = 16 * pr[p] + 4 * lg + v;
+                const int j = 16 * pb[p] + lr;
                 const float dec = j <= i ? expf(static_cast<float>(gam[i] - gam[j])) : 0.0f;
-                P[i * kC + j] = j <= i ? sq[b][v] * dec : 0.0f;
-                As[i][j] = j < i ? beta[i] * sk[b][v] * dec : 0.0f;
+                P[i * kC + j] = j <= i ? sq[p][v] * dec : 0.0f;
+                As[i][j] = j < i ? beta[i] * sk[p][v] * dec : 0.0f;
             }
         }
     }
@@ -251,19 +245,35 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_kernel(GdnPrefillArgs a) {
     // forward substitution on [beta v | beta e^gamma k], one column per thread
     float col[kC];
     if (tid < kD) {
-        const float* V = a.Vg + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + tid;
 #pragma unroll
-        for (int i = 0; i < kC; ++i) col[i] = beta[i] * V[static_cast<int64_t>(i) * kD];
+        for (int i = 0; i < kC; ++i) {
+            float acc = 0.0f;
+            acc += wv.x * xv[i];
+            acc += wv.y * xv[i + 1];
+            acc += wv.z * xv[i + 2];
+            acc += wv.w * xv[i + 3];
+            const float v = t0 + i < a.T ? silu_f(acc) : 0.0f;
+            col[i] = beta[i] * v;
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < kC; ++i) col[i] = beta[i] * expf(static_cast<float>(gam[i])) * Ks[i][tid - kD];
     }
+    float4 ar[2][16];
+    ar[1][0] = *reinterpret_cast<const float4*>(&As[1][0]);
 #pragma unroll
     for (int i = 1; i < kC; ++i) {
+        if (i + 1 < kC) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+                if (4 * q < i + 1) ar[(i + 1) & 1][q] = *reinterpret_cast<const float4*>(&As[i + 1][4 * q]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         float x = col[i];
 #pragma unroll
-        for (int k = 0; k < i; ++k) x = fmaf(-As[i][k], col[k], x);
+        for (int k = 0; k < i; ++k) x = fmaf(-ar[i & 1][k >> 2][k & 3], col[k], x);
         col[i] = x;
+        __builtin_amdgcn_sched_barrier(0);
     }
     float* dst = (tid < kD ? a.U : a.W) + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + (tid & (kD - 1));
 #pragma unroll
@@ -424,7 +434,8 @@ constexpr int kLdS = kD + 16;   // state / v_new rows (B operand)
 // readout. Wave w owns output rows [16w, 16w + 16), all 128 columns (8 blocks of 16).
 // S_c goes through LDS in two halves of 64 rows (71 KB of LDS, two workgroups per CU); every
 // operand is requested into registers at the start, so the later phases' loads (the second
-// half of S_c, P and v_new) arrive while the earlier phases multiply.
+// half of S_c, P and v_new, then the epilogue's gate and norm weight) arrive while the
+// earlier phases multiply.
 __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
@@ -494,6 +505,24 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
     }
     if (tid < kC) eg[tid] = egv;
     lds_barrier();  // LDS only: S_c[64:128), P and v_new stay in flight
+    // the epilogue's gate z (this lane's 4 rows x 8 columns) and norm weight (8 columns),
+    // requested now that the Q and S_c[0:64) registers are free (unconditional loads from a
+    // valid address: a raw readout reads the S_c tile and ignores it)
+    const bool gated = a.norm_w != nullptr;
+    float zr[4][8], nw[8];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int64_t t = row0 + 16 * wave + 4 * lg + v;
+        const int64_t tc = t < a.T ? t : a.T - 1;  // padding rows compute but store nothing
+        const float* zrow = gated ? a.z + tc * a.ld_z + vh * kD : Sc;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) zr[v][b] = zrow[16 * b + lr];
+    }
+    {
+        const float* nwp = gated ? a.norm_w : Sc;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) nw[b] = nwp[16 * b + lr];
+    }
 #pragma unroll
     for (int blk = 0; blk < kC / 16; ++blk) mma16(16 * blk, 16 * blk);
     lds_barrier();  // done with S_c[0:64)
@@ -529,14 +558,12 @@ __global__ __launch_bounds__(256, 2) void gdn_out_kernel(GdnPrefillArgs a) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);  // the 16 lanes of the row
         const float inv = 1.0f / sqrtf(static_cast<float>(ss / kD) + a.eps);
-        const int64_t tc = t < a.T ? t : a.T - 1;  // padding rows compute but store nothing
         float* out = a.out + t * (a.VH * kD) + vh * kD;
-        const float* z = a.z ? a.z + tc * a.ld_z + vh * kD : nullptr;
         float mx = 0.0f;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const int col = 16 * b + lr;
-            const float y = a.norm_w ? a.norm_w[col] * (acc[b][v] * inv) * silu_f(z[col]) : acc[b][v];
+            const float y = gated ? nw[b] * (acc[b][v] * inv) * silu_f(zr[v][b]) : acc[b][v];
             mx = fmaxf(mx, fabsf(y));
             if (t < a.T) {
                 if (a.out_tiled) a.out[xt_off(t, vh * kD + col, a.VH * kD)] = y;
@@ -1074,12 +1101,12 @@ int blocks_for(int64_t n) {
 
 int64_t gdn_prefill_workspace_floats(int KH, int VH, int T) {
     const int64_t Tp = (T + kC - 1) / kC * kC;
-    return (2 * KH + 3 * static_cast<int64_t>(VH)) * Tp * kD  // Qg Kg Vg U W
-           + 3 * static_cast<int64_t>(VH) * Tp                 // Bg Gg Eg
-           + static_cast<int64_t>(VH) * Tp * kD                // Kd
-           + static_cast<int64_t>(VH) * Tp * kC                // P
-           + static_cast<int64_t>(VH) * (Tp / kC) * kD * kD    // Sc (chunk-start states)
-           + 64 * 9;                                           // alignment slack
+    return (KH + 2 * static_cast<int64_t>(VH)) * Tp * kD  // Qg U W
+           + static_cast<int64_t>(VH) * Tp                 // Eg
+           + static_cast<int64_t>(VH) * Tp * kD            // Kd
+           + static_cast<int64_t>(VH) * Tp * kC            // P
+           + static_cast<int64_t>(VH) * (Tp / kC) * kD * kD  // Sc (chunk-start states)
+           + 64 * 6;                                       // alignment slack
 }
 
 void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
@@ -1090,12 +1117,8 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
         return p;
     };
     a.Qg = take(static_cast<int64_t>(a.KH) * a.Tp * kD);
-    a.Kg = take(static_cast<int64_t>(a.KH) * a.Tp * kD);
-    a.Vg = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
     a.U = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
     a.W = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
-    a.Bg = take(static_cast<int64_t>(a.VH) * a.Tp);
-    a.Gg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Eg = take(static_cast<int64_t>(a.VH) * a.Tp);
     a.Kd = take(static_cast<int64_t>(a.VH) * a.Tp * kD);
     a.P = take(static_cast<int64_t>(a.VH) * a.Tp * kC);
@@ -1103,10 +1126,8 @@ void gdn_prefill_carve(GdnPrefillArgs& a, float* ws) {
 }
 
 hipError_t launch_gdn_prefill(GdnPrefillArgs& a, hipStream_t s) {
-    klaunch(gdn_prep_kernel, dim3((a.T + kPT - 1) / kPT, a.KH), 384, 0, s, a);
-    if (a.Tp > a.T) klaunch(gdn_pad_kernel, blocks_for(static_cast<int64_t>(a.KH + a.VH) * (a.Tp - a.T) * kD), 256, 0, s, a);
-    klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
     klaunch(gdn_chunk_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
+    klaunch(gdn_ring_kernel, blocks_for(3 * (2 * a.KH * kD + a.VH * kD)), 256, 0, s, a);
     klaunch(gdn_state_kernel, dim3(a.VH, kD / kSW), kSThreads, 0, s, a);
     klaunch(gdn_out_kernel, dim3(a.VH, a.Tp / kC), 256, 0, s, a);
     return hipGetLastError();

@@ -209,10 +209,10 @@ struct GdnPrefillArgs {
     const float *conv_w, *A_log, *dt_bias, *norm_w;  // norm_w null: raw readout
     float *conv_ring, *state;
     float* out;        // [T][VH * 128]
-    // workspace (head-major, padded to Tp rows); Eg = e^gamma of each row, gamma the
-    // chunk-local cumulative decay; Kd = K e^(gamma_last - gamma) per (v-head, chunk),
-    // transposed ([128 dims][64 rows])
-    float *Qg, *Kg, *Vg, *U, *W, *Bg, *Gg, *Eg, *Kd, *P;
+    // workspace (head-major, padded to Tp rows): Qg the normalised, scaled q; Eg = e^gamma
+    // of each row, gamma the chunk-local cumulative decay; Kd = K e^(gamma_last - gamma) per
+    // (v-head, chunk), transposed ([128 dims][64 rows]); P the chunk's decayed Q K^T
+    float *Qg, *U, *W, *Eg, *Kd, *P;
     float* Sc;         // [VH][Tp / 64][128][128] state at the start of each chunk
     float* omax = nullptr;  // maximum |out| of each (token, v-head): [T][VH] (may be null)
     int out_tiled = 0;      // out in the xt_off layout (K = VH * 128)
