@@ -464,6 +464,8 @@ def main() -> None:
                     help="KV cache element type (decode, attn): fp32 is the reference's cache")
     ap.add_argument("--prefill-exact", action="store_true",
                     help="prefill: projection GEMMs on three exact bf16 parts (no fp16 weight copies)")
+    ap.add_argument("--no-prefill-line", action="store_true",
+                    help="default decode run: skip the 4096-token prefill measured beside it")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()
@@ -606,6 +608,20 @@ def bench_decode(a) -> None:
         "device_ms_per_step": dev_ms / a.steps,
     }
     m.close()
+    if not (small or long_ctx) and not a.no_prefill_line:
+        # the whole-prompt path measured in the same run (a 4096-token prefill of the same
+        # checkpoint, 2 warm-up + 8 timed + 1 kernel-timed), so that its figures are timed by
+        # whoever runs the default bench; `--workload prefill` gives the full line
+        try:
+            pa = argparse.Namespace(**vars(a))
+            pa.steps, pa.warmup, pa.prompt, pa.prefill_block = 8, 2, 4096, 0
+            pa.prefill_exact, pa.no_cpu_baseline, pa.model_dir = False, True, model_dir
+            pf = bench_prefill(pa)
+            result["prefill_4096"] = {"value": pf["value"], "unit": pf["unit"], "ms_per_prompt": pf["ms_per_step"],
+                                      "roofline": pf["roofline"], "mixers": pf["mixers"],
+                                      "kernels": pf["kernels"], "config": pf["config"]}
+        except Exception as e:  # the decode line stands on its own
+            result["prefill_4096"] = {"error": repr(e)}
     if a.calibration_copy:
         calibration_copy()
     traffic_file = os.path.join(ROOT, "profiles", "decode_2b_8k_traffic.json")
