@@ -237,7 +237,7 @@ q35_status q35_model_read_hidden(q35_model *m, float *host);
 #define Q35_KT_ATTN_COMBINE 3
 #define Q35_KT_OTHER 4
 #define Q35_KT_GEMM 5          /* prefill projections */
-#define Q35_KT_GDN_PREFILL 6   /* one layer's chunked GDN (prep, chunk, scan, gated norm) */
+#define Q35_KT_GDN_PREFILL 6   /* one layer's chunked GDN (chunk pass, ring, scan, gated norm) */
 #define Q35_KT_ATTN_PREFILL 7  /* one layer's q/k norm + RoPE + append and flash kernel */
 #define Q35_KT_COUNT 8
 q35_status q35_model_set_kernel_timing(q35_model *m, int32_t enable);
