@@ -610,11 +610,11 @@ def bench_decode(a) -> None:
     m.close()
     if not (small or long_ctx) and not a.no_prefill_line:
         # the whole-prompt path measured in the same run (a 4096-token prefill of the same
-        # checkpoint, 2 warm-up + 8 timed + 1 kernel-timed), so that its figures are timed by
+        # checkpoint, 4 warm-up + 16 timed + 1 kernel-timed), so that its figures are timed by
         # whoever runs the default bench; `--workload prefill` gives the full line
         try:
             pa = argparse.Namespace(**vars(a))
-            pa.steps, pa.warmup, pa.prompt, pa.prefill_block = 8, 2, 4096, 0
+            pa.steps, pa.warmup, pa.prompt, pa.prefill_block = 16, 4, 4096, 0
             pa.prefill_exact, pa.no_cpu_baseline, pa.model_dir = False, True, model_dir
             pf = bench_prefill(pa)
             result["prefill_4096"] = {"value": pf["value"], "unit": pf["unit"], "ms_per_prompt": pf["ms_per_step"],

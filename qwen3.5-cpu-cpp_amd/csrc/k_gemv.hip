@@ -20,6 +20,8 @@
 // overlaps the input staging (its barriers order LDS only, so they do not wait for the
 // weights in flight). bf16 is widened exactly (shift into the upper half of an
 // fp32) and accumulated in fp32 FMA; the 64 lane partials are summed with a butterfly.
+#include <climits>
+#include <cmath>
 #include <cstdlib>
 
 #include "dev_common.hpp"
@@ -46,13 +48,26 @@ __device__ __forceinline__ float dot8(const u32x4 w, const float4 x0, const floa
     return acc;
 }
 
+// 4 consecutive bf16 embedding elements, widened exactly
+__device__ __forceinline__ float4 embed4(const uint16_t* row, int i) {
+    const uint2 v = *reinterpret_cast<const uint2*>(row + i);
+    return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+}
+
 template <int PRO>
-__device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs) {
+__device__ __forceinline__ void stage_input(const GemvArgs& a, const uint16_t* erow, float* xs) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = a.in_dim;
     __shared__ double red[4];
     __shared__ float head_inv[64];
-    if (PRO == kProSwiGlu) {
+    if (PRO == kProRmsNorm && erow) {
+        for (int i = tid * 4; i < n; i += 1024) {
+            const float4 v = embed4(erow, i);
+            *reinterpret_cast<float4*>(xs + i) = v;
+            if (a.x_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.x_out + i) = v;
+        }
+        lds_barrier();  // the sum of squares below reads the staged row
+    } else if (PRO == kProSwiGlu) {
         for (int i = tid * 4; i < n; i += 1024) {
             const float4 g = *reinterpret_cast<const float4*>(a.x + i);
             const float4 u = *reinterpret_cast<const float4*>(a.x + n + i);
@@ -70,7 +85,7 @@ __device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs) {
     if (PRO == kProRmsNorm) {
         double ss = 0.0;
         for (int i = tid; i < n; i += 256) {
-            const double v = a.x[i];
+            const double v = erow ? xs[i] : a.x[i];
             ss += v * v;
         }
         ss = block_sum_lds(ss, red);
@@ -138,13 +153,26 @@ __device__ __forceinline__ void load_conv(const GemvArgs& a, int r0, int pos, Co
     }
 }
 
+// (value, row) order of the argmax partials: larger value first, then the smaller row
+__device__ __forceinline__ bool amax_better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
 template <int EPI, int RPW>
 __device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const float (&acc)[RPW],
-                                           const ConvIn<RPW>& cv, int pos) {
+                                           const ConvIn<RPW>& cv, int pos, float& bv, int& bi) {
     const int lane = threadIdx.x & 63;
     float sum[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) sum[r] = wave_sum(acc[r]);
+    if (EPI == kEpiStore && a.amax_part) {  // the sums are uniform: every lane tracks them
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            if (r0 + r < a.rows && amax_better(sum[r], r0 + r, bv, bi)) {
+                bv = sum[r];
+                bi = r0 + r;
+            }
+    }
     if (lane != 0) return;
     if (EPI == kEpiConvSilu) {
         // taps oldest first, the raw projection as the newest input; the raw value goes to
@@ -183,7 +211,7 @@ __device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const floa
 template <int EPI, int RPW, int KC, bool PF>
 __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, int r0,
                                           const u32x4 (&pf)[pf_chunks(KC)][RPW], const ConvIn<RPW>& cv,
-                                          int pos) {
+                                          int pos, float& bv, int& bi) {
     const int lane = threadIdx.x & 63;
     float acc[RPW];
 #pragma unroll
@@ -206,7 +234,7 @@ __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, in
 #pragma unroll
             for (int r = 0; r < RPW; ++r) acc[r] = dot8(w[u][r], x0, x1, acc[r]);
         }
-        store_rows<EPI, RPW>(a, r0, acc, cv, pos);
+        store_rows<EPI, RPW>(a, r0, acc, cv, pos, bv, bi);
         return;
     }
     const int n = a.in_dim;
@@ -264,7 +292,7 @@ __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, in
             acc[r] = dot8(w, x0, x1, acc[r]);
         }
     }
-    store_rows<EPI, RPW>(a, r0, acc, cv, pos);
+    store_rows<EPI, RPW>(a, r0, acc, cv, pos, bv, bi);
 }
 
 // Input staged through registers (n <= 1024 NX): the input loads are issued first, then
@@ -272,16 +300,18 @@ __device__ __forceinline__ void row_group(const GemvArgs& a, const float* xs, in
 // order for the wait counter, so issuing the input first lets the prologue wait for the
 // input alone while the weights are still in flight.
 template <int PRO, int NX>
-__device__ __forceinline__ void load_input(const GemvArgs& a, float4 (&xv)[NX], float4 (&gv)[NX],
-                                           float4 (&wv)[NX]) {
+__device__ __forceinline__ void load_input(const GemvArgs& a, const uint16_t* erow, float4 (&xv)[NX],
+                                           uint2 (&xe)[NX], float4 (&gv)[NX], float4 (&wv)[NX]) {
     const int tid = threadIdx.x, n = a.in_dim;
     // Unconditional loads (indices clamped into the vector, surplus lanes masked later): a
     // load under a branch makes the wait-count insertion fall back to waiting for every
-    // outstanding load, the weight prefetch included.
+    // outstanding load, the weight prefetch included. (`erow` is uniform over the grid; the
+    // embedding's bf16 elements are widened in finish_input, so nothing here waits for them.)
 #pragma unroll
     for (int j = 0; j < NX; ++j) {
         const int i = min((tid + j * 256) * 4, n - 4);
-        xv[j] = *reinterpret_cast<const float4*>(a.x + i);
+        if (PRO == kProRmsNorm && erow) xe[j] = *reinterpret_cast<const uint2*>(erow + i);
+        else xv[j] = *reinterpret_cast<const float4*>(a.x + i);
         if (PRO == kProRmsNorm) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + i);
         if (PRO == kProGatedNorm) {
             gv[j] = *reinterpret_cast<const float4*>(a.gate + i);
@@ -291,16 +321,27 @@ __device__ __forceinline__ void load_input(const GemvArgs& a, float4 (&xv)[NX], 
 }
 
 template <int PRO, int NX>
-__device__ __forceinline__ void finish_input(const GemvArgs& a, float4 (&xv)[NX], const float4 (&gv)[NX],
+__device__ __forceinline__ void finish_input(const GemvArgs& a, const uint16_t* erow, float4 (&xv)[NX],
+                                             const uint2 (&xe)[NX], const float4 (&gv)[NX],
                                              const float4 (&wv)[NX], float* xs) {
     const int tid = threadIdx.x, n = a.in_dim;
     __shared__ double red[4];
+    if (PRO == kProRmsNorm && erow) {
+#pragma unroll
+        for (int j = 0; j < NX; ++j)
+            xv[j] = make_float4(bf16_lo(xe[j].x), bf16_hi(xe[j].x), bf16_lo(xe[j].y), bf16_hi(xe[j].y));
+    }
     // Every use below is unconditional (slots past the input are zeroed by a select and
     // stored to the spare slot xs[n .. n+3]): a use under a branch lets the compiler sink
     // the input loads behind the weight loads, and then staging waits for all of them.
 #pragma unroll
     for (int j = 0; j < NX; ++j)
         if ((tid + j * 256) * 4 >= n) xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (PRO == kProRmsNorm && a.x_out && blockIdx.x == 0) {  // the embedding row, as read
+#pragma unroll
+        for (int j = 0; j < NX; ++j)
+            if ((tid + j * 256) * 4 < n) *reinterpret_cast<float4*>(a.x_out + (tid + j * 256) * 4) = xv[j];
+    }
     if (PRO == kProRmsNorm) {
         double ss = 0.0;
 #pragma unroll
@@ -345,35 +386,60 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int row_step = gridDim.x * 4 * RPW;
     int r0 = (blockIdx.x * 4 + wave) * RPW;
-    // the position first (a scalar load: the ring loads below depend on it, and waiting for
-    // it must not wait for the vector loads)
+    // the position and the token first (scalar loads: the ring and embedding loads below
+    // depend on them, and waiting for them must not wait for the vector loads)
     const int pos = EPI == kEpiConvSilu ? *a.pos_dev : 0;
+    const uint16_t* erow = PRO == kProRmsNorm && a.embed ? a.embed + static_cast<int64_t>(*a.token) * a.in_dim : nullptr;
     float4 xv[NX > 0 ? NX : 1], gv[NX > 0 ? NX : 1], wv[NX > 0 ? NX : 1];
-    if (NX > 0) load_input<PRO>(a, xv, gv, wv);
+    uint2 xe[NX > 0 ? NX : 1];
+    if (NX > 0) load_input<PRO>(a, erow, xv, xe, gv, wv);
     // The first row group's weights do not depend on the input: their loads are in flight
     // while the prologue works.
     u32x4 pf[pf_chunks(KC)][RPW];
     load_rows<RPW, KC>(a, r0, pf);  // rows clamped: unconditional, see load_input
     ConvIn<RPW> cv;
     if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
-    if (NX > 0) finish_input<PRO>(a, xv, gv, wv, xs);
-    else stage_input<PRO>(a, xs);
-    if (r0 >= a.rows) return;
-    if (KC > 0) {
-        // one register set: compute the group in `pf`, then load the next one into it
-        for (;;) {
-            row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos);
-            r0 += row_step;
-            if (r0 >= a.rows) break;
-            load_rows<RPW, KC>(a, r0, pf);
-            if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+    if (NX > 0) finish_input<PRO>(a, erow, xv, xe, gv, wv, xs);
+    else stage_input<PRO>(a, erow, xs);
+    float bv = -INFINITY;  // argmax partial of this wave's rows (amax_part)
+    int bi = INT_MAX;
+    if (r0 < a.rows) {
+        if (KC > 0) {
+            // one register set: compute the group in `pf`, then load the next one into it
+            for (;;) {
+                row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos, bv, bi);
+                r0 += row_step;
+                if (r0 >= a.rows) break;
+                load_rows<RPW, KC>(a, r0, pf);
+                if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+            }
+        } else {
+            row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos, bv, bi);
+            for (r0 += row_step; r0 < a.rows; r0 += row_step) {
+                if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+                row_group<EPI, RPW, KC, false>(a, xs, r0, pf, cv, pos, bv, bi);
+            }
         }
-        return;
     }
-    row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos);
-    for (r0 += row_step; r0 < a.rows; r0 += row_step) {
-        if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
-        row_group<EPI, RPW, KC, false>(a, xs, r0, pf, cv, pos);
+    if (EPI == kEpiStore && a.amax_part) {  // uniform over the grid
+        __shared__ float sv[4];
+        __shared__ int si[4];
+        if ((threadIdx.x & 63) == 0) {
+            sv[wave] = bv;
+            si[wave] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float v = sv[0];
+            int i = si[0];
+            for (int w = 1; w < 4; ++w)
+                if (amax_better(sv[w], si[w], v, i)) {
+                    v = sv[w];
+                    i = si[w];
+                }
+            a.amax_part[blockIdx.x] = v;
+            reinterpret_cast<int*>(a.amax_part + gridDim.x)[blockIdx.x] = i;
+        }
     }
 }
 
@@ -386,17 +452,14 @@ int gemv_max_blocks() {
     return v;
 }
 
+bool gemv_two_rows(int rows, int epilogue) { return epilogue == kEpiSwiGluPair || rows >= 8192; }
+
 template <int PRO, int EPI, int NX, int KC>
 hipError_t launch_kc(const GemvArgs& a, hipStream_t s) {
     const size_t lds = static_cast<size_t>(a.in_dim + 4) * sizeof(float);  // + the spare slot
-    const int max_blocks = gemv_max_blocks();
-    if (EPI == kEpiSwiGluPair || a.rows >= 8192) {
-        const int blocks = min(max_blocks, (a.rows + 7) / 8);
-        klaunch(gemv_kernel<PRO, EPI, 2, NX, KC>, blocks, 256, lds, s, a);
-    } else {
-        const int blocks = min(max_blocks, (a.rows + 3) / 4);
-        klaunch(gemv_kernel<PRO, EPI, 1, NX, KC>, blocks, 256, lds, s, a);
-    }
+    const int blocks = gemv_blocks(a, EPI);
+    if (gemv_two_rows(a.rows, EPI)) klaunch(gemv_kernel<PRO, EPI, 2, NX, KC>, blocks, 256, lds, s, a);
+    else klaunch(gemv_kernel<PRO, EPI, 1, NX, KC>, blocks, 256, lds, s, a);
     return hipGetLastError();
 }
 
@@ -459,7 +522,17 @@ hipError_t gemv_enable_wide_inputs() {
     return e;
 }
 
+int gemv_blocks(const GemvArgs& a, int epilogue) {
+    if (epilogue == kEpiAuto) epilogue = a.resid ? kEpiResidual : kEpiStore;
+    const int per = gemv_two_rows(a.rows, epilogue) ? 8 : 4;  // rows per workgroup and group
+    const int blocks = min(gemv_max_blocks(), (a.rows + per - 1) / per);
+    return a.amax_part ? min(blocks, kArgmaxParts) : blocks;
+}
+
 hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue) {
+    if ((a.embed && (prologue != kProRmsNorm || !a.token)) ||
+        (a.amax_part && !(epilogue == kEpiStore || (epilogue == kEpiAuto && !a.resid))))
+        return hipErrorInvalidValue;
     switch (prologue) {
         case kProPlain: return launch_pro<kProPlain>(a, epilogue, s);
         case kProRmsNorm: return launch_pro<kProRmsNorm>(a, epilogue, s);

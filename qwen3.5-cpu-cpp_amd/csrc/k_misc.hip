@@ -190,11 +190,11 @@ __global__ __launch_bounds__(256) void argmax_pass1(const float* logits, int n, 
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_pass2(const float* pv, const int* pi, int* token_out,
+__global__ __launch_bounds__(256) void argmax_pass2(const float* pv, const int* pi, int n_parts, int* token_out,
                                                     int* ids, int* pos) {
     float bv = -INFINITY;
     int bi = INT_MAX;
-    for (int b = threadIdx.x; b < kArgmaxBlocks; b += 256)
+    for (int b = threadIdx.x; b < n_parts; b += 256)
         if (better(pv[b], pi[b], bv, bi)) {
             bv = pv[b];
             bi = pi[b];
@@ -387,7 +387,14 @@ hipError_t launch_argmax(const float* logits, int n, void* part, int* token_out,
     float* pv = static_cast<float*>(part);
     int* pi = reinterpret_cast<int*>(pv + kArgmaxBlocks);
     klaunch(argmax_pass1, kArgmaxBlocks, 256, 0, s, logits, n, pv, pi);
-    klaunch(argmax_pass2, 1, 256, 0, s, pv, pi, token_out, ids, pos);
+    klaunch(argmax_pass2, 1, 256, 0, s, pv, pi, kArgmaxBlocks, token_out, ids, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_parts(const void* part, int n_parts, int* token_out, int* ids, int* pos,
+                               hipStream_t s) {
+    const float* pv = static_cast<const float*>(part);
+    klaunch(argmax_pass2, 1, 256, 0, s, pv, reinterpret_cast<const int*>(pv + n_parts), n_parts, token_out, ids, pos);
     return hipGetLastError();
 }
 

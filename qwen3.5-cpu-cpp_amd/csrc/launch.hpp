@@ -55,12 +55,24 @@ struct GemvArgs {
     float* conv_ring;
     const int* pos_dev;
     int conv_rows;
+    // kProRmsNorm input from the embedding: x = bf16 row *token of embed (in_dim wide) in
+    // place of x, and workgroup 0 stores it to x_out (the residual stream of the step)
+    const uint16_t* embed = nullptr;
+    const int* token = nullptr;
+    float* x_out = nullptr;
+    // kEpiStore: each workgroup also writes the largest output it stored and its row (the
+    // first row of that value; NaN never wins): values amax_part[0 .. blocks), then the rows
+    // as ints. The grid is gemv_blocks(); it is capped at kArgmaxParts when this is set.
+    float* amax_part = nullptr;
 };
 // Epilogue: store y, add the residual (the default when resid is set), or, for an
 // interleaved [gate_0; up_0; gate_1; up_1; ...] matrix, y[i] = silu(row 2i) * row 2i+1, or
 // the GDN in-projection's conv window + SiLU on its conv rows (kEpiConvSilu).
 enum GemvEpilogue : int { kEpiAuto = -1, kEpiStore = 0, kEpiResidual = 1, kEpiSwiGluPair = 2, kEpiConvSilu = 3 };
 hipError_t launch_gemv(const GemvArgs& a, int prologue, hipStream_t s, int epilogue = kEpiAuto);
+// Workgroups of a launch_gemv grid (the argmax partials of amax_part: one per workgroup).
+constexpr int kArgmaxParts = 4096;
+int gemv_blocks(const GemvArgs& a, int epilogue);
 // Largest in_dim the matvec stages in LDS (128 KB of the 160 KB a gfx950 workgroup may use).
 constexpr int kGemvMaxIn = 32768;
 // Raises the dynamic-LDS limit of the matvec instantiations that stage inputs wider than
@@ -270,6 +282,9 @@ hipError_t launch_embed(const uint16_t* embed, const int* token_dev, float* hidd
 constexpr int kArgmaxBlocks = 256;
 hipError_t launch_argmax(const float* logits, int n, void* part, int* token_out, int* ids,
                          int* pos, hipStream_t s);
+// The final pass alone over n_parts (value, index) partials (a matvec's amax_part).
+hipError_t launch_argmax_parts(const void* part, int n_parts, int* token_out, int* ids, int* pos,
+                               hipStream_t s);
 hipError_t launch_add_int(int* p, int v, hipStream_t s);
 hipError_t launch_set_int(int* p, int v, hipStream_t s);
 hipError_t launch_copy_f32(float* dst, const float* src, int64_t n, hipStream_t s);

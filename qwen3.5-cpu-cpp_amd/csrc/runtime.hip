@@ -346,12 +346,16 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
     const int CONV = 2 * KD + VD;
     const int NQ = d.attn_q_heads, NKV = d.attn_kv_heads, HD = d.attn_head_dim;
     Launcher L{m, s, timed};
-    L.run(Q35_KT_OTHER, [&] { return q35k::launch_embed(m->embed, m->token_dev, m->hidden, H, s); });
     for (size_t li = 0; li < m->layers.size(); ++li) {
         const LayerDev& ly = m->layers[li];
         q35k::GemvArgs g{};
         g.W = ly.w_in;
         g.x = m->hidden;
+        if (li == 0) {  // the token's embedding row is the first projection's input (and hidden)
+            g.embed = m->embed;
+            g.token = m->token_dev;
+            g.x_out = m->hidden;
+        }
         g.norm_w = ly.input_ln;
         g.y = m->proj;
         g.rows = ly.in_rows;
@@ -464,10 +468,11 @@ q35_status enqueue_step(q35_model* m, hipStream_t s, bool timed) {
     hd.rows = d.vocab_size;
     hd.in_dim = H;
     hd.eps = d.rms_norm_eps;
-    L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(hd, q35k::kProRmsNorm, s); });
+    hd.amax_part = static_cast<float*>(m->argmax_part);  // the argmax's first pass, per workgroup
+    L.run(Q35_KT_GEMV, [&] { return q35k::launch_gemv(hd, q35k::kProRmsNorm, s, q35k::kEpiStore); });
     L.run(Q35_KT_OTHER, [&] {
-        return q35k::launch_argmax(m->logits, d.vocab_size, m->argmax_part, m->token_dev, m->ids_dev,
-                                   m->pos_dev, s);
+        return q35k::launch_argmax_parts(m->argmax_part, q35k::gemv_blocks(hd, q35k::kEpiStore), m->token_dev,
+                                         m->ids_dev, m->pos_dev, s);
     });
     return L.st;
 }
@@ -590,7 +595,7 @@ ScratchPlan scratch_plan(const q35_dims& d, int64_t max_ctx) {
     p.part = take(static_cast<size_t>(q35k::attn_partial_floats(NQ, NKV, HD, kMaxSplits)) * 4);
     p.logits = take(static_cast<size_t>(d.vocab_size) * 4);
     p.trace = take(static_cast<size_t>(d.n_layers_total) * H * 4);
-    p.am = take(static_cast<size_t>(2) * q35k::kArgmaxBlocks * 4);
+    p.am = take(static_cast<size_t>(2) * std::max(q35k::kArgmaxBlocks, q35k::kArgmaxParts) * 4);
     p.ints = take(16 * 4);
     p.ids = take(static_cast<size_t>(max_ctx) * 4);
     p.rope = take(static_cast<size_t>(max_ctx) * std::max(1, rot_dims(d)) * 4);

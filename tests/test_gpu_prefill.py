@@ -216,6 +216,7 @@ def run_gdn_prefill(hip, kh, vh, T, pos0, fused, seed):
 @pytest.mark.parametrize("kh,vh,T,pos0,fused", [
     (2, 2, 1, 0, True), (2, 2, 3, 0, False), (2, 2, 63, 0, True), (2, 2, 64, 0, False),
     (2, 2, 65, 5, True), (2, 2, 200, 2, False),
+    (2, 2, 1, 5, True), (2, 2, 2, 9, False),  # blocks shorter than the conv window after a ring
     (8, 16, 130, 3, True),      # v-heads = 2 k-heads
     (16, 16, 300, 7, True),     # the 2B / isolated-GDN head shape, ragged last chunk
 ])
