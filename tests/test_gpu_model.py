@@ -2,6 +2,7 @@
 against the oracle: logits and residual stream after every layer, greedy ids, recurrent state
 and KV rows after 512 steps, the 0.8B-shaped full greedy decode, graph replay, the
 zero-allocation step and the error paths."""
+import json
 import os
 import tempfile
 
@@ -308,3 +309,67 @@ def test_prefill_widths_not_multiple_of_32(tmp_path):
     ref = np.stack([o.step(int(t)) for t in prompt])
     o.close()
     assert rel_l2(pf, ref) < REL_L2
+
+
+def test_decode_hidden_staged_through_lds(tmp_path):
+    """Hidden 2560 (not a width whose input the matvec keeps in registers): the first
+    projection reads the token's embedding row through the LDS-staged prologue and stores it
+    as the residual stream; decode logits equal the oracle's step by step, and the device
+    greedy loop equals the step-by-step argmax."""
+    d = pyq35.default_dims(hidden_size=2560, n_layers_total=4, gdn_k_heads=2, gdn_v_heads=2,
+                           attn_q_heads=2, attn_kv_heads=1, ffn_intermediate=512,
+                           vocab_size=1024, native_max_context=4096)
+    path = str(tmp_path / "h2560")
+    pyq35.synth_write_model(path, d, seed=11, std=0.02)
+    prompt = pyq35.synth_token_ids(12, d.vocab_size, 12)
+    m = pyq35.Model(path, 64)
+    o = op.Oracle(path, 64)
+    lg = np.stack([m.step(int(t))[0] for t in prompt])
+    ref = np.stack([o.step(int(t)) for t in prompt])
+    assert rel_l2(lg, ref) < REL_L2
+    tok = int(np.argmax(lg[-1]))
+    ids = m.decode_greedy(tok, 6)
+    want = []
+    for _ in range(6):
+        tok = int(np.argmax(o.step(tok)))
+        want.append(tok)
+    o.close()
+    m.close()
+    np.testing.assert_array_equal(ids, want)
+
+
+def _set_all_embedding_rows_to_row0(path: str) -> None:
+    """Rewrites the checkpoint's embedding (the tied output head) with every row a copy of
+    row 0, in place (safetensors: 8-byte header length, JSON header, raw data)."""
+    f = os.path.join(path, "model.safetensors")
+    with open(f, "r+b") as fh:
+        n = int.from_bytes(fh.read(8), "little")
+        hdr = json.loads(fh.read(n))
+        name = next(k for k in hdr if k.endswith("embed_tokens.weight"))
+        t = hdr[name]
+        rows, cols = t["shape"]
+        b0, b1 = t["data_offsets"]
+        assert t["dtype"] == "BF16" and b1 - b0 == rows * cols * 2
+        fh.seek(8 + n + b0)
+        row0 = fh.read(cols * 2)
+        fh.seek(8 + n + b0)
+        fh.write(row0 * rows)
+
+
+def test_greedy_ties_take_the_first_index(tmp_path):
+    """Every row of the tied embedding / output head equal, so every logit of a step is the
+    same value: the greedy id is the first index, 0 (the reference's first-maximum rule),
+    through the output head's per-workgroup argmax partials (40000 rows: 2048 workgroups of
+    several row groups each) and the final pass."""
+    d = pyq35.default_dims(hidden_size=256, n_layers_total=4, gdn_k_heads=2, gdn_v_heads=2,
+                           attn_q_heads=2, attn_kv_heads=1, ffn_intermediate=512,
+                           vocab_size=40000, native_max_context=4096)
+    path = str(tmp_path / "ties")
+    pyq35.synth_write_model(path, d, seed=13, std=0.02)
+    _set_all_embedding_rows_to_row0(path)
+    m = pyq35.Model(path, 64)
+    lg, am = m.step(123)
+    assert np.all(lg == lg[0]) and am == 0
+    ids = m.decode_greedy(7, 5)
+    m.close()
+    np.testing.assert_array_equal(ids, np.zeros(5, np.int32))
