@@ -292,10 +292,12 @@ constexpr int kLdV = kC + 4;    // v_new, transposed: one row per state column
 
 // grid (VH, 128 / kSW), 512 threads: sequential over the chunks of one state column slice.
 // Per chunk: store the chunk-start state, v_new = U - W S (written over U), then
-// S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Eight waves: v_new rows
-// [16 (w % 4), + 16) over the dims [64 (w / 4), + 64) (the two halves meet through LDS), and
-// the new state rows [16 w, 16 w + 16). The next chunk's W and decayed K are loaded into
-// registers while the current one is computed.
+// S <- e^(gamma_last) S + (K e^(gamma_last - gamma))^T v_new. Two barriers per chunk:
+//   waves 0-3   v_new rows [16 w, 16 w + 16) over all 128 dims (the dim halves [0, 64) and
+//               [64, 128) in separate accumulation chains, summed in a fixed order)
+//   waves 4-7   meanwhile store the next chunk's W and decayed K (requested one chunk ago)
+//               into the other of two LDS buffers, and request the chunk after it
+//   all waves   the new state rows [16 w, 16 w + 16)
 // Operand layout: every matrix-core operand is read 16 bytes at a time. MFMA i of a 64-deep
 // product takes the reduction index 16 lg + i from lane group lg (i < 16), so a lane's
 // operands for four consecutive MFMAs are four consecutive floats of one LDS row: W rows and
@@ -305,100 +307,96 @@ constexpr int kSThreads = 512;
 __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) {
     const int vh = blockIdx.x, cs = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    const int vb = wave & 3, kq = wave >> 2;  // v_new row block and dim half of this wave
     const int col0 = cs * kSW;
     const int nchunk = a.Tp / kC;
+    const bool stager = wave >= 4;  // uniform per wave
+    const int st = tid & 255;       // thread index within the half
     __shared__ __align__(16) float St[kSW][kLdSt];
-    __shared__ __align__(16) float Wl[kC][kLdW];
-    __shared__ __align__(16) float Kt[kD][kLdKt];
+    __shared__ __align__(16) float Wl[2][kC][kLdW];
+    __shared__ __align__(16) float Kt[2][kD][kLdKt];
     __shared__ __align__(16) float VNt[kSW][kLdV];
-    __shared__ __align__(16) float VPt[kSW][kLdV];  // partial v_new of the upper dim half
     float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
     for (int i = tid; i < kD * kSW; i += kSThreads) St[i & 15][i >> 4] = S[(i >> 4) * kD + col0 + (i & 15)];
 
-    // staging: float4 f = tid + 512 i of the chunk's W (64 rows x 128 dims: row f / 32) and of
-    // its decayed, transposed keys (128 dims x 64 rows: dim f / 16). Everything a chunk step
-    // reads from global memory (W, Kd, e^gamma_last and this lane's U entries) is requested
-    // one chunk ahead, so the sequential chain only waits on LDS.
-    constexpr int NF = kC * kD / 4 / kSThreads;
-    // (vector-typed: an array of float4 structs here was moved into LDS by the compiler)
+    constexpr int NF = kC * kD / 4 / 256;  // float4 of W (and of Kd) per staging thread: 8
     floatx4 rw[NF], rk[NF];
-    float relast, ru[4];
-    auto load_chunk = [&](int c) {
+    auto load_chunk = [&](int c) {  // staging waves: the chunk's W and decayed K
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
         const float* Kd = a.Kd + (static_cast<int64_t>(vh) * nchunk + c) * kD * kC;
-        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + row0) * kD + col0;
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
-            const int f = tid + kSThreads * i;
+            const int f = st + 256 * i;
             rw[i] = *reinterpret_cast<const floatx4*>(W + f * 4);
             rk[i] = *reinterpret_cast<const floatx4*>(Kd + f * 4);
         }
-        relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + row0 + kC - 1];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * vb + 4 * lg + v) * kD + lr];
     };
-    auto store_chunk = [&]() {
+    auto store_chunk = [&](int b) {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
-            const int f = tid + kSThreads * i;
-            *reinterpret_cast<floatx4*>(&Wl[f >> 5][(f & 31) * 4]) = rw[i];
-            *reinterpret_cast<floatx4*>(&Kt[f >> 4][(f & 15) * 4]) = rk[i];
+            const int f = st + 256 * i;
+            *reinterpret_cast<floatx4*>(&Wl[b][f >> 5][(f & 31) * 4]) = rw[i];
+            *reinterpret_cast<floatx4*>(&Kt[b][f >> 4][(f & 15) * 4]) = rk[i];
         }
     };
-    load_chunk(0);
-    // LDS-only barriers inside the loop: the next chunk's loads and this chunk's global
-    // stores stay in flight through them (a full barrier would wait for every outstanding
-    // load, the prefetch included)
-    __syncthreads();  // the state slice is in LDS
-    // chunk-start states for the output pass: chunk 0's from LDS here, every later one from
-    // the registers that computed it (the end of the previous chunk step)
+    // v_new waves: this lane's U entries (rows 16 wave + 4 lg + v, column lr) of chunk c
+    float ru[4];
+    auto load_u = [&](int c) {
+        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * (wave & 3) + 4 * lg + v) * kD + lr];
+    };
+    // chunk 0 into buffer 0 (the staging waves), chunk 1 requested
+    if (stager) {
+        load_chunk(0);
+        store_chunk(0);
+        load_chunk(min(1, nchunk - 1));
+    } else {
+        load_u(0);
+    }
+    float relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + kC - 1];
+    __syncthreads();  // the state slice and chunk 0 are in LDS
     for (int i = tid; i < kD * kSW; i += kSThreads)
         a.Sc[static_cast<int64_t>(vh) * nchunk * kD * kD + (i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
     for (int c = 0; c < nchunk; ++c) {
-        lds_barrier();  // previous chunk done with Wl / Kt / St
-        store_chunk();
+        const int b = c & 1;
         const float elast = relast;
-        floatx4 vn;
+        if (!stager) {
+            // v_new rows [16 w, 16 w + 16) over dims [0, 64) and [64, 128): four chains each
+            const int vb = wave;
+            floatx4 part[2];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) vn[v] = ru[v];
-        lds_barrier();
-        load_chunk(min(c + 1, nchunk - 1));  // unconditional (the last chunk is requested twice)
-
-        // W S for v_new rows [16 vb, 16 vb + 16), dims [64 kq, 64 kq + 64) in this wave: four
-        // independent accumulation chains (MFMA i on chain i % 4), summed in a fixed order
-        floatx4 part;
-        {
-            floatx4 ch[4];
+            for (int kq = 0; kq < 2; ++kq) {
+                floatx4 ch[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) ch[q] = floatx4{0.f, 0.f, 0.f, 0.f};
-            const int k0 = 64 * kq + 16 * lg;
+                for (int q = 0; q < 4; ++q) ch[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+                const int k0 = 64 * kq + 16 * lg;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 wa = *reinterpret_cast<const float4*>(&Wl[16 * vb + lr][k0 + 4 * q]);
-                const float4 sb = *reinterpret_cast<const float4*>(&St[lr][k0 + 4 * q]);
-                ch[0] = mfma4(wa.x, sb.x, ch[0]);
-                ch[1] = mfma4(wa.y, sb.y, ch[1]);
-                ch[2] = mfma4(wa.z, sb.z, ch[2]);
-                ch[3] = mfma4(wa.w, sb.w, ch[3]);
+                for (int q = 0; q < 4; ++q) {
+                    const float4 wa = *reinterpret_cast<const float4*>(&Wl[b][16 * vb + lr][k0 + 4 * q]);
+                    const float4 sb = *reinterpret_cast<const float4*>(&St[lr][k0 + 4 * q]);
+                    ch[0] = mfma4(wa.x, sb.x, ch[0]);
+                    ch[1] = mfma4(wa.y, sb.y, ch[1]);
+                    ch[2] = mfma4(wa.z, sb.z, ch[2]);
+                    ch[3] = mfma4(wa.w, sb.w, ch[3]);
+                }
+                part[kq] = (ch[0] + ch[1]) + (ch[2] + ch[3]);
             }
-            part = (ch[0] + ch[1]) + (ch[2] + ch[3]);
-        }
-        if (kq == 1) *reinterpret_cast<floatx4*>(&VPt[lr][16 * vb + 4 * lg]) = part;
-        lds_barrier();
-        if (kq == 0) {
             float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
-            const floatx4 hi = *reinterpret_cast<const floatx4*>(&VPt[lr][16 * vb + 4 * lg]);
             floatx4 x;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                x[v] = vn[v] - (part[v] + hi[v]);
+                x[v] = ru[v] - (part[0][v] + part[1][v]);
                 U[(16 * vb + 4 * lg + v) * kD + lr] = x[v];
             }
             *reinterpret_cast<floatx4*>(&VNt[lr][16 * vb + 4 * lg]) = x;
+            load_u(min(c + 1, nchunk - 1));
+        } else if (c + 1 < nchunk) {
+            store_chunk(b ^ 1);                   // chunk c + 1, requested one step ago
+            load_chunk(min(c + 2, nchunk - 1));   // (the last chunk is requested again at the end)
         }
-        lds_barrier();  // VNt complete, every wave done reading St
+        relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(min(c + 1, nchunk - 1)) * kC + kC - 1];
+        lds_barrier();  // VNt and the next chunk's buffer written; every v_new read of St done
 
         // new state rows [16 w, 16 w + 16): rows 16 w + 4 lg + v of column lr in this lane
         floatx4 sn = *reinterpret_cast<const floatx4*>(&St[lr][16 * wave + 4 * lg]);
@@ -406,7 +404,7 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
         floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 ka = *reinterpret_cast<const float4*>(&Kt[16 * wave + lr][16 * lg + 4 * q]);
+            const float4 ka = *reinterpret_cast<const float4*>(&Kt[b][16 * wave + lr][16 * lg + 4 * q]);
             const float4 vv = *reinterpret_cast<const float4*>(&VNt[lr][16 * lg + 4 * q]);
             ch[0] = mfma4(ka.x, vv.x, ch[0]);
             ch[1] = mfma4(ka.y, vv.y, ch[1]);
@@ -420,8 +418,8 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
 #pragma unroll
             for (int v = 0; v < 4; ++v) Sc[(16 * wave + 4 * lg + v) * kD] = sn[v];
         }
+        lds_barrier();  // the new state rows in LDS; every read of VNt and of buffer b done
     }
-    __syncthreads();
     for (int i = tid; i < kD * kSW; i += kSThreads) S[(i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
 }
 
