@@ -1,7 +1,10 @@
 // bf16-weight x fp32-activation matvec for every projection of the decode step
 // (the reference's matmul(WeightView), src/forward_pass.cpp:44-75), with the elementwise
 // work that feeds or follows each projection fused in:
-//   prologue  rmsnorm (1+w)       input_layernorm / post_attention_layernorm / final norm
+//   prologue  rmsnorm (1+w)       input_layernorm / post_attention_layernorm / final norm;
+//                                 the first layer's input can be the token's bf16 embedding
+//                                 row (SafeTensors::get_row_f32, src/safetensors_loader.cpp:
+//                                 280-298), which workgroup 0 also stores as the residual
 //             silu(g) * u         SwiGLU of a [gate | up] input vector
 //             gated rmsnorm        GDN rmsnorm_gated before linear_attn.out_proj
 //   epilogue  y = resid + W x     residual add of the mixer / FFN output
@@ -11,6 +14,8 @@
 //                                 (QwenModel::gdn_step's conv, src/qwen_model.cpp:173-186)
 //                                 runs once, in the wave that produced the channel, instead
 //                                 of in every mixer workgroup that reads it
+//             argmax partials      output head: each workgroup's largest logit and its row
+//                                 (first of equal values), the greedy pick's first pass
 //
 // HBM-bound: every weight byte is read exactly once per step. A 256-thread workgroup
 // stages the transformed input vector in LDS once, then each 64-lane wave streams RPW
