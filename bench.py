@@ -466,6 +466,8 @@ def main() -> None:
                     help="prefill: projection GEMMs on three exact bf16 parts (no fp16 weight copies)")
     ap.add_argument("--no-prefill-line", action="store_true",
                     help="default decode run: skip the 4096-token prefill measured beside it")
+    ap.add_argument("--no-mixer-lines", action="store_true",
+                    help="default decode run: skip the isolated GDN / attention mixers measured beside it")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a 256 MiB device copy (reference for counter runs)")
     a = ap.parse_args()
@@ -622,6 +624,29 @@ def bench_decode(a) -> None:
                                       "kernels": pf["kernels"], "config": pf["config"]}
         except Exception as e:  # the decode line stands on its own
             result["prefill_4096"] = {"error": repr(e)}
+    if not (small or long_ctx) and not a.no_mixer_lines:
+        # the isolated mixer workloads measured in the same run: 18 GDN layers per launch
+        # (state in the Infinity Cache, and 16 rotated state sets read from HBM) and 6
+        # attention layers at 8k with the KV caches beyond the Infinity Cache; `--workload gdn`
+        # / `--workload attn` give the full lines
+        try:
+            iso = {}
+            for R in (1, 16):
+                ga = argparse.Namespace(**vars(a))
+                ga.steps, ga.warmup, ga.rotate = 64, 8, R
+                g = bench_gdn(ga)
+                key = "gdn_18layers_cache_resident" if R == 1 else f"gdn_18layers_{R}_state_sets"
+                iso[key] = {k: {"us_per_token": v["us_per_token"], "GBs": v["GBs"], "frac": v["frac"]}
+                            for k, v in g["variants"].items()}
+            aa = argparse.Namespace(**vars(a))
+            aa.steps, aa.warmup, aa.rotate, aa.ctx_list, aa.attn_splits = 64, 8, 8, [8192], 0
+            at = bench_attn(aa)["contexts"]["8192"]
+            iso["attn_6layers_8k_beyond_cache"] = {
+                "kv_sets": at["kv_sets"], "kv_working_set_MiB": at["kv_working_set_MiB"],
+                "one_launch_6_layers": at["batched"], "one_launch_per_layer": at["per_layer"]}
+            result["isolated_mixers"] = iso
+        except Exception as e:  # the decode line stands on its own
+            result["isolated_mixers"] = {"error": repr(e)}
     if a.calibration_copy:
         calibration_copy()
     traffic_file = os.path.join(ROOT, "profiles", "decode_2b_8k_traffic.json")

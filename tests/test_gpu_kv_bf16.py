@@ -132,6 +132,12 @@ def test_attn_decode_bf16_split_invariance(hip, n_splits):
     run_attn_decode_bf16(hip, 16, 2, 3000, 4096, n_splits, seed=91)
 
 
+@pytest.mark.parametrize("pos,n_splits", [(8192, 128), (9200, 128), (9700, 128), (9, 4)])
+def test_attn_decode_bf16_split_shapes(hip, pos, n_splits):
+    """Splits just past a multiple of the tile, ragged and shorter than a tile, bf16 cache."""
+    run_attn_decode_bf16(hip, 16, 2, pos, pos + 1, n_splits, seed=pos + 3)
+
+
 def test_attn_decode_bf16_layer_batch(hip):
     """Three layers in one launch: each layer's cache starts maxc * NKV * HD bf16 elements on."""
     run_attn_decode_bf16(hip, 8, 2, 700, 800, 0, seed=5, layers=3)

@@ -183,6 +183,19 @@ def test_attn_decode_split_invariance(hip, n_splits):
     assert rel_l2(out, ref) < REL_L2
 
 
+# (pos, n_splits) -> positions per split of the matrix-core kernel (four waves of 16-position
+# tiles): 8192 / 8263 over 128: 65 per split (a second, one-position tile), the last split 3
+# positions; 9200: 72 per split; 9700: 76; 130 over 2: 66 and 65; 9 over 4: 3 per split
+@pytest.mark.parametrize("pos,n_splits", [(8192, 128), (8263, 128), (9200, 128), (9700, 128), (130, 2), (9, 4)])
+def test_attn_decode_split_shapes(hip, pos, n_splits):
+    """Splits just past a multiple of the tile, ragged last splits and splits shorter than a
+    tile, against the oracle."""
+    out, ref, krow, kref, vrow, vref = run_attn(hip, 16, 2, pos, pos + 1, n_splits, seed=pos + n_splits)
+    assert rel_l2(out, ref) < REL_L2
+    np.testing.assert_allclose(krow, kref, rtol=2e-6, atol=2e-6)
+    np.testing.assert_array_equal(vrow, vref)
+
+
 @pytest.mark.parametrize("L,nq,nkv,pos,maxc", [
     (3, 8, 2, 700, 800),      # vector-ALU kernel (GQA 4)
     (6, 16, 2, 8200, 8300),   # matrix-core kernel, 6 layers at 8k: two workgroups per CU (42 splits)
