@@ -437,16 +437,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kMW = 4;  // waves per workgroup of the matrix-core kernel
 
-template <bool KVB>
-struct KvRaw;
-template <>
-struct KvRaw<false> {
-    using T = float4;
-    static __device__ __forceinline__ T load(const float* base, int64_t off) { return load_stream(base + off); }
-    static __device__ __forceinline__ float4 f4(const T& v) { return v; }
-};
-template <>
-struct KvRaw<true> {
+// four consecutive bf16 cache elements, read non-temporally and widened exactly
+struct KvBf16 {
     using T = uint2;
     static __device__ __forceinline__ T load(const float* base, int64_t off) {
         typedef unsigned int u2 __attribute__((ext_vector_type(2)));
@@ -457,10 +449,6 @@ struct KvRaw<true> {
         return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
     }
 };
-
-__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // rmsnorm (1 + w) + RoPE of one 256-vector held as 4 dims per lane (dims 4 lane .. + 3),
 // sum of squares in double; cos / sin of dims (d mod ROT/2) for d < ROT from the table or
@@ -499,10 +487,14 @@ __device__ __forceinline__ float4 norm_rope_row(float4 x, float4 w, float4 c, fl
 // weight of a wave's partial with maximum mw in a merge with maximum M (0 for an empty wave)
 __device__ __forceinline__ float m_run_of(float mw, float M) { return mw == -INFINITY ? 0.0f : expf(mw - M); }
 
-template <bool KVB>
-__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a) {
+// bf16 caches, GQA 8: split-K over the cache, a workgroup of four waves per (kv head, range of
+// positions) serving the 8 query heads from each K/V row. Each wave walks tiles of 16
+// positions: S = K.Q^T on the 16x16x32 bf16 matrix cores against the three exact bf16 parts
+// of Q, O += P.V on the 16x16x16 bf16 cores with the three exact parts of P (every bf16 x bf16
+// product is exact in fp32); online softmax per head; waves merged once at the end.
+__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(AttnDecodeArgs a) {
     attn_select_layer(a, blockIdx.z);
-    using KV = KvRaw<KVB>;
+    using KV = KvBf16;
     using KT = typename KV::T;
     constexpr int GRP = 8, TP = 16;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -524,16 +516,14 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     const int wl = has_new ? w1 - 1 : w1;
 
     const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
-    const float* Kc_ = KVB ? reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff)
-                           : a.k_cache + hoff;
-    const float* Vc_ = KVB ? reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff)
-                           : a.v_cache + hoff;
+    const float* Kc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff);
+    const float* Vc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff);
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
-    __shared__ float4 qs[16][64];             // Q operand: [c][lane]
-    // bf16 caches: the three exact bf16 parts of Q as the B operand of the 16x16x32 products,
+    __shared__ float4 qs[16][64];             // Q in fp32 (the appended row's score): [c][lane]
+    // the three exact bf16 parts of Q as the B operand of the 16x16x32 products,
     // [part][c][lane] with lane 16 g + head holding dims 32 c + 8 g .. + 7
-    __shared__ uint4 qsb[KVB ? 3 : 1][KVB ? 8 : 1][64];
+    __shared__ uint4 qsb[3][8][64];
     __shared__ float4 ks[kHD / 4], vs[kHD / 4];  // the appended rows (as the cache holds them)
     __shared__ float os[kMW][GRP][kHD];
     __shared__ float ml_s[kMW][GRP][2];
@@ -558,10 +548,10 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         cs4 = *reinterpret_cast<const float4*>(t + min(ci, max(half - 4, 0)));
         sn4 = *reinterpret_cast<const float4*>(t + half + min(ci, max(half - 4, 0)));
     }
-    // K rows as the A operand: fp32, 4 dims 16 c + 4 g .. per register (16 per tile); bf16,
-    // 8 dims 32 c + 8 g .. per 16-byte register (8 per tile, the 16x16x32 bf16 operand)
-    using KOp = typename std::conditional<KVB, uint4, KT>::type;
-    constexpr int NK = KVB ? 8 : 16;
+    // K rows as the A operand: 8 dims 32 c + 8 g .. per 16-byte register (8 per tile, the
+    // 16x16x32 bf16 operand)
+    using KOp = uint4;
+    constexpr int NK = 8;
     KOp kA[NK];
     KT vr[4][4];
     // Loads are issued unconditionally (a load under a branch makes the wait-count pass wait
@@ -571,17 +561,12 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     auto loadK = [&](KOp (&kr)[NK], int p0) {
         const int mask = -static_cast<int>(p0 < wl);  // all ones while live (no branch)
         const int64_t row = min(p0 + n16, last);
-        if constexpr (KVB) {
-            typedef unsigned int u4 __attribute__((ext_vector_type(4)));
-            const uint16_t* Kb = reinterpret_cast<const uint16_t*>(Kc_);
+        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+        const uint16_t* Kb = reinterpret_cast<const uint16_t*>(Kc_);
 #pragma unroll
-            for (int c = 0; c < NK; ++c) {
-                const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(Kb + row * kHD + ((32 * c + 8 * g) & mask)));
-                kr[c] = make_uint4(v.x, v.y, v.z, v.w);
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < NK; ++c) kr[c] = KV::load(Kc_, row * kHD + ((16 * c + 4 * g) & mask));
+        for (int c = 0; c < NK; ++c) {
+            const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(Kb + row * kHD + ((32 * c + 8 * g) & mask)));
+            kr[c] = make_uint4(v.x, v.y, v.z, v.w);
         }
     };
     auto loadV = [&](int p0) {
@@ -598,10 +583,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
 
     // ---- Q operand and the appended rows
     if (!a.rope_cs) rope_cs4(a.theta, ROT, pos, lane, cs4, sn4);  // double-precision angles
-    for (int e = tid; e < 16 * 32; e += kMW * 64)  // columns 8-15: zero heads
-        qs[e >> 5][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (KVB)
-        for (int e = tid; e < 3 * 8 * 32; e += kMW * 64)
+    for (int e = tid; e < 3 * 8 * 32; e += kMW * 64)  // columns 8-15: zero heads
             qsb[e >> 8][(e >> 5) & 7][16 * ((e >> 3) & 3) + 8 + (e & 7)] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
@@ -610,7 +592,7 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
         float4 y = norm_rope_row(px[i], pw[i], cs4, sn4, lane, ROT, a.eps);
         if (r < GRP) {
             qs[lane >> 2][16 * (lane & 3) + r] = y;  // dims 4 lane .. + 3 of head r
-            if constexpr (KVB) {  // dims 4 lane .. + 3 = half (lane & 1) of the slot (lane >> 3, (lane >> 1) & 3)
+            {  // dims 4 lane .. + 3 = half (lane & 1) of the slot (lane >> 3, (lane >> 1) & 3)
                 const float v4[4] = {y.x, y.y, y.z, y.w};
                 uint32_t hh[4], mm[4], ll[4];
 #pragma unroll
@@ -624,29 +606,20 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
             }
         } else {
             const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + lane * 4;
-            if constexpr (KVB) {
-                const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.k_cache) + off) =
-                    make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
-                y = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
-            } else {
-                *reinterpret_cast<float4*>(a.k_cache + off) = y;
-            }
+            const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.k_cache) + off) =
+                make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
+            y = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
             ks[lane] = y;
         }
     }
     if (owns_new && wave == 1) {
         const int64_t off = hoff + static_cast<int64_t>(pos) * kHD + lane * 4;
-        float4 y = vn4;
-        if constexpr (KVB) {
-            const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.v_cache) + off) =
-                make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
-            y = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
-        } else {
-            *reinterpret_cast<float4*>(a.v_cache + off) = y;
-        }
-        vs[lane] = y;
+        const float4 y = vn4;
+        const uint16_t b0 = f32_to_bf16(y.x), b1 = f32_to_bf16(y.y), b2 = f32_to_bf16(y.z), b3 = f32_to_bf16(y.w);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.v_cache) + off) =
+            make_uint2(b0 | (static_cast<uint32_t>(b1) << 16), b2 | (static_cast<uint32_t>(b3) << 16));
+        vs[lane] = make_float4(bf16_to_f32(b0), bf16_to_f32(b1), bf16_to_f32(b2), bf16_to_f32(b3));
     }
     // LDS-only barrier: the K / V tiles in flight are not waited for here
     lds_barrier();
@@ -659,41 +632,21 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
     // one tile of positions p0 .. p0 + 15 from K registers kr and the V registers; the next
     // tile's rows are requested as soon as these registers are consumed
     auto tile = [&](KOp (&kr)[NK], int p0, auto more) {
-        floatx4 S;
-        if constexpr (KVB) {
-            // bf16 K times the three exact bf16 parts of Q on the 16x16x32 bf16 matrix cores
-            // (every product exact in fp32), one accumulation chain per part
-            floatx4 S3[3];
+        // bf16 K times the three exact bf16 parts of Q on the 16x16x32 bf16 matrix cores
+        // (every product exact in fp32), one accumulation chain per part
+        floatx4 S3[3];
 #pragma unroll
-            for (int i = 0; i < 3; ++i) S3[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 3; ++i) S3[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < NK; ++c) {
-                const bf16x8 kop = __builtin_bit_cast(bf16x8, kr[c]);
+        for (int c = 0; c < NK; ++c) {
+            const bf16x8 kop = __builtin_bit_cast(bf16x8, kr[c]);
 #pragma unroll
-                for (int part = 0; part < 3; ++part)
-                    S3[part] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, __builtin_bit_cast(bf16x8, qsb[part][c][lane]),
-                                                                       S3[part], 0, 0, 0);
-                if ((c & 1) == 1) __builtin_amdgcn_sched_barrier(0);
-            }
-            S = (S3[2] + S3[1]) + S3[0];
-        } else {
-            // four independent accumulation chains (dims 16c + 4g + i, one chain per i)
-            floatx4 S4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) S4[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const float4 q = qs[c][lane];
-                const float4 k = KV::f4(kr[c]);
-                S4[0] = mfma16(k.x, q.x, S4[0]);
-                S4[1] = mfma16(k.y, q.y, S4[1]);
-                S4[2] = mfma16(k.z, q.z, S4[2]);
-                S4[3] = mfma16(k.w, q.w, S4[3]);
-                // keep the Q operand reads close to their use (a few in flight, not all 16)
-                if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-            }
-            S = (S4[0] + S4[1]) + (S4[2] + S4[3]);
+            for (int part = 0; part < 3; ++part)
+                S3[part] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, __builtin_bit_cast(bf16x8, qsb[part][c][lane]),
+                                                                   S3[part], 0, 0, 0);
+            if ((c & 1) == 1) __builtin_amdgcn_sched_barrier(0);
         }
+        const floatx4 S = (S3[2] + S3[1]) + S3[0];
         if constexpr (decltype(more)::value) loadK(kr, p0 + TP);
         float s[4];
 #pragma unroll
@@ -727,45 +680,32 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
                 O[t][3] *= fh[3];
             }
         }
-        if constexpr (KVB) {
-            // the three exact bf16 parts of P (A operand: head n16, positions 4g .. 4g + 3)
-            // times bf16 V (B operand: those positions, dim 64t + 4 n16 + i) on the 16x16x16
-            // bf16 matrix cores; V's 16-bit elements are regrouped from the rows as loaded
-            typedef short short4_ __attribute__((ext_vector_type(4)));
-            uint32_t hh[4], mm[4], ll[4];
+        // the three exact bf16 parts of P (A operand: head n16, positions 4g .. 4g + 3)
+        // times bf16 V (B operand: those positions, dim 64t + 4 n16 + i) on the 16x16x16
+        // bf16 matrix cores; V's 16-bit elements are regrouped from the rows as loaded
+        typedef short short4_ __attribute__((ext_vector_type(4)));
+        uint32_t hh[4], mm[4], ll[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) split3(p[v], hh[v], mm[v], ll[v]);
-            const short4_ pp[3] = {
-                __builtin_bit_cast(short4_, make_uint2(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16))),
-                __builtin_bit_cast(short4_, make_uint2(mm[0] | (mm[1] << 16), mm[2] | (mm[3] << 16))),
-                __builtin_bit_cast(short4_, make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16)))};
+        for (int v = 0; v < 4; ++v) split3(p[v], hh[v], mm[v], ll[v]);
+        const short4_ pp[3] = {
+            __builtin_bit_cast(short4_, make_uint2(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16))),
+            __builtin_bit_cast(short4_, make_uint2(mm[0] | (mm[1] << 16), mm[2] | (mm[3] << 16))),
+            __builtin_bit_cast(short4_, make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16)))};
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    uint32_t e[4];
+            for (int i = 0; i < 4; ++i) {
+                uint32_t e[4];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const uint32_t w = i < 2 ? vr[v][t].x : vr[v][t].y;
-                        e[v] = (i & 1) ? w >> 16 : w & 0xffffu;
-                    }
-                    const short4_ vb = __builtin_bit_cast(short4_, make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)));
-#pragma unroll
-                    for (int part = 0; part < 3; ++part)  // lo, mid, hi
-                        O[4 * t + i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pp[part], vb, O[4 * t + i], 0, 0, 0);
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t w = i < 2 ? vr[v][t].x : vr[v][t].y;
+                    e[v] = (i & 1) ? w >> 16 : w & 0xffffu;
                 }
-        } else {
+                const short4_ vb = __builtin_bit_cast(short4_, make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)));
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const float4 vv = KV::f4(vr[v][t]);
-                    O[4 * t + 0] = mfma16(p[v], vv.x, O[4 * t + 0]);
-                    O[4 * t + 1] = mfma16(p[v], vv.y, O[4 * t + 1]);
-                    O[4 * t + 2] = mfma16(p[v], vv.z, O[4 * t + 2]);
-                    O[4 * t + 3] = mfma16(p[v], vv.w, O[4 * t + 3]);
-                }
-        }
+                for (int part = 0; part < 3; ++part)  // lo, mid, hi
+                    O[4 * t + i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pp[part], vb, O[4 * t + i], 0, 0, 0);
+            }
         if constexpr (decltype(more)::value) loadV(p0 + TP);
     };
     int p0 = w0;
@@ -838,6 +778,322 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_kernel(AttnDecodeArgs a
                     make_float4(O[4 * t][r] * sc4[r], O[4 * t + 1][r] * sc4[r], O[4 * t + 2][r] * sc4[r],
                                 O[4 * t + 3][r] * sc4[r]);
     }
+    lds_barrier();
+    const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
+#pragma unroll
+    for (int it = 0; it < GRP * kHD / (4 * kMW * 64); ++it) {
+        const int e = (it * kMW * 64 + tid) * 4, h = e / kHD, dd = e - h * kHD;
+        float4 o = *reinterpret_cast<const float4*>(&os[0][h][dd]);
+#pragma unroll
+        for (int w = 1; w < kMW; ++w) {
+            const float4 x = *reinterpret_cast<const float4*>(&os[w][h][dd]);
+            o.x += x.x;
+            o.y += x.y;
+            o.z += x.z;
+            o.w += x.w;
+        }
+        *reinterpret_cast<float4*>(a.part_o + base * kHD + e) = o;
+    }
+    if (tid < GRP) {
+        float M = ml_s[0][tid][0];
+        for (int w = 1; w < kMW; ++w) M = fmaxf(M, ml_s[w][tid][0]);
+        float L = 0.0f;
+        for (int w = 0; w < kMW; ++w) L += ml_s[w][tid][1] * m_run_of(ml_s[w][tid][0], M);
+        a.part_ml[(base + tid) * 2] = M;
+        a.part_ml[(base + tid) * 2 + 1] = L;
+    }
+}
+
+// ---- fp32 caches, GQA 8: both products on v_mfma_f32_4x4x1_16b_f32 ----------------------
+// 16x16x4 products would use 8 of their 16 columns (8 query heads); the 4x4x1 instruction
+// holds 16 independent 4 x 4 blocks, so every lane carries a useful product. Lane l = 16 g + 4 pg + j (block b = l / 4 = pg + 4 g, A row / B column j):
+//   S = K.Q^T: A = K[row 4 pg + j][dim], B = Q[head 4 hg + j][dim] for the dims 16 u + 4 g + e
+//   (u = 0..15, e = 0..3) -- the K registers are the rows as the 16x16x4 kernel loads them --
+//   so block (pg, g) accumulates positions 4 pg .. + 3 x heads 4 hg .. + 3 over a quarter of
+//   the dims; the quarters are summed across lanes by the gfx950 16- and 32-lane swaps.
+//   Result: lane l holds S[4 pg + i][4 hg + (l & 3)] in register i.
+//   O += P.V: A = P[head 4 hg + (l & 3)][p] (every block), B = V[p][4 l + c] (component c of
+//   the lane's float4 of row p: V rows are loaded as whole contiguous 1 KB rows), so
+//   accumulator (hg, c) register i of lane l holds O[4 hg + i][4 l + c]: 8 x 4 registers for
+//   the 8 heads x 256 dims. P goes from the score lanes to the A operand through 512 bytes of
+//   LDS per wave.
+// 256 products of 4x4x1 per 16-position tile against 128 of 16x16x4: measured about 10-11
+// cycles against 32 per instruction, so each tile's products take ~2.5k cycles instead of ~4k.
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
+// sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16- and 32-lane swaps of gfx950)
+__device__ __forceinline__ float dimq_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    v = __builtin_bit_cast(float, static_cast<int>(r[0])) + __builtin_bit_cast(float, static_cast<int>(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, static_cast<int>(r[0])) + __builtin_bit_cast(float, static_cast<int>(r[1]));
+}
+// over the lanes l, l + 4, l + 8, l + 12 of a 16-lane row (DPP row rotations by 4 and 8)
+__device__ __forceinline__ float pg_max(float v) {
+    v = fmaxf(v, dpp_f<0x124>(v));
+    return fmaxf(v, dpp_f<0x128>(v));
+}
+__device__ __forceinline__ float pg_sum(float v) {
+    v += dpp_f<0x124>(v);
+    return v + dpp_f<0x128>(v);
+}
+
+__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(AttnDecodeArgs a) {
+    attn_select_layer(a, blockIdx.z);
+    constexpr int GRP = 8, TP = 16;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop bounds
+    const int n16 = lane & 15, g = lane >> 4, jj = lane & 3, pg = (lane >> 2) & 3;
+    const int split = blockIdx.x, kh = blockIdx.y;
+    const int pos = read_pos(a);
+    const int n = pos + 1;
+    const int per = split_len(n, a.n_splits);
+    const int j0 = split * per;
+    if (j0 >= n) return;
+    const int j1 = min(n, j0 + per);
+    const bool owns_new = j1 == n;
+    const int tpw = ((j1 - j0 + TP - 1) / TP + kMW - 1) / kMW;  // tiles per wave
+    const int w0 = min(j1, j0 + wave * tpw * TP), w1 = min(j1, w0 + tpw * TP);
+    // the wave ending at pos walks the cached positions only; the appended row is added at
+    // the end from LDS (so nothing in the tile loop depends on where pos falls)
+    const bool has_new = owns_new && w0 < w1 && w1 == n;  // empty waves also end at n
+    const int wl = has_new ? w1 - 1 : w1;
+
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    const float* Kc = a.k_cache + hoff;
+    const float* Vc = a.v_cache + hoff;
+    const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
+
+    __shared__ float4 qs[2][16][4][4];       // Q operand: [hg][u][j][g] = Q[4 hg + j][16 u + 4 g .. + 3]
+    __shared__ float4 ks[kHD / 4], vs[kHD / 4];  // the appended rows
+    __shared__ float4 pl[kMW][2][4][4];      // softmax weights of a tile: [hg][j][t] = P[4 hg + j][4 t .. + 3]
+    __shared__ float os[kMW][GRP][kHD];
+    __shared__ float ml_s[kMW][GRP][2];
+
+    // ---- prologue loads first (rows of this wave: q heads wave, wave + 4; the key on wave
+    // 0 and the value on wave 1 of the workgroup holding pos), then the first K / V tiles
+    const int ROT = a.ROT, half = ROT / 2;
+    float4 px[3], pw[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
+        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
+                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
+        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
+        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
+    }
+    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    const int ci = (lane * 4) % max(half, 4);  // table column of this lane's first dim
+    float4 cs4 = make_float4(1.f, 1.f, 1.f, 1.f), sn4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.rope_cs) {
+        const float* t = a.rope_cs + static_cast<int64_t>(pos) * ROT;
+        cs4 = *reinterpret_cast<const float4*>(t + min(ci, max(half - 4, 0)));
+        sn4 = *reinterpret_cast<const float4*>(t + half + min(ci, max(half - 4, 0)));
+    }
+    // K: row n16, dims 16 u + 4 g .. + 3 in register u; V: row p, dims 4 lane .. + 3 in
+    // register p. Loads are issued unconditionally (a load under a branch makes the
+    // wait-count pass wait for all outstanding loads at the join); past the end of the range
+    // every lane reads the same 16 bytes of a valid row.
+    float4 kA[16], vr[16];
+    const int last = max(wl - 1, 0);  // a valid row to clamp to
+    auto loadK = [&](float4 (&kr)[16], int p0) {
+        const int mask = -static_cast<int>(p0 < wl);  // all ones while live (no branch)
+        const int64_t row = min(p0 + n16, last);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) kr[u] = load_stream(Kc + row * kHD + ((16 * u + 4 * g) & mask));
+    };
+    auto loadV = [&](int p0) {
+        const int mask = -static_cast<int>(p0 < wl);
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const int64_t row = min((p0 + p) & mask, last) | (last & ~mask);
+            vr[p] = load_stream(Vc + row * kHD + ((4 * lane) & mask));
+        }
+    };
+    loadK(kA, w0);
+    loadV(w0);
+
+    // ---- Q operand and the appended rows
+    if (!a.rope_cs) rope_cs4(a.theta, ROT, pos, lane, cs4, sn4);  // double-precision angles
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = wave + i * kMW;
+        if (r > GRP || (r == GRP && !owns_new)) continue;  // uniform per wave
+        const float4 y = norm_rope_row(px[i], pw[i], cs4, sn4, lane, ROT, a.eps);
+        if (r < GRP) {
+            qs[r >> 2][lane >> 2][r & 3][lane & 3] = y;  // dims 4 lane .. + 3 of head r
+        } else {
+            *reinterpret_cast<float4*>(a.k_cache + hoff + static_cast<int64_t>(pos) * kHD + lane * 4) = y;
+            ks[lane] = y;
+        }
+    }
+    if (owns_new && wave == 1) {
+        *reinterpret_cast<float4*>(a.v_cache + hoff + static_cast<int64_t>(pos) * kHD + lane * 4) = vn4;
+        vs[lane] = vn4;
+    }
+    // LDS-only barrier: the K / V tiles in flight are not waited for here
+    lds_barrier();
+
+    floatx4 O[2][4];  // [hg][c]: register i = O[4 hg + i][4 lane + c]
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[h][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};  // of heads jj + 4 hg
+
+    // rescale the accumulators of heads 4 hg + i by the factors f of lanes i (heads i + 4 hg)
+    auto rescale = [&](const float (&f)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float fh[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fh[i] = __shfl(f[h], i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[h][c][i] *= fh[i];
+        }
+    };
+
+    auto tile = [&](float4 (&kr)[16], int p0, auto more) {
+        floatx4 Sx[2][4];  // [hg][e]: eight independent accumulation chains
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Sx[h][e] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float4 k = kr[u];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float4 q = qs[h][u][jj][g];
+                Sx[h][0] = mfma4(k.x, q.x, Sx[h][0]);
+                Sx[h][1] = mfma4(k.y, q.y, Sx[h][1]);
+                Sx[h][2] = mfma4(k.z, q.z, Sx[h][2]);
+                Sx[h][3] = mfma4(k.w, q.w, Sx[h][3]);
+            }
+            // keep the Q operand reads close to their use (a few in flight, not all 32)
+            if ((u & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (decltype(more)::value) loadK(kr, p0 + TP);
+        // s[h][i]: position p0 + 4 pg + i, head 4 h + jj (the dim quarters summed)
+        float s[2][4], tm[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const floatx4 S = (Sx[h][0] + Sx[h][1]) + (Sx[h][2] + Sx[h][3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = dimq_sum(S[i]);
+                s[h][i] = p0 + 4 * pg + i < wl ? v * sc : -INFINITY;
+            }
+            tm[h] = pg_max(fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3])));
+        }
+        // the reference max moves only when a score exceeds it by more than 8 (the weights
+        // exp(s - m) stay below e^8, far from overflow), so the accumulators are rarely rescaled
+        float f[2], p[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float m_new = tm[h] > m_run[h] + 8.0f ? tm[h] : m_run[h];
+            f[h] = expf(m_run[h] - m_new);
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[h][i] = expf(s[h][i] - m_new);
+                ps += p[h][i];
+            }
+            l_run[h] = l_run[h] * f[h] + pg_sum(ps);
+            m_run[h] = m_new;
+        }
+        if (__any(f[0] != 1.0f || f[1] != 1.0f)) rescale(f);
+        // P to the A operand layout: the lanes of dim quarter 0 store their 4 positions of
+        // heads jj, jj + 4; every lane reads the 16 positions of its heads (same wave: LDS
+        // operations complete in order)
+        if (g == 0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) pl[wave][h][jj][pg] = make_float4(p[h][0], p[h][1], p[h][2], p[h][3]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        float4 pv[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) pv[h][t] = pl[wave][h][jj][t];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 v = vr[4 * t + e];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float pa = e == 0 ? pv[h][t].x : e == 1 ? pv[h][t].y : e == 2 ? pv[h][t].z : pv[h][t].w;
+                    O[h][0] = mfma4(pa, v.x, O[h][0]);
+                    O[h][1] = mfma4(pa, v.y, O[h][1]);
+                    O[h][2] = mfma4(pa, v.z, O[h][2]);
+                    O[h][3] = mfma4(pa, v.w, O[h][3]);
+                }
+            }
+        if constexpr (decltype(more)::value) loadV(p0 + TP);
+    };
+    int p0 = w0;
+    for (; p0 + TP < wl; p0 += TP) tile(kA, p0, std::true_type{});
+    if (p0 < wl) tile(kA, p0, std::false_type{});  // the last tile requests nothing more
+
+    if (has_new) {  // position pos: each lane's 4 dims for the 8 heads, then a halving butterfly
+        const float4 kn = ks[lane];
+        fvec<8> d;
+#pragma unroll
+        for (int h = 0; h < GRP; ++h) {
+            const float4 q = qs[h >> 2][lane >> 2][h & 3][lane & 3];
+            d[h] = ((q.x * kn.x + q.y * kn.y) + q.z * kn.z) + q.w * kn.w;
+        }
+        const float dh = butterfly<8, 32>(d, lane);  // head lane / 8 on every lane
+        float f[2], pn[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float sn = __shfl(dh, 8 * (jj + 4 * h)) * sc;
+            const float m_new = sn > m_run[h] + 8.0f ? sn : m_run[h];
+            f[h] = expf(m_run[h] - m_new);
+            pn[h] = expf(sn - m_new);
+            l_run[h] = l_run[h] * f[h] + pn[h];
+            m_run[h] = m_new;
+        }
+        rescale(f);
+        const float4 v = vs[lane];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float ph = __shfl(pn[h], i);
+                O[h][0][i] = fmaf(ph, v.x, O[h][0][i]);
+                O[h][1][i] = fmaf(ph, v.y, O[h][1][i]);
+                O[h][2][i] = fmaf(ph, v.z, O[h][2][i]);
+                O[h][3][i] = fmaf(ph, v.w, O[h][3][i]);
+            }
+    }
+
+    // ---- merge the waves: maxima first, then each wave rescales its own accumulators to the
+    // workgroup maximum and the four are summed in a fixed order
+    if (lane < 4) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            ml_s[wave][lane + 4 * h][0] = m_run[h];
+            ml_s[wave][lane + 4 * h][1] = l_run[h];
+        }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hd = 4 * h + i;
+            float M = ml_s[0][hd][0];
+#pragma unroll
+            for (int w = 1; w < kMW; ++w) M = fmaxf(M, ml_s[w][hd][0]);
+            const float w8 = m_run_of(ml_s[wave][hd][0], M);
+            *reinterpret_cast<float4*>(&os[wave][hd][4 * lane]) =
+                make_float4(O[h][0][i] * w8, O[h][1][i] * w8, O[h][2][i] * w8, O[h][3][i] * w8);
+        }
     lds_barrier();
     const int64_t base = (static_cast<int64_t>(kh) * a.n_splits + split) * GRP;
 #pragma unroll
@@ -941,8 +1197,8 @@ template <int GRP>
 hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
     if (GRP == 8 && a.ROT % 32 == 0 && a.ROT > 0 && !attn_force_valu()) {
         dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
-        if (a.kv_bf16) klaunch(attn_mfma_kernel<true>, grid, kMW * 64, 0, s, a);
-        else klaunch(attn_mfma_kernel<false>, grid, kMW * 64, 0, s, a);
+        if (a.kv_bf16) klaunch(attn_mfma_bf16_kernel, grid, kMW * 64, 0, s, a);
+        else klaunch(attn_mfma4_kernel, grid, kMW * 64, 0, s, a);
         return hipGetLastError();
     }
     constexpr int LPP = GRP <= 4 ? 16 : 32;
