@@ -466,6 +466,8 @@ def main() -> None:
                     help="prefill: projection GEMMs on three exact bf16 parts (no fp16 weight copies)")
     ap.add_argument("--no-prefill-line", action="store_true",
                     help="default decode run: skip the 4096-token prefill measured beside it")
+    ap.add_argument("--no-long-line", action="store_true",
+                    help="default decode run: skip the 131072-context decode measured beside it")
     ap.add_argument("--no-mixer-lines", action="store_true",
                     help="default decode run: skip the isolated GDN / attention mixers measured beside it")
     ap.add_argument("--calibration-copy", action="store_true",
@@ -483,10 +485,10 @@ def main() -> None:
             calibration_copy()
         print(json.dumps(result), flush=True)
         return
-    bench_decode(a)
+    print(json.dumps(bench_decode(a)), flush=True)
 
 
-def bench_decode(a) -> None:
+def bench_decode(a) -> dict:
     """The decode workloads: the 2B shape at --ctx positions of synthetic cache (default), the
     0.8B shape after a prompt (--model 0.8b), or the 2B shape at the end of a context the
     library plans itself (--workload long: KV arena sized by solve_max_context against the
@@ -647,6 +649,19 @@ def bench_decode(a) -> None:
             result["isolated_mixers"] = iso
         except Exception as e:  # the decode line stands on its own
             result["isolated_mixers"] = {"error": repr(e)}
+    if not (small or long_ctx) and not a.no_long_line:
+        # the same decode at the end of a 131072-position arena planned by solve_max_context
+        # (64 timed steps); `--workload long` gives the full line
+        try:
+            la = argparse.Namespace(**vars(a))
+            la.workload, la.steps, la.warmup, la.no_cpu_baseline, la.model_dir = "long", 64, 8, True, ""
+            la.calibration_copy = False
+            lr = bench_decode(la)
+            result["long_context"] = {"value": lr["value"], "unit": lr["unit"], "ms_per_step": lr["ms_per_step"],
+                                      "context": lr["config"]["context"], "max_context": lr["config"]["max_context"],
+                                      "roofline_attention": lr["roofline_attention"], "mixers": lr["mixers"]}
+        except Exception as e:  # the decode line stands on its own
+            result["long_context"] = {"error": repr(e)}
     if a.calibration_copy:
         calibration_copy()
     traffic_file = os.path.join(ROOT, "profiles", "decode_2b_8k_traffic.json")
@@ -660,7 +675,7 @@ def bench_decode(a) -> None:
         with stdout_to_stderr():
             result["cpu_baseline"] = (cpu_greedy_baseline(model_dir, d, ctx, a.cpu_steps) if small
                                       else cpu_baseline(model_dir, d, ctx, a.cpu_steps))
-    print(json.dumps(result), flush=True)
+    return result
 
 
 if __name__ == "__main__":
