@@ -315,12 +315,13 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
     __shared__ __align__(16) float Wl[2][kC][kLdW];
     __shared__ __align__(16) float Kt[2][kD][kLdKt];
     __shared__ __align__(16) float VNt[kSW][kLdV];
+    __shared__ __align__(16) float Ul[2][kC][kSW];  // the chunk's U entries of this slice
     float* S = a.state + static_cast<int64_t>(vh) * kD * kD;
     for (int i = tid; i < kD * kSW; i += kSThreads) St[i & 15][i >> 4] = S[(i >> 4) * kD + col0 + (i & 15)];
 
     constexpr int NF = kC * kD / 4 / 256;  // float4 of W (and of Kd) per staging thread: 8
-    floatx4 rw[NF], rk[NF];
-    auto load_chunk = [&](int c) {  // staging waves: the chunk's W and decayed K
+    floatx4 rw[NF], rk[NF], ru4;
+    auto load_chunk = [&](int c) {  // staging waves: the chunk's W, decayed K and U entries
         const int64_t row0 = static_cast<int64_t>(c) * kC;
         const float* W = a.W + (static_cast<int64_t>(vh) * a.Tp + row0) * kD;
         const float* Kd = a.Kd + (static_cast<int64_t>(vh) * nchunk + c) * kD * kC;
@@ -330,6 +331,8 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
             rw[i] = *reinterpret_cast<const floatx4*>(W + f * 4);
             rk[i] = *reinterpret_cast<const floatx4*>(Kd + f * 4);
         }
+        // U row st / 4, columns col0 + 4 (st % 4) .. + 3
+        ru4 = *reinterpret_cast<const floatx4*>(a.U + (static_cast<int64_t>(vh) * a.Tp + row0 + (st >> 2)) * kD + col0 + 4 * (st & 3));
     };
     auto store_chunk = [&](int b) {
 #pragma unroll
@@ -338,32 +341,61 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
             *reinterpret_cast<floatx4*>(&Wl[b][f >> 5][(f & 31) * 4]) = rw[i];
             *reinterpret_cast<floatx4*>(&Kt[b][f >> 4][(f & 15) * 4]) = rk[i];
         }
-    };
-    // v_new waves: this lane's U entries (rows 16 wave + 4 lg + v, column lr) of chunk c
-    float ru[4];
-    auto load_u = [&](int c) {
-        const float* U = a.U + (static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(c) * kC) * kD + col0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) ru[v] = U[(16 * (wave & 3) + 4 * lg + v) * kD + lr];
+        *reinterpret_cast<floatx4*>(&Ul[b][st >> 2][4 * (st & 3)]) = ru4;
     };
     // chunk 0 into buffer 0 (the staging waves), chunk 1 requested
     if (stager) {
         load_chunk(0);
         store_chunk(0);
         load_chunk(min(1, nchunk - 1));
-    } else {
-        load_u(0);
     }
-    float relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + kC - 1];
+    // e^(gamma_last) of each chunk through the constant address space: scalar loads, whose
+    // waits are on the scalar / LDS counter. (A vector load of it one chunk ahead made the
+    // loop's register copy wait for every vector load in flight -- the staged chunk too --
+    // at the end of each step.)
+    typedef __attribute__((address_space(4))) const float cfloat;
+    const cfloat* eg_last = reinterpret_cast<const cfloat*>(
+        reinterpret_cast<uintptr_t>(a.Eg + static_cast<int64_t>(vh) * a.Tp + kC - 1));
     __syncthreads();  // the state slice and chunk 0 are in LDS
     for (int i = tid; i < kD * kSW; i += kSThreads)
         a.Sc[static_cast<int64_t>(vh) * nchunk * kD * kD + (i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
-    for (int c = 0; c < nchunk; ++c) {
-        const int b = c & 1;
-        const float elast = relast;
-        if (!stager) {
+    // Phase 2 of chunk c: the new state rows [16 w, 16 w + 16) -- rows 16 w + 4 lg + v of
+    // column lr in this lane -- to LDS
+    auto phase2 = [&](int b, float elast) {
+        floatx4 sn = *reinterpret_cast<const floatx4*>(&St[lr][16 * wave + 4 * lg]);
+        sn = sn * elast;
+        floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 ka = *reinterpret_cast<const float4*>(&Kt[b][16 * wave + lr][16 * lg + 4 * q]);
+            const float4 vv = *reinterpret_cast<const float4*>(&VNt[lr][16 * lg + 4 * q]);
+            ch[0] = mfma4(ka.x, vv.x, ch[0]);
+            ch[1] = mfma4(ka.y, vv.y, ch[1]);
+            ch[0] = mfma4(ka.z, vv.z, ch[0]);
+            ch[1] = mfma4(ka.w, vv.w, ch[1]);
+        }
+        sn = sn + (ch[0] + ch[1]);
+        *reinterpret_cast<floatx4*>(&St[lr][16 * wave + 4 * lg]) = sn;
+    };
+    // The two roles run separate loops with the same barriers; the staging waves only load
+    // from memory and the v_new waves only store (v_new, and the chunk-start states from LDS),
+    // so no wait for a load one step old also waits for the stores issued since. (One loop
+    // with a branch per role made each step wait for the previous step's stores.)
+    if (!stager) {
+        const int vb = wave;
+        for (int c = 0; c < nchunk; ++c) {
+            const int b = c & 1;
+            const float elast = eg_last[static_cast<int64_t>(c) * kC];
+            if (c > 0) {  // the chunk-start state S_c (chunk 0's went out before the loop)
+                float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c) * kD * kD + col0;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int i = tid + 256 * j, row = i >> 2, q = 4 * (i & 3);  // 16 bytes of row `row`
+                    *reinterpret_cast<float4*>(Sc + row * kD + q) =
+                        make_float4(St[q][row], St[q + 1][row], St[q + 2][row], St[q + 3][row]);
+                }
+            }
             // v_new rows [16 w, 16 w + 16) over dims [0, 64) and [64, 128): four chains each
-            const int vb = wave;
             floatx4 part[2];
 #pragma unroll
             for (int kq = 0; kq < 2; ++kq) {
@@ -386,39 +418,26 @@ __global__ __launch_bounds__(kSThreads) void gdn_state_kernel(GdnPrefillArgs a) 
             floatx4 x;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                x[v] = ru[v] - (part[0][v] + part[1][v]);
+                x[v] = Ul[b][16 * vb + 4 * lg + v][lr] - (part[0][v] + part[1][v]);
                 U[(16 * vb + 4 * lg + v) * kD + lr] = x[v];
             }
             *reinterpret_cast<floatx4*>(&VNt[lr][16 * vb + 4 * lg]) = x;
-            load_u(min(c + 1, nchunk - 1));
-        } else if (c + 1 < nchunk) {
-            store_chunk(b ^ 1);                   // chunk c + 1, requested one step ago
-            load_chunk(min(c + 2, nchunk - 1));   // (the last chunk is requested again at the end)
+            lds_barrier();  // VNt and the next chunk's buffer written; every v_new read of St done
+            phase2(b, elast);
+            lds_barrier();  // the new state rows in LDS; every read of VNt and of buffer b done
         }
-        relast = a.Eg[static_cast<int64_t>(vh) * a.Tp + static_cast<int64_t>(min(c + 1, nchunk - 1)) * kC + kC - 1];
-        lds_barrier();  // VNt and the next chunk's buffer written; every v_new read of St done
-
-        // new state rows [16 w, 16 w + 16): rows 16 w + 4 lg + v of column lr in this lane
-        floatx4 sn = *reinterpret_cast<const floatx4*>(&St[lr][16 * wave + 4 * lg]);
-        sn = sn * elast;
-        floatx4 ch[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 ka = *reinterpret_cast<const float4*>(&Kt[b][16 * wave + lr][16 * lg + 4 * q]);
-            const float4 vv = *reinterpret_cast<const float4*>(&VNt[lr][16 * lg + 4 * q]);
-            ch[0] = mfma4(ka.x, vv.x, ch[0]);
-            ch[1] = mfma4(ka.y, vv.y, ch[1]);
-            ch[0] = mfma4(ka.z, vv.z, ch[0]);
-            ch[1] = mfma4(ka.w, vv.w, ch[1]);
+    } else {
+        for (int c = 0; c < nchunk; ++c) {
+            const int b = c & 1;
+            const float elast = eg_last[static_cast<int64_t>(c) * kC];
+            // chunk c + 1, requested one step ago, into the other buffer (after the last chunk:
+            // the last one again, into the buffer nothing reads any more)
+            store_chunk(b ^ 1);
+            load_chunk(min(c + 2, nchunk - 1));
+            lds_barrier();
+            phase2(b, elast);
+            lds_barrier();
         }
-        sn = sn + (ch[0] + ch[1]);
-        *reinterpret_cast<floatx4*>(&St[lr][16 * wave + 4 * lg]) = sn;
-        if (c + 1 < nchunk) {  // uniform
-            float* Sc = a.Sc + (static_cast<int64_t>(vh) * nchunk + c + 1) * kD * kD + col0 + lr;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) Sc[(16 * wave + 4 * lg + v) * kD] = sn[v];
-        }
-        lds_barrier();  // the new state rows in LDS; every read of VNt and of buffer b done
     }
     for (int i = tid; i < kD * kSW; i += kSThreads) S[(i >> 4) * kD + col0 + (i & 15)] = St[i & 15][i >> 4];
 }
