@@ -305,21 +305,46 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
         }
         return;
     }
+    // EPI 1: every residual value is requested before the first store. R may be Y itself, so
+    // a load placed after a store waits for that store's round trip (one per element, 64 in a
+    // row per lane); reading them all first keeps each element's read before its own write.
+    // (Rows and columns past the matrix read a clamped element and store nothing.)
+    float rv[kCB][2][4];
+    if constexpr (EPI == 1) {
 #pragma unroll
-    for (int j = 0; j < kCB; ++j) {
-        const int col = n0 + 16 * j + l16;
-        if (col >= a.N) continue;
+        for (int j = 0; j < kCB; ++j) {
+            const int col = min(n0 + 16 * j + l16, a.N - 1);
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
+            for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = rbase + 16 * r + v;
-                if (row < a.M) {
-                    float* y = a.Y + static_cast<int64_t>(row) * a.ldy + col;
-                    *y = EPI == 1 ? a.R[static_cast<int64_t>(row) * a.ldr + col] + acc[r][j][v] : acc[r][j][v];
+                for (int v = 0; v < 4; ++v) {
+                    const int row = min(rbase + 16 * r + v, a.M - 1);
+                    rv[j][r][v] = a.R[static_cast<int64_t>(row) * a.ldr + col];
                 }
-            }
+        }
     }
+    // a tile inside the matrix stores without per-element bounds checks (a store under a
+    // branch would also wait there for the stores before it)
+    auto store = [&](auto checked) {
+        constexpr bool CK = decltype(checked)::value;
+#pragma unroll
+        for (int j = 0; j < kCB; ++j) {
+            const int col = n0 + 16 * j + l16;
+            if (CK && col >= a.N) continue;
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = rbase + 16 * r + v;
+                    if (!CK || row < a.M) {
+                        float* y = a.Y + static_cast<int64_t>(row) * a.ldy + col;
+                        *y = EPI == 1 ? rv[j][r][v] + acc[r][j][v] : acc[r][j][v];
+                    }
+                }
+        }
+    };
+    if (m0 + kBM <= a.M && n0 + kBN <= a.N) store(std::false_type{});  // uniform
+    else store(std::true_type{});
 }
 
 template <int EPI, bool F16>
