@@ -135,14 +135,23 @@ __device__ __forceinline__ void load_rows(const GemvArgs& a, int r0, u32x4 (&w)[
     }
 }
 
-// Conv-window inputs of a wave's rows (kEpiConvSilu): the four taps and the raw inputs of the
-// three previous positions (ring slots (pos - 3..pos - 1) % 4), requested early so that the
-// epilogue does not wait for them.
+// Epilogue inputs of a wave's rows, requested with the rows' weights so that the epilogue
+// does not wait for them: the conv window (kEpiConvSilu: the four taps and the raw inputs of
+// the three previous positions, ring slots (pos - 3..pos - 1) % 4) or the residual
+// (kEpiResidual; y may be the residual itself, and each row is read here before its own
+// write).
 template <int RPW>
 struct ConvIn {
     float4 w[RPW];
     float r3[RPW], r2[RPW], r1[RPW];
+    float res[RPW];
 };
+
+template <int RPW>
+__device__ __forceinline__ void load_resid(const GemvArgs& a, int r0, ConvIn<RPW>& cv) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) cv.res[r] = a.resid[min(r0 + r, a.rows - 1)];
+}
 
 template <int RPW>
 __device__ __forceinline__ void load_conv(const GemvArgs& a, int r0, int pos, ConvIn<RPW>& cv) {
@@ -206,7 +215,7 @@ __device__ __forceinline__ void store_rows(const GemvArgs& a, int r0, const floa
     } else {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
-            if (r0 + r < a.rows) a.y[r0 + r] = EPI == kEpiResidual ? a.resid[r0 + r] + sum[r] : sum[r];
+            if (r0 + r < a.rows) a.y[r0 + r] = EPI == kEpiResidual ? cv.res[r] + sum[r] : sum[r];
     }
 }
 
@@ -404,6 +413,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     load_rows<RPW, KC>(a, r0, pf);  // rows clamped: unconditional, see load_input
     ConvIn<RPW> cv;
     if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+    if (EPI == kEpiResidual) load_resid<RPW>(a, r0, cv);
     if (NX > 0) finish_input<PRO>(a, erow, xv, xe, gv, wv, xs);
     else stage_input<PRO>(a, erow, xs);
     float bv = -INFINITY;  // argmax partial of this wave's rows (amax_part)
@@ -417,11 +427,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 if (r0 >= a.rows) break;
                 load_rows<RPW, KC>(a, r0, pf);
                 if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+                if (EPI == kEpiResidual) load_resid<RPW>(a, r0, cv);
             }
         } else {
             row_group<EPI, RPW, KC, true>(a, xs, r0, pf, cv, pos, bv, bi);
             for (r0 += row_step; r0 < a.rows; r0 += row_step) {
                 if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
+                if (EPI == kEpiResidual) load_resid<RPW>(a, r0, cv);
                 row_group<EPI, RPW, KC, false>(a, xs, r0, pf, cv, pos, bv, bi);
             }
         }
