@@ -394,8 +394,23 @@ __device__ __forceinline__ void finish_input(const GemvArgs& a, const uint16_t* 
     lds_barrier();
 }
 
+// The fields the first loads need come first as separate arguments: the library is built
+// with kernarg preloading for them (k_gemv's build line), so the CP hands them over in
+// SGPRs at wave launch and the input and weight loads do not wait for a kernarg load.
 template <int PRO, int EPI, int RPW, int NX, int KC>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* W, const float* x, const float* norm_w,
+                                                   const float* gate, const uint16_t* embed, int rows,
+                                                   GemvArgs a) {
+    a.W = W;
+    a.x = x;
+    a.norm_w = norm_w;
+    a.gate = gate;
+    a.embed = embed;
+    a.rows = rows;
+    // constants of this instantiation (the dispatch picks KC = in_dim / 512, and register
+    // staging of the gated norm only for 128-wide heads)
+    if (KC > 0) a.in_dim = KC * 512;
+    if (PRO == kProGatedNorm && NX > 0) a.head_dim = 128;
     extern __shared__ float xs[];
     const int wave = threadIdx.x >> 6;
     const int row_step = gridDim.x * 4 * RPW;
@@ -411,6 +426,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     // while the prologue works.
     u32x4 pf[pf_chunks(KC)][RPW];
     load_rows<RPW, KC>(a, r0, pf);  // rows clamped: unconditional, see load_input
+    // nothing after this point is scheduled before the weight loads (a wait for a kernarg
+    // loaded later, e.g. the residual's pointer, would hold them back)
+    __builtin_amdgcn_sched_barrier(0);
     ConvIn<RPW> cv;
     if (EPI == kEpiConvSilu) load_conv<RPW>(a, r0, pos, cv);
     if (EPI == kEpiResidual) load_resid<RPW>(a, r0, cv);
@@ -475,8 +493,12 @@ template <int PRO, int EPI, int NX, int KC>
 hipError_t launch_kc(const GemvArgs& a, hipStream_t s) {
     const size_t lds = static_cast<size_t>(a.in_dim + 4) * sizeof(float);  // + the spare slot
     const int blocks = gemv_blocks(a, EPI);
-    if (gemv_two_rows(a.rows, EPI)) klaunch(gemv_kernel<PRO, EPI, 2, NX, KC>, blocks, 256, lds, s, a);
-    else klaunch(gemv_kernel<PRO, EPI, 1, NX, KC>, blocks, 256, lds, s, a);
+    if (gemv_two_rows(a.rows, EPI))
+        klaunch(gemv_kernel<PRO, EPI, 2, NX, KC>, blocks, 256, lds, s, a.W, a.x, a.norm_w, a.gate, a.embed, a.rows,
+                a);
+    else
+        klaunch(gemv_kernel<PRO, EPI, 1, NX, KC>, blocks, 256, lds, s, a.W, a.x, a.norm_w, a.gate, a.embed, a.rows,
+                a);
     return hipGetLastError();
 }
 
