@@ -223,9 +223,16 @@ __device__ __forceinline__ float rowgroup_sum(float v) {
 // channels each, a double-precision wave sum) and scales its own 16 rows. 3.5 us per layer
 // against 4.0 us for the workgroup kernel with its five LDS barriers, same results to fp32
 // rounding.
-__global__ __launch_bounds__(64) void gdn_wave_kernel(GdnDecodeArgs a) {
+// The pointers and head counts the first loads need come first as separate arguments,
+// preloaded into SGPRs at wave launch (k_gdn's build line); the per-layer strides are read
+// only by launches of more than one layer.
+__global__ __launch_bounds__(64) void gdn_wave_kernel(float* state, const float* qkv_in, const float* b_in,
+                                                      const float* a_in, const float* A_log_in,
+                                                      const float* dt_bias_in, int VH, int KH, GdnDecodeArgs a) {
     constexpr int CW = 32, RR = 16;
     const int lane = threadIdx.x;
+    a.VH = VH;
+    a.KH = KH;
     const int rg = lane >> 3, cq = lane & 7;
     // workgroups go to the 8 XCDs in turn: with VH a multiple of 8 the four slices of a head
     // get ids of one residue mod 8, so one L2 fetches the head's q / k rows for all four
@@ -241,13 +248,18 @@ __global__ __launch_bounds__(64) void gdn_wave_kernel(GdnDecodeArgs a) {
     const int layer = blockIdx.y;
     const int rep = a.VH / a.KH, kh = vh / rep;
     const int KD = a.KH * kD;
-    const float* qkv = a.qkv + layer * a.ls_qkv;
-    const float* bin = a.b + layer * a.ls_ba;
-    const float* ain = a.a + layer * a.ls_ba;
-    const float* A_log = a.A_log + layer * a.ls_vh;
-    const float* dt_bias = a.dt_bias + layer * a.ls_vh;
-    float* S = a.state + layer * a.ls_state + static_cast<int64_t>(vh) * kD * kD;
-    float* out = a.out + layer * a.ls_out;
+    const float *qkv = qkv_in, *bin = b_in, *ain = a_in, *A_log = A_log_in, *dt_bias = dt_bias_in;
+    float* out = a.out;
+    if (layer > 0) {  // uniform
+        qkv += layer * a.ls_qkv;
+        bin += layer * a.ls_ba;
+        ain += layer * a.ls_ba;
+        A_log += layer * a.ls_vh;
+        dt_bias += layer * a.ls_vh;
+        state += layer * a.ls_state;
+        out += layer * a.ls_out;
+    }
+    float* S = state + static_cast<int64_t>(vh) * kD * kD;
     const int col0 = split * CW + 4 * cq;
 
     // inputs first, then the state slice (loads complete in order for the wait counter)
@@ -343,7 +355,8 @@ hipError_t launch_gdn_decode(const GdnDecodeArgs& in, bool fuse_norm, hipStream_
     if (!a.ls_state) a.ls_state = static_cast<int64_t>(a.VH) * kD * kD;
     if (!a.ls_out) a.ls_out = VD;
     if (a.conv_done && !fuse_norm) {  // the model's decode step
-        klaunch(gdn_wave_kernel, dim3(a.VH * 4, a.n_layers), 64, 0, s, a);
+        klaunch(gdn_wave_kernel, dim3(a.VH * 4, a.n_layers), 64, 0, s, a.state, a.qkv, a.b, a.a, a.A_log, a.dt_bias,
+                a.VH, a.KH, a);
         return hipGetLastError();
     }
     if (fuse_norm) {
