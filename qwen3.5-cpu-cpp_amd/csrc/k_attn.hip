@@ -38,6 +38,24 @@ __device__ __forceinline__ int read_pos(const AttnDecodeArgs& a) {
     return a.pos_dev ? *a.pos_dev : a.pos_val;
 }
 
+// The matrix-core decode kernels take the position and the pointers of their first loads as
+// leading arguments, preloaded into SGPRs at wave launch (k_attn's build line): the
+// position (device pointer and value), the query rows, the appended key / value and the two
+// norm weights; they request the query-side rows before anything that depends on the
+// position. The combine takes the position, the partials, the gate rows and the split and
+// head counts.
+__device__ __forceinline__ void set_lead(AttnDecodeArgs& a, const int* pos_dev, int pos_val, const float* qg,
+                                         const float* k_new, const float* v_new, const float* q_norm,
+                                         const float* k_norm) {
+    a.pos_dev = pos_dev;
+    a.pos_val = pos_val;
+    a.qg = qg;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+}
+
 __device__ __forceinline__ int split_len(int n, int n_splits) { return (n + n_splits - 1) / n_splits; }
 
 // Reduce GRP per-lane partial sums over groups of LPP lanes. On return lane l holds in v[0]
@@ -492,8 +510,14 @@ __device__ __forceinline__ float m_run_of(float mw, float M) { return mw == -INF
 // positions: S = K.Q^T on the 16x16x32 bf16 matrix cores against the three exact bf16 parts
 // of Q, O += P.V on the 16x16x16 bf16 cores with the three exact parts of P (every bf16 x bf16
 // product is exact in fp32); online softmax per head; waves merged once at the end.
-__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(AttnDecodeArgs a) {
-    attn_select_layer(a, blockIdx.z);
+// ML: several layers in one launch (grid.z); a single-layer launch reads no layer strides
+template <bool ML>
+__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(const int* pos_dev, int pos_val, const float* qg,
+                                                            const float* k_new, const float* v_new,
+                                                            const float* q_norm, const float* k_norm,
+                                                            AttnDecodeArgs a) {
+    set_lead(a, pos_dev, pos_val, qg, k_new, v_new, q_norm, k_norm);
+    if (ML) attn_select_layer(a, blockIdx.z);
     using KV = KvBf16;
     using KT = typename KV::T;
     constexpr int GRP = 8, TP = 16;
@@ -501,7 +525,28 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(AttnDecodeA
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop bounds
     const int n16 = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, kh = blockIdx.y;
+    // the query-side rows first (rows of this wave: q heads wave, wave + 4, and row 8 the
+    // appended key); they do not depend on the position
+    float4 px[3], pw[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
+        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
+                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
+        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
+        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
+    }
+    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    // the kernarg fields the K / V addresses need, requested now (with the position below
+    // they arrive in one round trip); nothing below is scheduled before the loads above (a
+    // wait for a kernarg field would hold them back)
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    float *const kcache = a.k_cache, *const vcache = a.v_cache;
+    const int ROT = a.ROT, half = ROT / 2;
+    __builtin_amdgcn_sched_barrier(0);
     const int pos = read_pos(a);
+    // (the fields are requested with the position, not after the split check below)
+    asm volatile("" ::"s"(hoff), "s"(kcache), "s"(vcache), "s"(ROT));
     const int n = pos + 1;
     const int per = split_len(n, a.n_splits);
     const int j0 = split * per;
@@ -515,9 +560,8 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(AttnDecodeA
     const bool has_new = owns_new && w0 < w1 && w1 == n;  // empty waves also end at n
     const int wl = has_new ? w1 - 1 : w1;
 
-    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
-    const float* Kc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.k_cache) + hoff);
-    const float* Vc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(a.v_cache) + hoff);
+    const float* Kc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(kcache) + hoff);
+    const float* Vc_ = reinterpret_cast<const float*>(reinterpret_cast<const uint16_t*>(vcache) + hoff);
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
     __shared__ float4 qs[16][64];             // Q in fp32 (the appended row's score): [c][lane]
@@ -528,19 +572,9 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma_bf16_kernel(AttnDecodeA
     __shared__ float os[kMW][GRP][kHD];
     __shared__ float ml_s[kMW][GRP][2];
 
-    // ---- prologue loads first (rows of this wave: q heads wave, wave + 4; the key on wave
-    // 0 and the value on wave 1 of the workgroup holding pos), then the first K / V tiles
-    const int ROT = a.ROT, half = ROT / 2;
-    float4 px[3], pw[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
-        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
-                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
-        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
-        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
-    }
-    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    // ---- prologue (the rows requested above: q heads wave, wave + 4 of this wave, the key
+    // on wave 0 and the value on wave 1 of the workgroup holding pos): the RoPE table row,
+    // then the first K / V tiles
     const int ci = (lane * 4) % max(half, 4);  // table column of this lane's first dim
     float4 cs4 = make_float4(1.f, 1.f, 1.f, 1.f), sn4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (a.rope_cs) {
@@ -839,14 +873,40 @@ __device__ __forceinline__ float pg_sum(float v) {
     return v + dpp_f<0x128>(v);
 }
 
-__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(AttnDecodeArgs a) {
-    attn_select_layer(a, blockIdx.z);
+template <bool ML>
+__global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(const int* pos_dev, int pos_val, const float* qg,
+                                                            const float* k_new, const float* v_new,
+                                                            const float* q_norm, const float* k_norm,
+                                                            AttnDecodeArgs a) {
+    set_lead(a, pos_dev, pos_val, qg, k_new, v_new, q_norm, k_norm);
+    if (ML) attn_select_layer(a, blockIdx.z);
     constexpr int GRP = 8, TP = 16;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loop bounds
     const int n16 = lane & 15, g = lane >> 4, jj = lane & 3, pg = (lane >> 2) & 3;
     const int split = blockIdx.x, kh = blockIdx.y;
+    // the query-side rows first (rows of this wave: q heads wave, wave + 4, and row 8 the
+    // appended key); they do not depend on the position
+    float4 px[3], pw[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
+        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
+                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
+        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
+        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
+    }
+    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    // the kernarg fields the K / V addresses need, requested now (with the position below
+    // they arrive in one round trip); nothing below is scheduled before the loads above (a
+    // wait for a kernarg field would hold them back)
+    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
+    float *const kcache = a.k_cache, *const vcache = a.v_cache;
+    const int ROT = a.ROT, half = ROT / 2;
+    __builtin_amdgcn_sched_barrier(0);
     const int pos = read_pos(a);
+    // (the fields are requested with the position, not after the split check below)
+    asm volatile("" ::"s"(hoff), "s"(kcache), "s"(vcache), "s"(ROT));
     const int n = pos + 1;
     const int per = split_len(n, a.n_splits);
     const int j0 = split * per;
@@ -860,9 +920,8 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(AttnDecodeArgs 
     const bool has_new = owns_new && w0 < w1 && w1 == n;  // empty waves also end at n
     const int wl = has_new ? w1 - 1 : w1;
 
-    const int64_t hoff = static_cast<int64_t>(kh) * a.max_ctx * kHD;  // elements
-    const float* Kc = a.k_cache + hoff;
-    const float* Vc = a.v_cache + hoff;
+    const float* Kc = kcache + hoff;
+    const float* Vc = vcache + hoff;
     const float sc = 1.0f / sqrtf(static_cast<float>(kHD));
 
     __shared__ float4 qs[2][16][4][4];       // Q operand: [hg][u][j][g] = Q[4 hg + j][16 u + 4 g .. + 3]
@@ -871,19 +930,9 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(AttnDecodeArgs 
     __shared__ float os[kMW][GRP][kHD];
     __shared__ float ml_s[kMW][GRP][2];
 
-    // ---- prologue loads first (rows of this wave: q heads wave, wave + 4; the key on wave
-    // 0 and the value on wave 1 of the workgroup holding pos), then the first K / V tiles
-    const int ROT = a.ROT, half = ROT / 2;
-    float4 px[3], pw[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int r = min(wave + i * kMW, GRP);  // row 8 = the new key
-        const float* src = r < GRP ? a.qg + static_cast<int64_t>(kh * GRP + r) * 2 * kHD
-                                   : a.k_new + static_cast<int64_t>(kh) * kHD;
-        px[i] = *reinterpret_cast<const float4*>(src + lane * 4);
-        pw[i] = *reinterpret_cast<const float4*>((r < GRP ? a.q_norm : a.k_norm) + lane * 4);
-    }
-    const float4 vn4 = *reinterpret_cast<const float4*>(a.v_new + static_cast<int64_t>(kh) * kHD + lane * 4);
+    // ---- prologue (the rows requested above: q heads wave, wave + 4 of this wave, the key
+    // on wave 0 and the value on wave 1 of the workgroup holding pos): the RoPE table row,
+    // then the first K / V tiles
     const int ci = (lane * 4) % max(half, 4);  // table column of this lane's first dim
     float4 cs4 = make_float4(1.f, 1.f, 1.f, 1.f), sn4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (a.rope_cs) {
@@ -1125,7 +1174,16 @@ __global__ __launch_bounds__(kMW * 64, 2) void attn_mfma4_kernel(AttnDecodeArgs 
 // 32 w .. 32 w + 31 on wave w -- so the merge waits for one memory round trip; the maximum
 // and the split weights exp(m_s - M) go through LDS. Past 128 (o rows) or 256 ((m, l)
 // pairs) active splits further passes follow.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a) {
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int* pos_dev, const float* part_ml,
+                                                           const float* part_o, const float* qg, int n_splits,
+                                                           int NQ, int NKV, AttnDecodeArgs a) {
+    a.pos_dev = pos_dev;
+    a.part_ml = const_cast<float*>(part_ml);
+    a.part_o = const_cast<float*>(part_o);
+    a.qg = qg;
+    a.n_splits = n_splits;
+    a.NQ = NQ;
+    a.NKV = NKV;
     attn_select_layer(a, blockIdx.z);
     constexpr int kRW = 32;  // o rows per wave per pass
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1197,8 +1255,12 @@ template <int GRP>
 hipError_t launch_partial_grp(const AttnDecodeArgs& a, hipStream_t s) {
     if (GRP == 8 && a.ROT % 32 == 0 && a.ROT > 0 && !attn_force_valu()) {
         dim3 grid(a.n_splits, a.NKV, a.n_layers > 0 ? a.n_layers : 1);
-        if (a.kv_bf16) klaunch(attn_mfma_bf16_kernel, grid, kMW * 64, 0, s, a);
-        else klaunch(attn_mfma4_kernel, grid, kMW * 64, 0, s, a);
+        auto go = [&](auto k) {
+            klaunch(k, grid, kMW * 64, 0, s, a.pos_dev, a.pos_val, a.qg, a.k_new, a.v_new, a.q_norm, a.k_norm, a);
+        };
+        const bool ml = grid.z > 1;
+        if (a.kv_bf16) ml ? go(attn_mfma_bf16_kernel<true>) : go(attn_mfma_bf16_kernel<false>);
+        else ml ? go(attn_mfma4_kernel<true>) : go(attn_mfma4_kernel<false>);
         return hipGetLastError();
     }
     constexpr int LPP = GRP <= 4 ? 16 : 32;
@@ -1241,7 +1303,7 @@ int device_cu_count() {
 
 hipError_t launch_attn_combine(const AttnDecodeArgs& a, hipStream_t s) {
     dim3 grid(a.NQ, kHD / 64, a.n_layers > 0 ? a.n_layers : 1);
-    klaunch(attn_combine_kernel, grid, 256, 0, s, a);
+    klaunch(attn_combine_kernel, grid, 256, 0, s, a.pos_dev, a.part_ml, a.part_o, a.qg, a.n_splits, a.NQ, a.NKV, a);
     return hipGetLastError();
 }
 
