@@ -31,7 +31,9 @@ size_t dtype_size(const std::string& dt) {
 // n elements of a BF16 or F32 tensor as fp32 (bf16 is the upper half of an fp32: exact).
 bool widen(const std::string& dt, const void* src, int64_t n, float* dst) {
     if (dt == "F32") {
-        std::memcpy(dst, src, static_cast<size_t>(n) * 4);
+        // (no copy of an empty tensor: dst may then be null; a shape-less entry has 0
+        // elements, as numel() defines it)
+        if (n > 0) std::memcpy(dst, src, static_cast<size_t>(n) * 4);
         return true;
     }
     if (dt == "BF16") {
