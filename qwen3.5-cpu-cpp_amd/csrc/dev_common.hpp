@@ -105,6 +105,24 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // silu(x) = x / (1 + e^-x), sigmoid, softplus with the > 20 pass-through.
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// Two-part fp16 form of the prefill GEMM's activations, shared by the GEMM and the kernels
+// that write its input already split: the power-of-two exponent that brings a row whose
+// largest |x| is mx into [2^14, 2^15) (0 for a zero or non-finite maximum), and for two
+// values (already scaled) h = fp16(x), l = fp16(x - h), each pair packed low value first.
+__device__ __forceinline__ int split_row_exp(float mx) {
+    int ex = 0;
+    (void)frexpf(mx, &ex);
+    return mx > 0.0f && mx < INFINITY ? min(max(15 - ex, -100), 100) : 0;
+}
+typedef _Float16 split_h2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split2h_pair(float a, float b, uint32_t& h, uint32_t& l) {
+    const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+    const _Float16 la = static_cast<_Float16>(a - static_cast<float>(ha));
+    const _Float16 lb = static_cast<_Float16>(b - static_cast<float>(hb));
+    h = __builtin_bit_cast(uint32_t, split_h2_t{ha, hb});
+    l = __builtin_bit_cast(uint32_t, split_h2_t{la, lb});
+}
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 

@@ -65,7 +65,6 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128, kBN = 128, kBK = 32;
@@ -85,20 +84,14 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& h, uint3
 }
 
 // the two fp16 parts of two (scaled) floats a, b: h = rn(x), l = rn(x - h), each pair packed
-__device__ __forceinline__ void split2h_pair(float a, float b, uint32_t& h, uint32_t& l) {
-    const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
-    const _Float16 la = static_cast<_Float16>(a - static_cast<float>(ha));
-    const _Float16 lb = static_cast<_Float16>(b - static_cast<float>(hb));
-    h = __builtin_bit_cast(uint32_t, half2_t{ha, hb});
-    l = __builtin_bit_cast(uint32_t, half2_t{la, lb});
-}
-
 // One 128 x 128 tile. MASK: some W rows of the tile lie past N or K is not a whole number of
 // flush blocks, so W and X chunks past N or K are zeroed (X rows past M are clamped to row 0
 // and their outputs dropped).
 // EPI: 0 store, 1 add the residual, 2 SwiGLU of interleaved (gate, up) column pairs.
 // F16: two fp16 parts per activation against the fp16 weight copy (see launch_gemm).
-template <int EPI, bool MASK, bool F16>
+// XP (with F16): X already split by its producer (x_planes, the layout of xp_off): the two
+// parts are loaded as the operands themselves, nothing is split here.
+template <int EPI, bool MASK, bool F16, bool XP>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uint16_t (*Ws)[kLd]) {
     using OpT = typename std::conditional<F16, halfx8, bf16x8>::type;
     constexpr int NP = F16 ? 2 : 3;  // parts per activation
@@ -111,9 +104,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
     for (int r = 0; r < 2; ++r) {
         const int row = m0 + wave * 32 + 16 * r + l16;
         arow_i[r] = row < a.M ? row : 0;
-        // F16 (tiled X): the lane's 16 bytes in the first k block of its row block
-        arow[r] = F16 ? a.X + static_cast<int64_t>((m0 >> 4) + 2 * wave + r) * (a.K >> 5) * 512 + (l16 << 4) +
-                            ((lane >> 4) << 2)
+        // F16 (tiled X): the lane's 16 bytes in the first k block of its row block (XP: of the
+        // high part; the low part's are 1 KB further, where the tiled fp32 layout has the
+        // second 16 bytes)
+        arow[r] = F16 ? a.X + static_cast<int64_t>((m0 >> 4) + 2 * wave + r) * (a.K >> 5) * 512 +
+                            (XP ? lane << 2 : (l16 << 4) + ((lane >> 4) << 2))
                       : a.X + static_cast<int64_t>(arow_i[r]) * a.ldx;
     }
     // F16: each row's scale 2^xe, xe = 15 - (exponent of its maximum |x| as in frexp), so
@@ -127,9 +122,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
             for (int j = lane >> 4; j < a.xmax_n; j += 4) mx = fmaxf(mx, a.xmax[static_cast<int64_t>(arow_i[r]) * a.xmax_n + j]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            int ex = 0;
-            (void)frexpf(mx, &ex);
-            xe[r] = mx > 0.0f && mx < INFINITY ? min(max(15 - ex, -100), 100) : 0;
+            xe[r] = split_row_exp(mx);
             xs[r] = ldexpf(1.0f, xe[r]);
         }
     }
@@ -178,6 +171,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
             if constexpr (MASK) {  // k past K: zeros (the clamped values could be infinite)
                 if (k0 + kq >= a.K) x0 = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (k0 + kq + 4 >= a.K) x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if constexpr (XP) {  // the parts as stored (k past K: zeros, as below)
+                const bool live = !MASK || k0 < a.K;
+                aop[r][0] = __builtin_bit_cast(OpT, live ? xa[r][0] : make_uint4(0u, 0u, 0u, 0u));
+                aop[r][1] = __builtin_bit_cast(OpT, live ? xa[r][1] : make_uint4(0u, 0u, 0u, 0u));
+                continue;
             }
             if constexpr (F16) {
                 const float sc = xs[r];
@@ -353,7 +352,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, int tx, int ty, uin
     else store(std::true_type{});
 }
 
-template <int EPI, bool F16>
+template <int EPI, bool F16, bool XP = false>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     __shared__ __align__(16) uint16_t Ws[2 * kBN][kLd];
     // tile (tx, ty) of workgroup L = x + X y (dispatch order): with a ragged last column
@@ -372,8 +371,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     }
     // tiles whose W rows all lie inside N (with whole flush blocks of K) store W unmasked
     const bool full = (tx + 1) * kBN <= a.N && a.K % (kFlush * kBK) == 0;
-    if (full) gemm_tile<EPI, false, F16>(a, tx, ty, Ws);
-    else gemm_tile<EPI, true, F16>(a, tx, ty, Ws);
+    if (full) gemm_tile<EPI, false, F16, XP>(a, tx, ty, Ws);
+    else gemm_tile<EPI, true, F16, XP>(a, tx, ty, Ws);
 }
 
 }  // namespace
@@ -383,7 +382,12 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     const bool f16 = a.Wh && a.xmax && a.xmax_n > 0 && a.x_tiled && a.K % 32 == 0;
     // the tiled layouts exist on the two-part path only (Y: its SwiGLU output)
     if ((a.x_tiled && !f16) || (a.y_tiled && !(f16 && a.swiglu && (a.N / 2) % 32 == 0))) return hipErrorInvalidValue;
-    if (f16) {
+    if (a.x_planes && !(f16 && a.xmax_n == 1)) return hipErrorInvalidValue;  // the producer's one row maximum
+    if (f16 && a.x_planes) {
+        if (a.swiglu) klaunch(gemm_kernel<2, true, true>, grid, 256, 0, s, a);
+        else if (a.R) klaunch(gemm_kernel<1, true, true>, grid, 256, 0, s, a);
+        else klaunch(gemm_kernel<0, true, true>, grid, 256, 0, s, a);
+    } else if (f16) {
         if (a.swiglu) klaunch(gemm_kernel<2, true>, grid, 256, 0, s, a);
         else if (a.R) klaunch(gemm_kernel<1, true>, grid, 256, 0, s, a);
         else klaunch(gemm_kernel<0, true>, grid, 256, 0, s, a);

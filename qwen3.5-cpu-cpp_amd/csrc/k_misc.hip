@@ -45,7 +45,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
 
 // The same for rows of n = 256 NV4 floats, one row per wave: the row stays in registers
 // between the sum of squares (double, reduced across the wave) and the scaling, so it is
-// read once, and no block barrier is needed.
+// read once, and no block barrier is needed. y_tiled == 2: the scaled row also stays in
+// registers until its maximum is known, then goes out split for the two-part GEMM (scale
+// 2^split_row_exp(max), fp16 high and low parts in the layout of xp_off) -- the split the
+// GEMM would otherwise redo for every 128-column tile of its output.
 template <int NV4>
 __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const float* w, float* y,
                                                                 int rows, float eps, int gated,
@@ -78,13 +81,31 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
             o = make_float4(v[i].x * inv * (1.0f + w4.x), v[i].y * inv * (1.0f + w4.y), v[i].z * inv * (1.0f + w4.z),
                             v[i].w * inv * (1.0f + w4.w));
         }
-        *reinterpret_cast<float4*>(y + (y_tiled ? xt_off(row, c, n) : off + c)) = o;
+        if (y_tiled != 2) *reinterpret_cast<float4*>(y + (y_tiled ? xt_off(row, c, n) : off + c)) = o;
+        v[i] = o;
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
     }
-    if (ymax) {  // uniform
-        mx = wave_max(mx);
-        if (lane == 0) ymax[row] = mx;
+    if (ymax || y_tiled == 2) mx = wave_max(mx);  // uniform
+    if (y_tiled == 2) {
+        const float sc = ldexpf(1.0f, split_row_exp(mx));
+        uint16_t* yh = reinterpret_cast<uint16_t*>(y);
+        const bool odd = lane & 1;
+#pragma unroll
+        for (int i = 0; i < NV4; ++i) {
+            // 4 consecutive k: lanes 2m and 2m + 1 hold one 8-k group, which the even lane
+            // stores as its 16 bytes of high parts and the odd lane as its 16 bytes of low
+            // parts, after trading the halves they do not store
+            const int c = (64 * i + lane) * 4;
+            uint32_t h0, l0, h1, l1;
+            split2h_pair(v[i].x * sc, v[i].y * sc, h0, l0);
+            split2h_pair(v[i].z * sc, v[i].w * sc, h1, l1);
+            const uint32_t r0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(odd ? h0 : l0), 1));
+            const uint32_t r1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(odd ? h1 : l1), 1));
+            const uint4 q = odd ? make_uint4(r0, r1, l0, l1) : make_uint4(h0, h1, r0, r1);
+            *reinterpret_cast<uint4*>(yh + xp_off(row, c & ~7, n, odd ? 1 : 0)) = q;
+        }
     }
+    if (ymax && lane == 0) ymax[row] = mx;
 }
 
 // x *= 1 / sqrt(sum(x^2) + eps), in place, one block per row.
@@ -260,6 +281,10 @@ int grid_for(int64_t n) {
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
                                float eps, int gated, const float* gate, hipStream_t s, float* ymax, int y_tiled) {
     if (y_tiled && n % 32 != 0) return hipErrorInvalidValue;
+    // the split form comes from the one-row-per-wave kernels only
+    if (y_tiled == 2 && (!ymax || !rmsnorm_rows_splits(n) || ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                                               reinterpret_cast<uintptr_t>(y)) & 15) != 0 || gated))
+        return hipErrorInvalidValue;
     const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                          reinterpret_cast<uintptr_t>(y) | (gated ? reinterpret_cast<uintptr_t>(gate) : 0);
     const int wb = (rows + 3) / 4;

@@ -104,6 +104,9 @@ struct GemmArgs {
     // X (two-part path) and, for SwiGLU, Y in the tiled layout of xt_off (ldx / ldy unused;
     // rows padded to a multiple of 128, K to a multiple of 32)
     int x_tiled = 0, y_tiled = 0;
+    // X already split (two-part path, x_tiled): X holds the fp16 parts of each row scaled by
+    // 2^split_row_exp(row maximum of xmax) in the split-plane layout of xp_off
+    int x_planes = 0;
 };
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Tiled activation layout of the two-part GEMM's X operand: blocks of 16 rows x 32 k
@@ -115,6 +118,16 @@ __host__ __device__ inline int64_t xt_off(int64_t row, int k, int K) {
            (((k & 31) >> 3) << 2) + (k & 3);
 }
 inline int64_t rows_tiled(int64_t rows) { return (rows + 127) / 128 * 128; }
+// Split-plane layout of the two-part GEMM's X operand (x_planes), in fp16 elements: the same
+// blocks of 16 rows x 32 k as xt_off and the same 2 KB each, holding the 512 high parts and
+// then the 512 low parts, each as [k / 8][row % 16][k % 8]: lane l of a wave-wide 16-byte
+// load reads the 16 bytes at 16 l, its matrix-core operand (row l % 16, k = 8 (l / 16) .. + 7).
+// (Rows kept whole, [row % 16][k / 8][k % 8], made the producer's stores contiguous and the
+// GEMM's loads scattered over four 64-byte pieces per lane quad: 0.25% slower overall.)
+__host__ __device__ inline int64_t xp_off(int64_t row, int k, int K, int part) {
+    return ((row >> 4) * (K >> 5) + (k >> 5)) * 1024 + part * 512 + (((k & 31) >> 3) << 7) + ((row & 15) << 3) +
+           (k & 7);
+}
 // Column tiles of the GEMM (the ymax row width)
 inline int gemm_col_tiles(int N) { return (N + 127) / 128; }
 // max |w| over n bf16 weights, into *out (a uint zeroed beforehand: the bits of the
@@ -267,9 +280,12 @@ hipError_t launch_embed_rows(const uint16_t* embed, const int* ids, float* hidde
 // y = W x with fp32 weights [rows][n], any n
 hipError_t launch_matvec_f32(const float* W, const float* x, float* y, int rows, int n, hipStream_t s);
 // ymax (may be null): the maximum |y| of each row
+// y_tiled: 0 row-major, 1 the tiled layout of xt_off, 2 split already for the two-part GEMM
+// (the layout of xp_off; needs ymax, and n with rmsnorm_rows_splits(n))
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* y, int rows, int n,
                                float eps, int gated, const float* gate, hipStream_t s, float* ymax = nullptr,
                                int y_tiled = 0);
+inline bool rmsnorm_rows_splits(int n) { return n == 1024 || n == 2048 || n == 4096; }
 hipError_t launch_l2norm_rows(float* x, int rows, int n, float eps, hipStream_t s);
 hipError_t launch_rope_rows(float* x, int rows, int hd, int rot, const int* pos, int pos0,
                             double theta, hipStream_t s);

@@ -1105,6 +1105,7 @@ hipError_t gemm(const float* X, int64_t ldx, const uint16_t* W, int M, int N, in
 
 // The same on the two-part fp16 path: weight matrix i of layer ly, the row maxima of X
 // (xmax_n partial maxima per row), and for the SwiGLU GEMM the row maxima of its output.
+// tiled: 0 row-major X (three exact bf16 parts), 1 tiled fp32 X, 2 X split by its producer.
 hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const float* xmax, int xmax_n, int M, int N,
                   int K, const float* R, float* Y, int64_t ldy, hipStream_t s, int tiled, float* ymax = nullptr) {
     const uint16_t* W[4] = {ly.w_in, ly.w_out, ly.w_gu, ly.w_down};
@@ -1115,7 +1116,8 @@ hipError_t gemm_h(const float* X, int64_t ldx, const LayerDev& ly, int i, const 
     g.xmax = xmax;
     g.xmax_n = xmax_n;
     g.ymax = ymax;
-    g.x_tiled = tiled;
+    g.x_tiled = tiled != 0;
+    g.x_planes = tiled == 2;
     g.y_tiled = tiled && ymax != nullptr;
     return q35k::launch_gemm(g, s);
 }
@@ -1135,15 +1137,18 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
     float *hb = F + p.hb, *ws = F + p.ws, *lg = F + p.logits;
     float *xn_max = F + p.xn_max, *mix_max = F + p.mix_max, *hb_max = F + p.hb_max;
     const int* ids = reinterpret_cast<const int*>(F + p.ids);
+    // the input norms' rows feed only the in-projection and gate/up GEMMs: on the tiled
+    // path they are written split for them (row widths the one-row-per-wave norm handles)
+    const int xn_form = p.tiled ? (q35k::rmsnorm_rows_splits(H) ? 2 : 1) : 0;
     Launcher Lr{m, s, m->timing_on};
 
     Lr.run(Q35_KT_OTHER, [&] { return q35k::launch_embed_rows(m->embed, ids, hidden, T, H, s); });
     for (int li = 0; li < L; ++li) {
         const LayerDev& ly = m->layers[static_cast<size_t>(li)];
         Lr.run(Q35_KT_OTHER, [&] {
-            return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s, xn_max, p.tiled);
+            return q35k::launch_rmsnorm_rows(hidden, ly.input_ln, xn, T, H, eps, 0, nullptr, s, xn_max, xn_form);
         });
-        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 0, xn_max, 1, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s, p.tiled); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 0, xn_max, 1, T, ly.in_rows, H, nullptr, proj, ly.in_rows, s, xn_form); });
         if (!ly.attn) {
             q35k::GdnPrefillArgs g{};
             g.T = T;
@@ -1202,11 +1207,11 @@ q35_status prefill_block(q35_model* m, const PrefillPlan& p, int pos0, int T, in
             });
         }
         Lr.run(Q35_KT_OTHER, [&] {
-            return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s, xn_max, p.tiled);
+            return q35k::launch_rmsnorm_rows(hidden, ly.post_ln, xn, T, H, eps, 0, nullptr, s, xn_max, xn_form);
         });
         // gate/up projection with silu(gate) * up in its epilogue: hb = T x I, with the row
         // maxima of hb per column tile for the down projection
-        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 2, xn_max, 1, T, 2 * I, H, nullptr, hb, I, s, p.tiled, hb_max); });
+        Lr.run(Q35_KT_GEMM, [&] { return gemm_h(xn, H, ly, 2, xn_max, 1, T, 2 * I, H, nullptr, hb, I, s, xn_form, hb_max); });
         Lr.run(Q35_KT_GEMM, [&] {
             return gemm_h(hb, I, ly, 3, hb_max, q35k::gemm_col_tiles(2 * I), T, H, I, hidden, hidden, H, s, p.tiled);
         });
