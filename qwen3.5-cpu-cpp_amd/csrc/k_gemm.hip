@@ -21,6 +21,9 @@
 //   epilogue multiplies by 2^-(row exponent + w_exp), exactly. Two MFMAs per product instead
 //   of three: 5-8% faster; against float64 the outputs stay within the fp32 accumulation
 //   error (the dropped 2^-22 |x| averages out over K like the accumulator's own roundings).
+//   x_planes: the producer (the prefill's input norm) already wrote each row scaled and split
+//   the same way (xp_off), and the parts are loaded as the operands themselves -- the split
+//   is not repeated for every 128-column tile of the output.
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, each of the 4 waves a 32-row slab
 // of it: 2 x 8 MFMA blocks of 16 x 16 (64 accumulator registers per lane). K advances in
